@@ -1,0 +1,179 @@
+// Gated-DeltaNet single-token decode for gfx950.
+//
+// Math (per batch b, value head hv, key head hk = hv / (Hv/Hk)), following
+// analysis/wave15-attention-architecture/reference/pytorch_reference_gdn.py:38-91
+// and cutile-attn-gdn/main.py:92-185:
+//     u      = k^T (alpha S)                 (d_v)
+//     r      = v - u
+//     S'     = alpha S + beta k r^T          (d_k x d_v, fp32)
+//     o      = S'^T q
+// The output is formed without a second pass over S' through
+//     o = alpha (q^T S) + beta (q.k) r,
+// so both reductions (k^T S and q^T S) come out of the single read of S.
+//
+// Layout and schedule (bandwidth-bound: 2 x d_k x d_v x 4 bytes per head):
+//  * one workgroup per (b, hv); NT = d_k*d_v/64 threads so that every thread
+//    keeps exactly 16 rows x 4 columns (64 fp32) of the state in VGPRs
+//    between the read and the write — S is read once and written once;
+//  * a thread's 4 columns are one 128-bit load/store; TC = d_v/4 threads
+//    cover a full row, so each wave-wide load touches whole 512-byte rows;
+//  * the d_v-wide partial reductions over each thread's 16 rows meet in LDS
+//    (RG = d_k/16 row groups), one barrier, then every thread forms u, r, o
+//    for its own columns and streams its rows of S' back out.
+#include "mx_common.h"
+
+namespace mx {
+namespace gdn {
+
+template <int DK, int DV, typename T>
+__global__ __launch_bounds__(DK * DV / 64) void gdn_decode_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const float* __restrict__ alpha, const float* __restrict__ beta, const float* S_in, float* S_out,
+    uint16_t* __restrict__ o, int Hk, int Hv) {
+  constexpr int NT = DK * DV / 64;
+  constexpr int TC = DV / 4;   // threads across a row
+  constexpr int RG = NT / TC;  // row groups (= DK / 16)
+  constexpr int RPT = DK / RG; // rows per thread (= 16)
+  static_assert(RPT == 16, "16 rows per thread");
+
+  __shared__ float qs[DK], ks[DK];
+  __shared__ __align__(16) float red_u[RG][DV];
+  __shared__ __align__(16) float red_w[RG][DV];
+  __shared__ float red_qk[RG];
+
+  const int bh = blockIdx.x;  // b * Hv + hv
+  const int b = bh / Hv, hv = bh % Hv;
+  const int hk = hv / (Hv / Hk);
+  const int t = threadIdx.x;
+  const int cg = t % TC, rg = t / TC;
+  const int c0 = cg * 4;
+
+  const size_t sbase = (size_t)bh * DK * DV;
+  const float* Sin = S_in + sbase;
+  float* Sout = S_out + sbase;
+
+  // Issue the 16 state loads first: they dominate and need to be in flight.
+  f32x4 s[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + RG * r;
+    s[r] = __builtin_bit_cast(f32x4, ld128_nt(Sin + (size_t)i * DV + c0));
+  }
+
+  const size_t qkbase = ((size_t)b * Hk + hk) * DK;
+  for (int i = t; i < DK; i += NT) {
+    qs[i] = T::to_f32(q[qkbase + i]);
+    ks[i] = T::to_f32(k[qkbase + i]);
+  }
+  const size_t vbase = (size_t)bh * DV + c0;
+  const u32x2 vv = ld64(v + vbase);
+  const float vf[4] = {T::to_f32(vv[0] & 0xffffu), T::to_f32(vv[0] >> 16), T::to_f32(vv[1] & 0xffffu),
+                       T::to_f32(vv[1] >> 16)};
+  const float a = alpha[bh], be = beta[bh];
+  __syncthreads();
+
+  float u[4] = {0.f, 0.f, 0.f, 0.f}, w[4] = {0.f, 0.f, 0.f, 0.f};
+  float qk = 0.f;
+  float kr[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + RG * r;
+    const float ki = ks[i], qi = qs[i];
+    kr[r] = ki;
+    qk = fmaf(qi, ki, qk);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u[c] = fmaf(ki, s[r][c], u[c]);
+      w[c] = fmaf(qi, s[r][c], w[c]);
+    }
+  }
+  *reinterpret_cast<f32x4*>(&red_u[rg][c0]) = f32x4{u[0], u[1], u[2], u[3]};
+  *reinterpret_cast<f32x4*>(&red_w[rg][c0]) = f32x4{w[0], w[1], w[2], w[3]};
+  if (cg == 0) red_qk[rg] = qk;
+  __syncthreads();
+
+  f32x4 ut{0.f, 0.f, 0.f, 0.f}, wt{0.f, 0.f, 0.f, 0.f};
+  float qkt = 0.f;
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    ut += *reinterpret_cast<const f32x4*>(&red_u[g][c0]);
+    wt += *reinterpret_cast<const f32x4*>(&red_w[g][c0]);
+    qkt += red_qk[g];
+  }
+
+  float res[4], of[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    res[c] = vf[c] - a * ut[c];                  // r = v - alpha k^T S
+    of[c] = fmaf(be * qkt, res[c], a * wt[c]);   // o = alpha q^T S + beta (q.k) r
+  }
+
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + RG * r;
+    const float bk = be * kr[r];
+    f32x4 nv;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) nv[c] = fmaf(bk, res[c], a * s[r][c]);
+    st128_nt(Sout + (size_t)i * DV + c0, __builtin_bit_cast(u32x4, nv));
+  }
+  if (rg == 0) {
+    st64(o + vbase, u32x2{T::pack2(of[0], of[1]), T::pack2(of[2], of[3])});
+  }
+}
+
+template <int DK, int DV, typename T>
+static int launch(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
+                  const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, hipStream_t s) {
+  hipLaunchKernelGGL((gdn_decode_kernel<DK, DV, T>), dim3(B * Hv), dim3(DK * DV / 64), 0, s,
+                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, alpha, beta, S_in, S_out,
+                     (uint16_t*)o, Hk, Hv);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+template <typename T>
+static int dispatch(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
+                    const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dk, int dv,
+                    hipStream_t s) {
+#define MX_GDN_CASE(DK_, DV_) \
+  if (dk == DK_ && dv == DV_) return launch<DK_, DV_, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, s);
+  MX_GDN_CASE(64, 64)
+  MX_GDN_CASE(64, 128)
+  MX_GDN_CASE(64, 256)
+  MX_GDN_CASE(128, 64)
+  MX_GDN_CASE(128, 128)
+  MX_GDN_CASE(128, 256)
+  MX_GDN_CASE(256, 64)
+  MX_GDN_CASE(256, 128)
+  MX_GDN_CASE(256, 256)
+#undef MX_GDN_CASE
+  return MX_ERR_UNSUPPORTED;
+}
+
+}  // namespace gdn
+}  // namespace mx
+
+static bool mx_is_dim(int d) { return d == 64 || d == 128 || d == 256; }
+
+extern "C" int mx_gdn_decode(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
+                             const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dk, int dv,
+                             int dtype, void* stream) {
+  if (!q || !k || !v || !alpha || !beta || !S_in || !S_out || !o) return MX_ERR_NULL;
+  if (B <= 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return MX_ERR_SHAPE;
+  if (!mx_is_dim(dk) || !mx_is_dim(dv)) return MX_ERR_SHAPE;
+  if ((long long)B * Hv > 0x7fffffffLL) return MX_ERR_SHAPE;
+  if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
+  if (((uintptr_t)S_in | (uintptr_t)S_out) & 15) return MX_ERR_ALIGN;
+  if (((uintptr_t)v | (uintptr_t)o) & 7) return MX_ERR_ALIGN;
+  // The state may be updated in place; any other overlap would let one
+  // workgroup overwrite rows another has not read yet.
+  const size_t sbytes = (size_t)B * Hv * dk * dv * sizeof(float);
+  const char* si = (const char*)S_in;
+  const char* so = (const char*)S_out;
+  if (si != so && si < so + sbytes && so < si + sbytes) return MX_ERR_ALIAS;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == MX_DTYPE_BF16)
+    return mx::gdn::dispatch<mx::BF16>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dk, dv, s);
+  return mx::gdn::dispatch<mx::F16>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dk, dv, s);
+}

@@ -1,0 +1,293 @@
+// Fused grouped-query attention forward for gfx950 (flash-attention style).
+//
+// Semantics: cutile-attn-gqa/main.py:64-170 (one pass, online softmax in
+// fp32, P cast to the I/O type before the PV product, final 1/l) and the
+// oracle analysis/wave15-attention-architecture/reference/pytorch_reference.py:51-74,
+// plus the causal mask this path adds.
+//
+// MI355X design:
+//  * Scores are computed transposed, S^T = K · Q^T, with 32x32x16 MFMAs.
+//    The query index then runs along lanes (lane l <-> query l%32) and each
+//    lane holds 16 key positions per 32x32 tile, so the row max and row sum
+//    of the softmax are lane-local reductions plus one v_permlane32_swap.
+//  * The probabilities never leave registers: the S^T accumulator of a
+//    query is exactly the B operand (k = key position, col = query) of
+//    O^T = V^T · P^T.  The key order inside the registers is a fixed
+//    permutation, so the V^T operand is fetched in that same order.
+//  * One workgroup = 4 waves = (up to 4 query heads that share a KV head)
+//    x (query sub-blocks of 32 rows).  The K tile [64 x D] and the
+//    transposed V tile [D x 64] are staged once in LDS and used by all four
+//    waves; V is transposed in registers (byte permutes) on its way in.
+//  * K/V tiles are double buffered in LDS; the next tile's global loads are
+//    in flight during the current tile's MFMAs; one barrier per tile.
+//  * Causal: work per query block grows with its index, so workgroups are
+//    launched heaviest-first.  Blocks strictly below the diagonal skip the
+//    mask; kv tiles entirely above a wave's diagonal are skipped.
+#include "mx_common.h"
+
+namespace mx {
+namespace gqa {
+
+constexpr int BN = 64;      // key/value positions per tile
+constexpr int QW = 32;      // queries per wave
+constexpr int NWAVES = 4;
+constexpr int NT = 64 * NWAVES;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// K tile: [BN rows][D] bf16, 16-byte chunks XOR-swizzled by row & 7.
+template <int D>
+__device__ __forceinline__ int k_off(int row, int chunk) {
+  return row * (D * 2) + ((chunk ^ (row & 7)) << 4);
+}
+// V^T tile: [D rows][BN] bf16 (128 B per row), 8-byte chunks swizzled.
+__device__ __forceinline__ int vt_off(int d, int chunk8) {
+  return d * (BN * 2) + ((chunk8 ^ ((d ^ (d >> 3)) & 15)) << 3);
+}
+
+template <int D>
+struct Lds {
+  static constexpr int K_BYTES = BN * D * 2;
+  static constexpr int V_BYTES = D * BN * 2;
+  static constexpr int STAGE = K_BYTES + V_BYTES;
+  static constexpr int TOTAL = 2 * STAGE;
+};
+
+template <int D, typename T, bool CAUSAL>
+__global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
+                                                        const uint16_t* __restrict__ K,
+                                                        const uint16_t* __restrict__ V,
+                                                        uint16_t* __restrict__ O, int B, int Hq, int Hkv,
+                                                        int S, float sl2, int hpw) {
+  constexpr int DC = D / 16;          // 16-deep k steps of QK^T
+  constexpr int DT = D / 32;          // 32-row d tiles of O^T
+  constexpr int K_LD = BN * D / 8 / NT;   // 16-B chunks of K per thread
+  static_assert(K_LD >= 1, "K tile split");
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5;      // lane half
+  const int ql = lane & 31;     // query within the wave
+
+  // ---- workgroup -> (qblock, b, kv head, head group) ----
+  const int G = Hq / Hkv;
+  const int qsb = NWAVES / hpw;            // query sub-blocks per workgroup
+  const int QB = QW * qsb;                 // query rows per workgroup
+  const int hgroups = G / hpw;
+  const int nqb = (S + QB - 1) / QB;
+  const int per_q = B * Hkv * hgroups;
+  const int qb = nqb - 1 - (int)(blockIdx.x / per_q);  // heaviest first
+  int rest = blockIdx.x % per_q;
+  const int hg = rest % hgroups;
+  rest /= hgroups;
+  const int kvh = rest % Hkv;
+  const int b = rest / Hkv;
+
+  const int head = kvh * G + hg * hpw + (wave % hpw);
+  const int q0w = qb * QB + (wave / hpw) * QW;   // this wave's first query
+  const int q0wg = qb * QB;
+
+  const size_t q_head = ((size_t)b * Hq + head) * S;
+  const size_t kv_head = ((size_t)b * Hkv + kvh) * S;
+  const uint16_t* Kh = K + kv_head * D;
+  const uint16_t* Vh = V + kv_head * D;
+
+  // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole loop ----
+  const int qrow = q0w + ql;
+  u32x4 qf[DC];
+#pragma unroll
+  for (int dc = 0; dc < DC; ++dc)
+    qf[dc] = (qrow < S) ? ld128(Q + (q_head + qrow) * D + dc * 16 + g * 8) : u32x4{0, 0, 0, 0};
+
+  // ---- kv range ----
+  const int kv_end_wg = CAUSAL ? min(S, q0wg + QB) : S;
+  const int nblk = (kv_end_wg + BN - 1) / BN;
+  const int kv_end_w = CAUSAL ? min(S, q0w + QW) : S;
+
+  // ---- global -> register staging assignments ----
+  // K: chunk q = tid + i*NT -> row q / (D/8), chunk q % (D/8).
+  // V: 4(kv) x 8(d) block per thread: kvb = tid / (D/8), db = tid % (D/8);
+  //    for D=64 only the first half of the threads carry a V block.
+  constexpr int DB = D / 8;
+  const int v_kvb = tid / DB, v_db = tid % DB;
+  const bool v_active = v_kvb < BN / 4;
+  u32x4 rk[K_LD], rv[4];
+
+  auto load_kv = [&](int kv0) {
+#pragma unroll
+    for (int i = 0; i < K_LD; ++i) {
+      const int q = tid + i * NT;
+      const int row = q / DB, c = q % DB;
+      const int kv = kv0 + row;
+      rk[i] = (kv < S) ? ld128(Kh + (size_t)kv * D + c * 8) : u32x4{0, 0, 0, 0};
+    }
+    if (v_active) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kv = kv0 + v_kvb * 4 + r;
+        rv[r] = (kv < S) ? ld128(Vh + (size_t)kv * D + v_db * 8) : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_kv = [&](int stage) {
+    unsigned char* sk = smem + stage * Lds<D>::STAGE;
+    unsigned char* sv = sk + Lds<D>::K_BYTES;
+#pragma unroll
+    for (int i = 0; i < K_LD; ++i) {
+      const int q = tid + i * NT;
+      *reinterpret_cast<u32x4*>(sk + k_off<D>(q / DB, q % DB)) = rk[i];
+    }
+    if (v_active) {
+      u32x2 cols[8];
+      transpose4x8_b16(rv, cols);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) *reinterpret_cast<u32x2*>(sv + vt_off(v_db * 8 + c, v_kvb)) = cols[c];
+    }
+  };
+
+  f32x16 acc_o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) acc_o[i] = f32x16{};
+  float m_run = -1e30f, l_run = 0.f;
+
+  if (nblk > 0) {
+    load_kv(0);
+    store_kv(0);
+  }
+  __syncthreads();
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int cur = blk & 1;
+    const int kv0 = blk * BN;
+    if (blk + 1 < nblk) load_kv(kv0 + BN);
+
+    if (kv0 < kv_end_w) {
+      const unsigned char* sk = smem + cur * Lds<D>::STAGE;
+      const unsigned char* sv = sk + Lds<D>::K_BYTES;
+
+      // ---- S^T tiles: rows = keys (2 x 32), cols = this wave's 32 queries ----
+      f32x16 s[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        s[t] = f32x16{};
+#pragma unroll
+        for (int dc = 0; dc < DC; ++dc) {
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(sk + k_off<D>(t * 32 + ql, dc * 2 + g));
+          s[t] = mfma32<T>(kf, qf[dc], s[t]);
+        }
+      }
+
+      // ---- scale, mask, online softmax (lane-local + one lane^32 exchange) ----
+      const bool need_mask = (kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0w);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float x = s[t][e] * sl2;
+          if (need_mask) {
+            const int kv = kv0 + t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+            const bool dead = (kv >= S) || (CAUSAL && kv > qrow);
+            x = dead ? -INFINITY : x;
+          }
+          s[t][e] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = max_xor32(mx);
+      const float m_new = fmaxf(m_run, mx);
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      float lsum = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float p = __builtin_amdgcn_exp2f(s[t][e] - m_new);
+          s[t][e] = p;
+          lsum += p;
+        }
+      l_run = l_run * corr + lsum;
+#pragma unroll
+      for (int i = 0; i < DT; ++i) acc_o[i] *= corr;
+
+      // ---- O^T += V^T P^T over 4 key chunks of 16 ----
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int t = c >> 1, i0 = 2 * (c & 1);
+        const u32x4 pf{T::pack2(s[t][4 * i0 + 0], s[t][4 * i0 + 1]), T::pack2(s[t][4 * i0 + 2], s[t][4 * i0 + 3]),
+                       T::pack2(s[t][4 * i0 + 4], s[t][4 * i0 + 5]), T::pack2(s[t][4 * i0 + 6], s[t][4 * i0 + 7])};
+        // key positions carried: 16c + 4g + {0..3} and 16c + 8 + 4g + {0..3}
+        const int ch0 = 4 * c + g, ch1 = 4 * c + 2 + g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int d = dt * 32 + ql;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(sv + vt_off(d, ch0));
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(sv + vt_off(d, ch1));
+          const u32x4 vf{lo[0], lo[1], hi[0], hi[1]};
+          acc_o[dt] = mfma32<T>(vf, pf, acc_o[dt]);
+        }
+      }
+    }
+
+    if (blk + 1 < nblk) store_kv(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and store: lane holds query qrow, d = 32dt + 8i + 4g + j ----
+  const float l_tot = sum_xor32(l_run);
+  const float inv = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
+  if (qrow < S) {
+    uint16_t* orow = O + (q_head + qrow) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = dt * 32 + 8 * i + 4 * g;
+        const f32x16& a = acc_o[dt];
+        st64(orow + d, u32x2{T::pack2(a[4 * i] * inv, a[4 * i + 1] * inv), T::pack2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)});
+      }
+  }
+}
+
+template <int D, typename T, bool CAUSAL>
+static int launch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
+                  hipStream_t stream) {
+  const int G = Hq / Hkv;
+  const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
+  const int QB = QW * (NWAVES / hpw);
+  const long long grid = (long long)((S + QB - 1) / QB) * B * Hkv * (G / hpw);
+  if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
+  auto kern = gqa_fwd_kernel<D, T, CAUSAL>;
+  MX_RETURN_IF_HIP(
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Lds<D>::TOTAL));
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), Lds<D>::TOTAL, stream, (const uint16_t*)Q,
+                     (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, B, Hq, Hkv, S, scale * kLog2e, hpw);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+template <typename T>
+static int dispatch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int D,
+                    float scale, int causal, hipStream_t s) {
+  if (D == 128) return causal ? launch<128, T, true>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
+                              : launch<128, T, false>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+  if (D == 64) return causal ? launch<64, T, true>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
+                             : launch<64, T, false>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+  return MX_ERR_UNSUPPORTED;
+}
+
+}  // namespace gqa
+}  // namespace mx
+
+extern "C" int mx_gqa_fwd(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int D,
+                          float scale, int causal, int dtype, void* stream) {
+  if (!Q || !K || !V || !O) return MX_ERR_NULL;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || Hq % Hkv) return MX_ERR_SHAPE;
+  if (D != 64 && D != 128) return MX_ERR_SHAPE;
+  if (!(scale > 0.f) || !__builtin_isfinite(scale)) return MX_ERR_SHAPE;
+  if ((long long)B * Hq * S * D > (1LL << 40)) return MX_ERR_SHAPE;
+  if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
+  if (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)O) & 15) return MX_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == MX_DTYPE_BF16) return mx::gqa::dispatch<mx::BF16>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, s);
+  return mx::gqa::dispatch<mx::F16>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, s);
+}

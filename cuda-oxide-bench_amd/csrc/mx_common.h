@@ -1,0 +1,211 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of this library.
+//
+// Everything here is written for one target: gfx950, wave64, MFMA matrix
+// cores, 160 KB LDS per CU.  There is no other code path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mx_kernels.h"
+
+namespace mx {
+
+// ---------------------------------------------------------------------------
+// Vector types used as MFMA operands / accumulators and for 128-bit traffic.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Scalar conversions.  bf16 <-> fp32 by bit manipulation with round-to-
+// nearest-even on the narrowing side (the same rounding torch's CPU cast
+// uses), so device outputs are comparable bit-for-bit with a host cast of
+// the same fp32 value.  NaN inputs keep a quiet NaN.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Pack two fp32 into one dword of two bf16 (lo = a, hi = b).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  _Float16 x = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)x;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  _Float16 x = (_Float16)f;  // v_cvt_f16_f32: round-to-nearest-even
+  return (uint32_t)__builtin_bit_cast(uint16_t, x);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+}
+
+// Element-type tags for the 16-bit I/O formats the kernels accept.
+struct BF16 {
+  static __device__ __forceinline__ float to_f32(uint32_t h) { return bf16_bits_to_f32(h); }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
+};
+struct F16 {
+  static __device__ __forceinline__ float to_f32(uint32_t h) { return f16_bits_to_f32(h); }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) { return pack_f16x2(a, b); }
+};
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers.  Operand register images are passed as raw dwords so the
+// same staging code serves bf16 and f16.
+//
+// Lane layouts assumed (CDNA3/CDNA4 MFMA, wave64):
+//   16x16x32 (bf16/f16): A: lane l holds row l%16, k = 8*(l/16) .. +7
+//                        B: lane l holds col l%16, k = 8*(l/16) .. +7
+//                        D: lane l holds col l%16, rows 4*(l/16) .. +3
+//   32x32x16 (bf16/f16): A: lane l holds row l%32, k = 8*(l/32) .. +7
+//                        B: lane l holds col l%32, k = 8*(l/32) .. +7
+//                        D: lane l holds col l%32,
+//                           rows 8*i + 4*(l/32) + j  for acc[4*i + j]
+// A contraction only needs A and B to agree on which k each register
+// position carries, so kernels are free to permute k consistently.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c);
+template <>
+__device__ __forceinline__ f32x4 mfma16<BF16>(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16<F16>(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c);
+template <>
+__device__ __forceinline__ f32x16 mfma32<BF16>(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32<F16>(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// fp8 e4m3 (OCP "fn" encoding on gfx950) x e4m3 -> fp32, 16x16x128.
+// Issued through the block-scaled form with both E8M0 scales = 127 (2^0),
+// i.e. an unscaled product.  A: lane l holds row l%16 and 32 k-bytes,
+// B: lane l holds col l%16 and the same 32 k positions.
+__device__ __forceinline__ f32x4 mfma16_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane reductions inside a wave.
+// ---------------------------------------------------------------------------
+// max(x[l], x[l ^ 32]) for every lane, through v_permlane32_swap.
+__device__ __forceinline__ float max_xor32(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// max(x[l], x[l ^ 16]) within each half-wave, through v_permlane16_swap.
+__device__ __forceinline__ float max_xor16(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// ---------------------------------------------------------------------------
+// 8x8 transpose of 16-bit elements held as 8 rows x 4 dwords.
+// in[r] holds row r (elements 2j, 2j+1 in dword j); out[c] holds column c
+// (rows 2j, 2j+1 in dword j).  Pure VALU byte permutes.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void transpose8x8_b16(const u32x4 in[8], u32x4 out[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {      // dword j of every output = rows 2j, 2j+1
+#pragma unroll
+    for (int c2 = 0; c2 < 4; ++c2) { // input dword c2 holds columns 2c2, 2c2+1
+      uint32_t x = in[2 * j][c2];
+      uint32_t y = in[2 * j + 1][c2];
+      out[2 * c2][j] = __builtin_amdgcn_perm(y, x, 0x05040100u);      // lo halves
+      out[2 * c2 + 1][j] = __builtin_amdgcn_perm(y, x, 0x07060302u);  // hi halves
+    }
+  }
+}
+
+// 4x8 (rows x cols) 16-bit transpose: in[r] (r<4) holds row r as 4 dwords;
+// out[c] (c<8) receives column c as 2 dwords (rows 0,1 | rows 2,3).
+__device__ __forceinline__ void transpose4x8_b16(const u32x4 in[4], u32x2 out[8]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+#pragma unroll
+    for (int c2 = 0; c2 < 4; ++c2) {
+      uint32_t x = in[2 * j][c2];
+      uint32_t y = in[2 * j + 1][c2];
+      out[2 * c2][j] = __builtin_amdgcn_perm(y, x, 0x05040100u);
+      out[2 * c2 + 1][j] = __builtin_amdgcn_perm(y, x, 0x07060302u);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Global memory helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st128(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x2 ld64(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
+__device__ __forceinline__ void st64(void* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+__device__ __forceinline__ u32x4 ld128_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void st128_nt(void* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+// XCD-aware block remap.  The dispatcher places workgroup i on XCD i % 8;
+// renumbering so that consecutive logical tiles share an XCD keeps tiles
+// that reuse the same operands inside one L2.  Valid for any nblocks: the
+// tail that does not fill all 8 XCDs evenly keeps its identity mapping.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  constexpr int kXcd = 8;
+  const int full = (nblocks / kXcd) * kXcd;
+  if (bid >= full) return bid;
+  const int per = full / kXcd;
+  return (bid % kXcd) * per + bid / kXcd;
+}
+
+}  // namespace mx
+
+// Host-side error plumbing shared by the entry points.
+#define MX_RETURN_IF_HIP(expr)                   \
+  do {                                           \
+    hipError_t _e = (expr);                      \
+    if (_e != hipSuccess) return MX_ERR_LAUNCH;  \
+  } while (0)

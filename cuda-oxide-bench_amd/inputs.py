@@ -1,0 +1,112 @@
+"""Seeded synthetic inputs for every kernel (CPU torch.Generator, seed 0xC0FFEE).
+
+Two distributions per kernel:
+  * "baseline": the distributions this path is measured on (uniform[-1,1]
+    GEMM operands, N(0,1) attention inputs, L2-normalised GDN keys with
+    exp(-softplus)/sigmoid gates);
+  * "reference": the reference's own generators, restated —
+    cutile-matmul-tc-bf16/main.py:89-95 (numpy PCG64 U[0,1)),
+    pytorch_reference.py:77-97 (make_qkv), pytorch_reference_mla.py:84-108,
+    pytorch_reference_gdn.py:126-165 (make_inputs).
+The draw order inside each function is fixed; changing it changes every
+fixture.  Tensors are returned on the CPU; callers move them to the GPU.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from .quant import quantize_fp8_blockwise
+from .shapes import FP8GemmShape, GDNShape, GemmShape, GQAShape, MLADecodeShape
+
+SEED = 0xC0FFEE
+SAMPLE_SEED = 0xBEEF
+
+
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator(device="cpu").manual_seed(seed)
+
+
+def gemm_inputs(s: GemmShape, seed: int = SEED, dist: str = "baseline") -> tuple[torch.Tensor, torch.Tensor]:
+    """A[M,K], B[K,N] bf16 (round-to-nearest-even from fp32)."""
+    if dist == "reference":
+        rng = np.random.default_rng(seed)
+        a = torch.from_numpy(rng.random((s.m, s.k), dtype=np.float32))
+        b = torch.from_numpy(rng.random((s.k, s.n), dtype=np.float32))
+    else:
+        g = _gen(seed)
+        a = torch.rand((s.m, s.k), generator=g, dtype=torch.float32) * 2.0 - 1.0
+        b = torch.rand((s.k, s.n), generator=g, dtype=torch.float32) * 2.0 - 1.0
+    return a.to(torch.bfloat16), b.to(torch.bfloat16)
+
+
+def fp8_gemm_inputs(s: FP8GemmShape, seed: int = SEED):
+    """A, B ~ N(0,1) quantised to e4m3 with 1x128 (A) / 128x128 (B) fp32 scales.
+
+    Returns (a_fp8, sa, b_fp8, sb).
+    """
+    g = _gen(seed)
+    a = torch.randn((s.m, s.k), generator=g, dtype=torch.float32)
+    b = torch.randn((s.k, s.n), generator=g, dtype=torch.float32)
+    a8, sa = quantize_fp8_blockwise(a, (1, 128))
+    b8, sb = quantize_fp8_blockwise(b, (128, 128))
+    return a8, sa, b8, sb
+
+
+def gqa_inputs(s: GQAShape, dtype: torch.dtype = torch.bfloat16, seed: int = SEED, dist: str = "baseline"):
+    """q [B,Hq,S,D], k, v [B,Hkv,S,D]."""
+    g = _gen(seed)
+    qs = (s.batch, s.n_q, s.seq, s.d_head)
+    ks = (s.batch, s.n_kv, s.seq, s.d_head)
+    if dist == "reference":
+        sc = 1.0 / math.sqrt(s.d_head)
+        q = torch.randn(qs, generator=g, dtype=torch.float32) * sc
+        k = torch.randn(ks, generator=g, dtype=torch.float32) * sc
+        v = torch.randn(ks, generator=g, dtype=torch.float32)
+    else:
+        q = torch.randn(qs, generator=g, dtype=torch.float32)
+        k = torch.randn(ks, generator=g, dtype=torch.float32)
+        v = torch.randn(ks, generator=g, dtype=torch.float32)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def mla_inputs(s: MLADecodeShape, seed: int = SEED):
+    """q [B,H,d_latent+d_rope], kv [B,T,d_latent+d_rope], both ~N(0,1) bf16."""
+    g = _gen(seed)
+    q = torch.randn((s.batch, s.n_h, s.d_qk), generator=g, dtype=torch.float32)
+    kv = torch.randn((s.batch, s.ctx, s.d_qk), generator=g, dtype=torch.float32)
+    return q.to(torch.bfloat16), kv.to(torch.bfloat16)
+
+
+def gdn_inputs(s: GDNShape, dtype: torch.dtype = torch.bfloat16, seed: int = SEED, dist: str = "baseline"):
+    """Returns dict q, k [B,Hk,dk]; v [B,Hv,dv]; alpha, beta [B,Hv] fp32; S_in fp32."""
+    g = _gen(seed)
+    B, Hv, Hk, dk, dv = s.batch, s.n_heads, s.hk, s.d_k, s.d_v
+    if dist == "reference":
+        sc = 1.0 / math.sqrt(dk)
+        q = torch.randn((B, Hk, dk), generator=g, dtype=torch.float32) * sc
+        k = torch.randn((B, Hk, dk), generator=g, dtype=torch.float32) * sc
+        v = torch.randn((B, Hv, dv), generator=g, dtype=torch.float32)
+        alpha = 0.85 + 0.13 * torch.rand((B, Hv), generator=g, dtype=torch.float32)
+        beta = -0.5 + torch.rand((B, Hv), generator=g, dtype=torch.float32)
+        S = torch.randn((B, Hv, dk, dv), generator=g, dtype=torch.float32) * 0.1
+        # The reference stores its gates as f16; keep the f16-rounded values.
+        alpha = alpha.to(torch.float16).float()
+        beta = beta.to(torch.float16).float()
+    else:
+        q = torch.randn((B, Hk, dk), generator=g, dtype=torch.float32)
+        k = torch.randn((B, Hk, dk), generator=g, dtype=torch.float32)
+        q = q / q.norm(dim=-1, keepdim=True)
+        k = k / k.norm(dim=-1, keepdim=True)
+        v = torch.randn((B, Hv, dv), generator=g, dtype=torch.float32)
+        S = torch.randn((B, Hv, dk, dv), generator=g, dtype=torch.float32) * 0.02
+        xa = torch.randn((B, Hv), generator=g, dtype=torch.float32)
+        xb = torch.randn((B, Hv), generator=g, dtype=torch.float32)
+        alpha = torch.exp(-torch.nn.functional.softplus(xa))
+        beta = torch.sigmoid(xb)
+    return {
+        "q": q.to(dtype), "k": k.to(dtype), "v": v.to(dtype),
+        "alpha": alpha.contiguous(), "beta": beta.contiguous(), "S_in": S.contiguous(),
+    }

@@ -1,0 +1,200 @@
+"""Tensor-level operators over the gfx950 kernel library.
+
+Each operator validates dtype, device, contiguity and shape, allocates any
+output the caller did not pass, and launches the HIP kernel on the current
+torch stream through the C-ABI (``_lib``).  Launches are asynchronous, like
+the reference harnesses' ``ct.launch`` (e.g. cutile-attn-gqa/main.py:249-252):
+the caller synchronises.  There is no CPU path: inputs must be on a HIP
+device and the native library must be present.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_IO_DTYPES = {torch.bfloat16: _lib.MX_DTYPE_BF16, torch.float16: _lib.MX_DTYPE_F16}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require(t: torch.Tensor, name: str, dtypes, ndim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name} has dtype {t.dtype}, expected one of {list(dtypes)}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a HIP device (got {t.device})")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D (got shape {tuple(t.shape)})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _same_device(*ts: torch.Tensor) -> None:
+    devs = {t.device for t in ts}
+    if len(devs) != 1:
+        raise ValueError(f"all tensors must be on one device (got {sorted(map(str, devs))})")
+
+
+def gemm_bf16(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A @ B for row-major bf16 A[M,K], B[K,N]; fp32 accumulate, bf16 C.
+
+    Semantics of cutile-matmul-tc-bf16/main.py:59-78.
+    """
+    _require(a, "a", (torch.bfloat16,), 2)
+    _require(b, "b", (torch.bfloat16,), 2)
+    M, K = a.shape
+    K2, N = b.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: a {tuple(a.shape)} vs b {tuple(b.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    _require(out, "out", (torch.bfloat16,), 2)
+    if tuple(out.shape) != (M, N):
+        raise ValueError(f"out must be {(M, N)}, got {tuple(out.shape)}")
+    _same_device(a, b, out)
+    _lib.call("mx_gemm_bf16", a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, K, N, N, _stream())
+    return out
+
+
+def gemm_fp8_bs(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Block-scaled e4m3 GEMM, bf16 out.
+
+    a[M,K], b[K,N]: torch.float8_e4m3fn; sa[M, K/128], sb[K/128, ceil(N/128)]:
+    fp32 dequantisation scales.  C[m,n] = sum_kb sa[m,kb] sb[kb,n//128] *
+    (A[m,kb-block] . B[kb-block,n]).
+    """
+    f8 = (torch.float8_e4m3fn,)
+    _require(a, "a", f8, 2)
+    _require(b, "b", f8, 2)
+    _require(sa, "sa", (torch.float32,), 2)
+    _require(sb, "sb", (torch.float32,), 2)
+    M, K = a.shape
+    K2, N = b.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: a {tuple(a.shape)} vs b {tuple(b.shape)}")
+    if K % 128:
+        raise ValueError(f"K={K} must be a multiple of 128 (scale block depth)")
+    if tuple(sa.shape) != (M, K // 128):
+        raise ValueError(f"sa must be {(M, K // 128)}, got {tuple(sa.shape)}")
+    if tuple(sb.shape) != (K // 128, (N + 127) // 128):
+        raise ValueError(f"sb must be {(K // 128, (N + 127) // 128)}, got {tuple(sb.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    _require(out, "out", (torch.bfloat16,), 2)
+    if tuple(out.shape) != (M, N):
+        raise ValueError(f"out must be {(M, N)}, got {tuple(out.shape)}")
+    _same_device(a, sa, b, sb, out)
+    _lib.call("mx_gemm_fp8_bs", a.data_ptr(), sa.data_ptr(), b.data_ptr(), sb.data_ptr(), out.data_ptr(),
+              M, N, K, _stream())
+    return out
+
+
+def gqa_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
+            scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused GQA forward.  q [B,Hq,S,D]; k, v [B,Hkv,S,D]; bf16 or f16.
+
+    Semantics of cutile-attn-gqa/main.py:64-170 (scale defaults to 1/sqrt(D)
+    as in :85) with an optional causal mask.
+    """
+    _require(q, "q", _IO_DTYPES, 4)
+    _require(k, "k", (q.dtype,), 4)
+    _require(v, "v", (q.dtype,), 4)
+    B, Hq, S, D = q.shape
+    Bk, Hkv, Sk, Dk = k.shape
+    if (Bk, Sk, Dk) != (B, S, D) or tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if Hq % Hkv:
+        raise ValueError(f"n_q ({Hq}) must be divisible by n_kv ({Hkv})")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty_like(q)
+    _require(out, "out", (q.dtype,), 4)
+    if out.shape != q.shape:
+        raise ValueError(f"out must be {tuple(q.shape)}")
+    _same_device(q, k, v, out)
+    _lib.call("mx_gqa_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
+              float(scale), int(bool(causal)), _IO_DTYPES[q.dtype], _stream())
+    return out
+
+
+def mla_decode_workspace_bytes(B: int, H: int, T: int, d_latent: int = 512) -> int:
+    return int(_lib.load().mx_mla_decode_workspace(B, H, T, d_latent))
+
+
+def mla_decode(q: torch.Tensor, kv: torch.Tensor, scale: float, d_latent: int = 512,
+               out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Absorbed MLA decode.  q [B,H,576], kv [B,T,576] bf16 -> out [B,H,512].
+
+    out[b,h] = softmax(scale * q[b,h] . kv[b]^T) . kv[b][:, :d_latent].
+    """
+    _require(q, "q", (torch.bfloat16,), 3)
+    _require(kv, "kv", (torch.bfloat16,), 3)
+    B, H, Dq = q.shape
+    Bk, T, Dk = kv.shape
+    if Bk != B or Dk != Dq:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)} kv {tuple(kv.shape)}")
+    d_rope = Dq - d_latent
+    if out is None:
+        out = torch.empty((B, H, d_latent), dtype=torch.bfloat16, device=q.device)
+    _require(out, "out", (torch.bfloat16,), 3)
+    if tuple(out.shape) != (B, H, d_latent):
+        raise ValueError(f"out must be {(B, H, d_latent)}")
+    need = mla_decode_workspace_bytes(B, H, T, d_latent)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
+    ws_bytes = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
+    _same_device(q, kv, out)
+    _lib.call("mx_mla_decode", q.data_ptr(), kv.data_ptr(), out.data_ptr(), B, H, T, d_latent, d_rope,
+              float(scale), ws_ptr, ws_bytes, _stream())
+    return out
+
+
+def gdn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, beta: torch.Tensor,
+               S_in: torch.Tensor, S_out: torch.Tensor | None = None,
+               o: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Gated-DeltaNet decode step.  Returns (o, S_out).
+
+    q, k [B,Hk,dk]; v [B,Hv,dv] (bf16 or f16); alpha, beta [B,Hv] fp32;
+    S_in [B,Hv,dk,dv] fp32.  S_out may be S_in for an in-place update.
+    Semantics of cutile-attn-gdn/main.py:92-185 with Hk != Hv grouping.
+    """
+    _require(q, "q", _IO_DTYPES, 3)
+    _require(k, "k", (q.dtype,), 3)
+    _require(v, "v", (q.dtype,), 3)
+    _require(alpha, "alpha", (torch.float32,), 2)
+    _require(beta, "beta", (torch.float32,), 2)
+    _require(S_in, "S_in", (torch.float32,), 4)
+    B, Hk, dk = q.shape
+    Bv, Hv, dv = v.shape
+    if tuple(k.shape) != (B, Hk, dk) or Bv != B:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if Hv % Hk:
+        raise ValueError(f"n_v_heads ({Hv}) must be a multiple of n_k_heads ({Hk})")
+    if tuple(alpha.shape) != (B, Hv) or tuple(beta.shape) != (B, Hv):
+        raise ValueError(f"alpha/beta must be {(B, Hv)}")
+    if tuple(S_in.shape) != (B, Hv, dk, dv):
+        raise ValueError(f"S_in must be {(B, Hv, dk, dv)}, got {tuple(S_in.shape)}")
+    if S_out is None:
+        S_out = torch.empty_like(S_in)
+    _require(S_out, "S_out", (torch.float32,), 4)
+    if S_out.shape != S_in.shape:
+        raise ValueError("S_out must match S_in")
+    if o is None:
+        o = torch.empty((B, Hv, dv), dtype=q.dtype, device=q.device)
+    _require(o, "o", (q.dtype,), 3)
+    if tuple(o.shape) != (B, Hv, dv):
+        raise ValueError(f"o must be {(B, Hv, dv)}")
+    _same_device(q, k, v, alpha, beta, S_in, S_out, o)
+    _lib.call("mx_gdn_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), alpha.data_ptr(), beta.data_ptr(),
+              S_in.data_ptr(), S_out.data_ptr(), o.data_ptr(), B, Hk, Hv, dk, dv, _IO_DTYPES[q.dtype],
+              _stream())
+    return o, S_out

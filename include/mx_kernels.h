@@ -1,0 +1,133 @@
+/*
+ * mx_kernels.h — C-ABI of the MI355X (gfx950) quant-inference kernel path.
+ *
+ * One shared library (libmxkernels.so) exports these entry points.  Every
+ * pointer argument is a device pointer the caller allocated (for instance a
+ * torch tensor's data_ptr()); every call is asynchronous on the HIP stream
+ * passed as `stream` (NULL = the legacy default stream) and returns an int
+ * status: MX_OK (0) or a negative MX_ERR_* code.  No entry point exits,
+ * aborts, synchronises the device or allocates device memory.  Arguments
+ * are validated before anything is launched, so an error return means
+ * nothing was enqueued.  The library holds no state: calls are re-entrant
+ * and may be issued from several host threads on different streams.
+ *
+ * The reference (baladithyab/cuda-oxide-bench) launches each of these
+ * operations from a Python harness through `ct.launch(stream.ptr, grid,
+ * kernel, (arrays...))` on caller-allocated, row-major, contiguous device
+ * arrays; the citation on each declaration names the launch it replaces.
+ */
+#ifndef MX_KERNELS_H
+#define MX_KERNELS_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define MX_OK 0
+#define MX_ERR_NULL (-1)        /* a required pointer is NULL                    */
+#define MX_ERR_SHAPE (-2)       /* a size is <= 0, inconsistent or too large     */
+#define MX_ERR_ALIGN (-3)       /* pointer / leading dimension not 16-B aligned  */
+#define MX_ERR_DTYPE (-4)       /* unsupported element-type code                 */
+#define MX_ERR_WORKSPACE (-5)   /* workspace missing or smaller than required    */
+#define MX_ERR_ALIAS (-6)       /* an output overlaps an input it may not alias  */
+#define MX_ERR_LAUNCH (-7)      /* the HIP runtime rejected the kernel launch    */
+#define MX_ERR_UNSUPPORTED (-8) /* valid request this build has no kernel for    */
+
+/* ---- element-type codes for the 16-bit I/O tensors --------------------- */
+#define MX_DTYPE_BF16 0
+#define MX_DTYPE_F16 1
+
+/* Human-readable name of a status code (static storage, never NULL). */
+const char* mx_strerror(int code);
+
+/* Library version string, e.g. "mxkernels 0.1.0 gfx950". */
+const char* mx_version(void);
+
+/*
+ * bf16 GEMM:  C[M,N] = A[M,K] · B[K,N]
+ * A, B, C row-major bf16 with leading dimensions lda >= K, ldb >= N,
+ * ldc >= N (in elements).  fp32 accumulation, C rounded to bf16 (RNE).
+ * Requires K % 8 == 0, N % 8 == 0, lda/ldb/ldc % 8 == 0 and 16-byte aligned
+ * pointers; M, N, K otherwise arbitrary (ragged edges are zero-padded).
+ * Replaces: cutile-matmul-tc-bf16/main.py:117-118 (ct.launch of the
+ * `matmul_bf16` kernel defined at :59-78) and the bf16 row of
+ * cutile-matmul-tiled-mixed/main.py:121-130.
+ */
+int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb,
+                 int ldc, void* stream);
+
+/*
+ * fp8 block-scaled GEMM:
+ *   C[m,n] = sum_kb sA[m,kb] * sB[kb,n/128] * sum_{k in block kb} A[m,k] * B[k,n]
+ * A[M,K], B[K,N] row-major OCP e4m3 ("e4m3fn", torch.float8_e4m3fn) bytes;
+ * sA[M, K/128] and sB[K/128, ceil(N/128)] row-major fp32 dequantisation
+ * scales (1x128 blocks of A, 128x128 blocks of B); C[M,N] row-major bf16.
+ * fp32 accumulation with the scale applied once per 128-deep K block.
+ * Requires K % 128 == 0, N % 16 == 0, 16-byte aligned A, B, C.
+ * Replaces: mojo-matmul-fp8/matmul_fp8.mojo:48-218 (matmul_fp8_kernel,
+ * e4m3 x e4m3 -> f32, launched at :285-289), extended with the block
+ * scaling and bf16 output this path specifies.
+ */
+int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, const float* sB, void* C, int M,
+                   int N, int K, void* stream);
+
+/*
+ * Fused grouped-query attention forward (flash-attention style, one pass):
+ *   O[b,h,s,:] = softmax_t( scale * Q[b,h,s,:]·K[b,h/G,t,:] + mask ) · V[b,h/G,t,:]
+ * with G = Hq / Hkv and mask = -inf for t > s when causal != 0.
+ * Q, O: [B, Hq, S, D]; K, V: [B, Hkv, S, D]; contiguous, dtype as given
+ * (MX_DTYPE_BF16 or MX_DTYPE_F16).  fp32 scores, online softmax and
+ * accumulation; O rounded to the I/O dtype.  D must be 64 or 128,
+ * Hq % Hkv == 0; S arbitrary (>= 1).
+ * Replaces: cutile-attn-gqa/main.py:249-252 (ct.launch of `gqa_fwd`,
+ * kernel at :64-170, non-causal f16) — the causal flag and bf16 are the
+ * extensions this path specifies.
+ */
+int mx_gqa_fwd(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S,
+               int D, float scale, int causal, int dtype, void* stream);
+
+/*
+ * MLA absorbed decode (one query token per sequence, latent KV cache):
+ *   O[b,h,:] = softmax_t( scale * Q[b,h,:]·KV[b,t,:] ) · KV[b,t,0:d_latent]
+ * Q[B,H,d_latent+d_rope], KV[B,T,d_latent+d_rope], O[B,H,d_latent], all
+ * contiguous bf16.  d_latent = 512 and d_rope = 64 are supported (the
+ * DeepSeek-V3 latent width 576).  The kernel splits T across workgroups
+ * and merges the partial softmax states; the caller passes a device
+ * workspace of at least mx_mla_decode_workspace(B, H, T, d_latent) bytes.
+ * Replaces: cutile-attn-mla/main.py:250-253 (ct.launch of `mla_fwd`,
+ * kernel at :81-163).  The reference kernel attends over pre-projected
+ * per-head K/V; this entry point is the weight-absorbed latent form of the
+ * same softmax attention (analysis/wave15-attention-research/MECHANISMS.md:91-94).
+ */
+int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int H, int T, int d_latent,
+                  int d_rope, float scale, void* workspace, size_t ws_bytes, void* stream);
+
+/* Bytes of device workspace mx_mla_decode needs for this problem (0 on
+ * invalid sizes). */
+size_t mx_mla_decode_workspace(int B, int H, int T, int d_latent);
+
+/*
+ * Gated-DeltaNet single-token recurrent decode, per (b, value head hv),
+ * with key head hk = hv / (Hv / Hk):
+ *   u     = alpha * (k^T S)                  (d_v)
+ *   S_out = alpha * S + beta * k (v - u)^T   (d_k x d_v, fp32)
+ *   o     = S_out^T q                        (d_v)
+ * q, k: [B, Hk, dk]; v, o: [B, Hv, dv] (dtype as given); alpha, beta:
+ * [B, Hv] fp32; S_in, S_out: [B, Hv, dk, dv] fp32 with dv contiguous.
+ * S_out may equal S_in (in-place update); partial overlap is rejected.
+ * dk and dv must be 64, 128 or 256; Hv % Hk == 0.
+ * Replaces: cutile-attn-gdn/main.py:268-272 (ct.launch of `gdn_decode`,
+ * kernel at :92-185), extended with Hk != Hv grouping.
+ */
+int mx_gdn_decode(const void* q, const void* k, const void* v, const float* alpha,
+                  const float* beta, const float* S_in, float* S_out, void* o, int B, int Hk,
+                  int Hv, int dk, int dv, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MX_KERNELS_H */

@@ -1,0 +1,48 @@
+"""MLA absorbed-decode oracle (test infrastructure only).
+
+The reference's MLA oracle (analysis/wave15-attention-architecture/reference/
+pytorch_reference_mla.py:66-81, mla_naive) is softmax attention with an
+explicit scale 1/sqrt(qk_head_dim).  In weight-absorbed decode
+(analysis/wave15-attention-research/MECHANISMS.md:91-94, 115-120) every
+head attends over the same latent cache: K := KV[b] (576 = 512 latent +
+64 rope), V := KV[b][:, :512], one query token per sequence.  This is
+mla_naive with n_kv = 1, computed in fp32 per sequence.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def mla_decode_ref(q: torch.Tensor, kv: torch.Tensor, scale: float, d_latent: int = 512,
+                   batches: list[int] | None = None) -> torch.Tensor:
+    """q [B,H,Dqk], kv [B,T,Dqk] -> fp32 [B,H,d_latent]."""
+    q = q.detach().cpu().float()
+    kv = kv.detach().cpu().float()
+    B, H, _ = q.shape
+    out = torch.zeros((B, H, d_latent), dtype=torch.float32)
+    for b in (batches if batches is not None else range(B)):
+        scores = (q[b] @ kv[b].transpose(0, 1)) * scale     # [H, T]
+        probs = torch.softmax(scores, dim=-1)
+        out[b] = probs @ kv[b][:, :d_latent]                 # [H, 512]
+    return out
+
+
+def mla_partial(q: torch.Tensor, kv: torch.Tensor, scale: float, d_latent: int = 512):
+    """Unnormalised partial softmax state over a token slice:
+    (m [B,H], l [B,H], o [B,H,d_latent]) with o = sum_t exp(s_t - m) v_t."""
+    q = q.detach().cpu().float()
+    kv = kv.detach().cpu().float()
+    s = torch.einsum("bhd,btd->bht", q, kv) * scale
+    m = s.amax(dim=-1)
+    p = torch.exp(s - m[..., None])
+    return m, p.sum(-1), torch.einsum("bht,btd->bhd", p, kv[..., :d_latent])
+
+
+def mla_merge(parts) -> torch.Tensor:
+    """Log-sum-exp merge of partial states (the split-KV combine rule)."""
+    ms = torch.stack([p[0] for p in parts])
+    M = ms.amax(0)
+    ws = torch.exp(ms - M)
+    l = sum(w * p[1] for w, p in zip(ws, parts))
+    o = sum(w[..., None] * p[2] for w, p in zip(ws, parts))
+    return o / l[..., None]

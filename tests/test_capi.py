@@ -1,0 +1,99 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry
+point include/mx_kernels.h declares, and rejects invalid arguments before
+launching anything (these calls never reach the HIP runtime)."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from conftest import REPO_ROOT, import_submodule
+
+_lib = import_submodule("_lib")
+HEADER = REPO_ROOT / "include" / "mx_kernels.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ("mx_gemm_bf16", "mx_gemm_fp8_bs", "mx_gqa_fwd", "mx_mla_decode", "mx_mla_decode_workspace",
+              "mx_gdn_decode", "mx_strerror", "mx_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for n in declared_functions():
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.lib_path())], capture_output=True, text=True)
+    if out.returncode == 0:
+        exported = set(re.findall(r" T (mx_[a-z0-9_]+)", out.stdout))
+        assert set(declared_functions()) <= exported
+
+
+def test_strerror_and_version():
+    lib = _lib.load()
+    assert lib.mx_version().decode().startswith("mxkernels")
+    for code in range(0, -9, -1):
+        assert lib.mx_strerror(code)
+    assert _lib.strerror(_lib.MX_ERR_ALIAS) == "output overlaps an input"
+
+
+P = ctypes.c_void_p(0x10000)  # never dereferenced: every call below fails validation
+
+
+@pytest.mark.parametrize("args,code", [
+    ((None, P, P, 64, 64, 64, 64, 64, 64, None), _lib.MX_ERR_NULL),
+    ((P, P, P, 0, 64, 64, 64, 64, 64, None), _lib.MX_ERR_SHAPE),
+    ((P, P, P, 64, 64, 60, 60, 64, 64, None), _lib.MX_ERR_ALIGN),
+    ((P, P, P, 64, 64, 64, 32, 64, 64, None), _lib.MX_ERR_SHAPE),
+    ((ctypes.c_void_p(0x10008), P, P, 64, 64, 64, 64, 64, 64, None), _lib.MX_ERR_ALIGN),
+])
+def test_gemm_bf16_validation(args, code):
+    assert _lib.load().mx_gemm_bf16(*args) == code
+
+
+def test_gemm_fp8_validation():
+    f = _lib.load().mx_gemm_fp8_bs
+    assert f(P, P, P, P, None, 64, 64, 128, None) == _lib.MX_ERR_NULL
+    assert f(P, P, P, P, P, 64, 64, 100, None) == _lib.MX_ERR_SHAPE
+    assert f(P, P, P, P, P, 64, 40, 128, None) == _lib.MX_ERR_ALIGN
+
+
+def test_gqa_validation():
+    f = _lib.load().mx_gqa_fwd
+    assert f(None, P, P, P, 1, 4, 2, 16, 64, 0.125, 1, 0, None) == _lib.MX_ERR_NULL
+    assert f(P, P, P, P, 1, 4, 3, 16, 64, 0.125, 1, 0, None) == _lib.MX_ERR_SHAPE   # Hq % Hkv
+    assert f(P, P, P, P, 1, 4, 2, 16, 96, 0.125, 1, 0, None) == _lib.MX_ERR_SHAPE   # D
+    assert f(P, P, P, P, 1, 4, 2, 16, 64, 0.125, 1, 7, None) == _lib.MX_ERR_DTYPE
+    assert f(P, P, P, P, 1, 4, 2, 16, 64, -1.0, 1, 0, None) == _lib.MX_ERR_SHAPE
+
+
+def test_mla_validation_and_workspace():
+    lib = _lib.load()
+    assert lib.mx_mla_decode_workspace(32, 128, 4096, 512) > 0
+    assert lib.mx_mla_decode_workspace(32, 128, 4096, 256) == 0
+    assert lib.mx_mla_decode_workspace(1, 16, 64, 512) == 0  # short context: no split
+    f = lib.mx_mla_decode
+    assert f(P, P, P, 32, 128, 4096, 512, 64, 0.07, None, 0, None) == _lib.MX_ERR_WORKSPACE
+    assert f(P, P, P, 1, 16, 64, 256, 64, 0.07, None, 0, None) == _lib.MX_ERR_UNSUPPORTED
+    assert f(None, P, P, 1, 16, 64, 512, 64, 0.07, None, 0, None) == _lib.MX_ERR_NULL
+
+
+def test_gdn_validation():
+    f = _lib.load().mx_gdn_decode
+    args = [P] * 8
+    assert f(None, *args[1:], 2, 2, 4, 64, 64, 0, None) == _lib.MX_ERR_NULL
+    assert f(*args, 2, 3, 4, 64, 64, 0, None) == _lib.MX_ERR_SHAPE     # Hv % Hk
+    assert f(*args, 2, 2, 4, 96, 64, 0, None) == _lib.MX_ERR_SHAPE     # dk
+    assert f(*args, 2, 2, 4, 64, 64, 3, None) == _lib.MX_ERR_DTYPE
+    s_in, s_out = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x100000 + 256)
+    assert f(P, P, P, P, P, s_in, s_out, P, 2, 2, 4, 64, 64, 0, None) == _lib.MX_ERR_ALIAS

@@ -1,0 +1,109 @@
+"""bf16 GEMM parity on the GPU: HIP kernel vs the CPU oracle (fp32 matmul of
+the bf16 operands, cutile-matmul-tc-bf16/main.py:98-107).  Bound: normwise
+max|got-ref|/max|ref| <= 2e-2 (bf16 output), plus the reference harness's
+own sampled gate |err| <= 0.2 + 0.05|ref| (:129-135) and exact KATs."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, from_bits, import_submodule, load_golden
+from oracle import gemm as ogemm
+from oracle.metrics import normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+shapes = import_submodule("shapes")
+inputs = import_submodule("inputs")
+
+
+def run(ops, a, b):
+    c = ops.gemm_bf16(a.cuda(), b.cuda())
+    torch.cuda.synchronize()
+    return c.cpu()
+
+
+def test_golden_fixture(ops):
+    announce("gemm_bf16 golden 72x136x96")
+    g = load_golden("gemm_bf16_72x136x96")
+    a, b = from_bits(g["a"], torch.bfloat16), from_bits(g["b"], torch.bfloat16)
+    c = run(ops, a, b)
+    assert normwise_rel_err(c, g["c"]) <= 1e-2
+
+
+@pytest.mark.parametrize("mnk", [(1, 8, 8), (16, 16, 32), (100, 136, 72), (257, 264, 520), (512, 512, 512),
+                                 (1024, 1024, 1024), (2048, 1024, 512), (4096, 8192, 256)])
+def test_parity_vs_oracle(ops, mnk):
+    m, n, k = mnk
+    announce(f"gemm_bf16 {m}x{n}x{k}")
+    a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
+    c = run(ops, a, b)
+    ref = ogemm.gemm_ref(a, b)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    # bf16 output: every element within a few bf16 ulps of the fp32 result
+    assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+
+
+def test_reference_distribution_sampled_gate(ops):
+    """The reference harness's own check at its smoke size: U[0,1) inputs,
+    200 sampled cells, |err| <= 0.2 + 0.05|ref| (cutile-matmul-tc-bf16/main.py:110-135)."""
+    announce("gemm_bf16 reference-dist 512 sampled")
+    s = shapes.GEMM_SMOKE
+    a, b = inputs.gemm_inputs(s, dist="reference")
+    c = run(ops, a, b).float().numpy()
+    rng = np.random.default_rng(inputs.SAMPLE_SEED)
+    rows = rng.integers(0, s.m, size=200)
+    cols = rng.integers(0, s.n, size=200)
+    refs = ogemm.sample_reference(a, b, rows, cols)
+    got = c[rows, cols]
+    assert np.all(np.abs(got - refs) <= 0.2 + 0.05 * np.abs(refs))
+
+
+@pytest.mark.parametrize("k", [64, 1024])
+def test_kat_constant(ops, k):
+    """A=1, B=1 -> K; A=2, B=3 -> 6K (oxide-gemm-sol/bench/cublas_correctness_test.py:8-11)."""
+    announce(f"gemm_bf16 KAT constant K={k}")
+    m = n = 256
+    for av, bv, want in ((1.0, 1.0, k), (2.0, 3.0, 6 * k)):
+        a = torch.full((m, k), av, dtype=torch.bfloat16)
+        b = torch.full((k, n), bv, dtype=torch.bfloat16)
+        c = run(ops, a, b)
+        assert torch.all(c.float() == want)
+
+
+def test_kat_pattern(ops):
+    """A[i,:]=(i%8+1), B[:,j]=(j%8+1) -> (i%8+1)(j%8+1)K, exactly representable."""
+    announce("gemm_bf16 KAT pattern")
+    m, n, k = 384, 264, 128
+    a = (torch.arange(m) % 8 + 1).float()[:, None].expand(m, k).to(torch.bfloat16).contiguous()
+    b = (torch.arange(n) % 8 + 1).float()[None, :].expand(k, n).to(torch.bfloat16).contiguous()
+    c = run(ops, a, b).float()
+    want = ((torch.arange(m) % 8 + 1)[:, None] * (torch.arange(n) % 8 + 1)[None, :] * k).float()
+    assert torch.equal(c, want)
+
+
+def test_target_size_sampled(ops):
+    """8192^3 (the roofline target): 256 cells against fp64 dot products."""
+    announce("gemm_bf16 8192^3 sampled")
+    s = shapes.GEMM_TARGET
+    a, b = inputs.gemm_inputs(s)
+    c = ops.gemm_bf16(a.cuda(), b.cuda())
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(inputs.SAMPLE_SEED)
+    rows = rng.integers(0, s.m, size=256)
+    cols = rng.integers(0, s.n, size=256)
+    got = c[torch.from_numpy(rows).cuda(), torch.from_numpy(cols).cuda()].float().cpu().numpy()
+    a32, b32 = a.float().numpy(), b.float().numpy()
+    ref = np.array([ogemm.ref_elem(a32, b32, r, cc) for r, cc in zip(rows, cols)])
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref).max() / scale <= TOL
+
+
+def test_rejects_bad_arguments(ops):
+    a = torch.zeros((64, 60), dtype=torch.bfloat16, device="cuda")  # K % 8 != 0
+    b = torch.zeros((60, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(Exception):
+        ops.gemm_bf16(a, b)
