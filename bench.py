@@ -1,0 +1,299 @@
+"""Benchmark of the quant-inference kernel path on one MI355X.
+
+Headline (the `value` of the JSON line): the fused causal GQA forward at
+BASELINE configs[1] — B=1, Hq=32, Hkv=8, S=4096, D=128, bf16, N(0,1)
+inputs, scale 1/sqrt(128) — reported in algorithmic TFLOP/s (causal work
+2*B*Hq*D*S*(S+1)).  A "step" is one forward pass over that batch with
+inputs already resident in HBM.  The other four kernels (bf16 GEMM at
+1024^3 and 8192^3, fp8 block-scaled GEMM at 8192^3, MLA absorbed decode,
+GDN decode) are measured the same way and reported under "others".
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       [--only-headline]
+Prints exactly one JSON line on stdout (progress goes to stderr).
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO_ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO_ROOT))
+
+METRIC = "TFLOPS & %MFMA peak (GEMM, GQA fwd); GB/s & %HBM peak (MLA/GDN decode)"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(fn, steps: int, warmup: int):
+    """Run fn warmup times, then time exactly `steps` calls with a HIP event
+    pair around each launch on the current stream.  Returns (per-launch ms
+    list, wall ms per step over the bracketed region)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return per, wall_ms
+
+
+def summarize(per: list[float]) -> dict:
+    srt = sorted(per)
+    return {"mean_ms": sum(per) / len(per), "median_ms": srt[len(srt) // 2], "best_ms": srt[0]}
+
+
+def cpu_info() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def bench_gqa(pkg, ops, steps, warmup, cpu_baseline: bool):
+    import torch
+
+    S, F = pkg.shapes, pkg.flops
+    shape = S.GQA_BASELINE
+    q, k, v = pkg.inputs.gqa_inputs(shape)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out = torch.empty_like(qd)
+    fn = lambda: ops.gqa_fwd(qd, kd, vd, causal=True, out=out)  # noqa: E731
+    per, wall_ms = time_launches(fn, steps, warmup)
+    st = summarize(per)
+    flops = F.gqa_causal_flops(shape)
+    res = {
+        "shape": shape,
+        "per": per,
+        "wall_ms": wall_ms,
+        "stats": st,
+        "flops": flops,
+        "tflops_mean": F.tflops(flops, st["mean_ms"]),
+        "tflops_best": F.tflops(flops, st["best_ms"]),
+        "tflops_ref_convention_best": F.tflops(F.gqa_attention_flops(shape), st["best_ms"]),
+    }
+    if cpu_baseline:
+        res["cpu"] = cpu_baseline_gqa(shape, q, k, v, out)
+    return res
+
+
+def cpu_baseline_gqa(shape, q, k, v, out_gpu) -> dict:
+    """The oracle (CPU restatement of gqa_naive + causal mask) on a bounded
+    sample of the same workload: whole query heads at S=4096, in a fixed
+    order, until ~15 s of CPU work or all heads are done.  Also compares the
+    GPU output on those heads (a parity spot check on the bench inputs)."""
+    import torch
+
+    from oracle import gqa as ogqa
+    from oracle.metrics import normwise_rel_err
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    threads = torch.get_num_threads()
+    budget_s = float(os.environ.get("MX_CPU_BASELINE_SECONDS", "15"))
+    order = [(7 * i) % shape.n_q for i in range(shape.n_q)]  # 7 is coprime to n_q = 32
+    heads, elapsed = [], 0.0
+    ogqa.gqa_naive(q, k, v, causal=True, heads=[order[0]])  # warm-up (allocator, threads)
+    ref = None
+    for h in order:
+        t0 = time.perf_counter()
+        r = ogqa.gqa_naive(q, k, v, causal=True, heads=[h])
+        elapsed += time.perf_counter() - t0
+        ref = r if ref is None else ref + r
+        heads.append(h)
+        if elapsed >= budget_s:
+            break
+    per_head_flops = 2 * shape.batch * shape.d_head * shape.seq * (shape.seq + 1)
+    tfl = per_head_flops * len(heads) / elapsed / 1e12
+    got = out_gpu.cpu()
+    err = normwise_rel_err(got[:, heads], ref[:, heads])
+    return {
+        "value": tfl,
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(heads)} of {shape.n_q} query heads (causal, S={shape.seq}, D={shape.d_head}), "
+                  f"fp32 torch CPU oracle, {elapsed:.1f} s, {threads} threads on {os.cpu_count()} logical CPUs "
+                  f"({cpu_info()})",
+        "parity_normwise_on_sample": err,
+    }
+
+
+def bench_others(pkg, ops, steps, warmup) -> dict:
+    import torch
+
+    S, F, I = pkg.shapes, pkg.flops, pkg.inputs
+    res = {}
+
+    for shape in (S.GEMM_PARITY, S.GEMM_TARGET):
+        a, b = I.gemm_inputs(shape)
+        ad, bd = a.cuda(), b.cuda()
+        c = torch.empty((shape.m, shape.n), dtype=torch.bfloat16, device="cuda")
+        per, _ = time_launches(lambda: ops.gemm_bf16(ad, bd, out=c), steps, warmup)
+        st = summarize(per)
+        fl = F.gemm_flops(shape)
+        res[f"gemm_bf16_{shape.m}"] = {
+            "unit": "TFLOPS", "mean_ms": st["mean_ms"], "best_ms": st["best_ms"],
+            "tflops_mean": F.tflops(fl, st["mean_ms"]), "tflops_best": F.tflops(fl, st["best_ms"]),
+            "frac_mfma_peak_mean": F.tflops(fl, st["mean_ms"]) / F.PEAK_BF16_TFLOPS,
+        }
+        del ad, bd, c
+        log(f"gemm_bf16 {shape.m}^3: {res[f'gemm_bf16_{shape.m}']['tflops_mean']:.1f} TFLOPS mean")
+
+    shape = S.FP8_TARGET
+    a8, sa, b8, sb = I.fp8_gemm_inputs(shape)
+    a8d, sad, b8d, sbd = a8.cuda(), sa.cuda(), b8.cuda(), sb.cuda()
+    c = torch.empty((shape.m, shape.n), dtype=torch.bfloat16, device="cuda")
+    per, _ = time_launches(lambda: ops.gemm_fp8_bs(a8d, sad, b8d, sbd, out=c), steps, warmup)
+    st = summarize(per)
+    fl = F.gemm_flops(shape)
+    res["gemm_fp8_bs_8192"] = {
+        "unit": "TFLOPS", "mean_ms": st["mean_ms"], "best_ms": st["best_ms"],
+        "tflops_mean": F.tflops(fl, st["mean_ms"]), "tflops_best": F.tflops(fl, st["best_ms"]),
+        "frac_mfma_peak_mean": F.tflops(fl, st["mean_ms"]) / F.PEAK_FP8_TFLOPS,
+    }
+    del a8d, sad, b8d, sbd, c
+    log(f"gemm_fp8_bs 8192^3: {res['gemm_fp8_bs_8192']['tflops_mean']:.1f} TFLOPS mean")
+
+    shape = S.MLA_BASELINE
+    q, kv = I.mla_inputs(shape)
+    qd, kvd = q.cuda(), kv.cuda()
+    o = torch.empty((shape.batch, shape.n_h, shape.d_latent), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(max(1, ops.mla_decode_workspace_bytes(shape.batch, shape.n_h, shape.ctx)),
+                     dtype=torch.uint8, device="cuda")
+    per, _ = time_launches(lambda: ops.mla_decode(qd, kvd, shape.scale, out=o, workspace=ws), steps, warmup)
+    st = summarize(per)
+    nb, fl = F.mla_decode_bytes(shape), F.mla_decode_flops(shape)
+    res["mla_decode"] = {
+        "unit": "GB/s", "mean_us": st["mean_ms"] * 1e3, "best_us": st["best_ms"] * 1e3,
+        "gbps_mean": F.gbps(nb, st["mean_ms"]), "gbps_best": F.gbps(nb, st["best_ms"]),
+        "frac_hbm_peak_mean": F.gbps(nb, st["mean_ms"]) / F.PEAK_HBM_GBPS,
+        "tflops_mean": F.tflops(fl, st["mean_ms"]),
+    }
+    del qd, kvd, o, ws
+    log(f"mla_decode: {res['mla_decode']['gbps_mean']:.0f} GB/s mean")
+
+    shape = S.GDN_BASELINE
+    x = {n: t.cuda() for n, t in I.gdn_inputs(shape).items()}
+    so = torch.empty_like(x["S_in"])
+    od = torch.empty((shape.batch, shape.n_heads, shape.d_v), dtype=torch.bfloat16, device="cuda")
+    per, _ = time_launches(lambda: ops.gdn_decode(x["q"], x["k"], x["v"], x["alpha"], x["beta"], x["S_in"],
+                                                  S_out=so, o=od), steps, warmup)
+    st = summarize(per)
+    nb = F.gdn_decode_bytes(shape)
+    res["gdn_decode"] = {
+        "unit": "GB/s", "mean_us": st["mean_ms"] * 1e3, "best_us": st["best_ms"] * 1e3,
+        "gbps_mean": F.gbps(nb, st["mean_ms"]), "gbps_best": F.gbps(nb, st["best_ms"]),
+        "frac_hbm_peak_mean": F.gbps(nb, st["mean_ms"]) / F.PEAK_HBM_GBPS,
+    }
+    log(f"gdn_decode: {res['gdn_decode']['gbps_mean']:.0f} GB/s mean")
+    return res
+
+
+def load_traffic(workload: str):
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated), if it covers this workload."""
+    p = REPO_ROOT / "profiles" / "gqa_fwd_causal_s4096_traffic.json"
+    try:
+        d = json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+    if d.get("workload") != workload:
+        return None
+    return d.get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-headline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every kernel is single-device; sharding is described in DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+
+    pkg = importlib.import_module("cuda-oxide-bench_amd")
+    ops = pkg.load_ops()
+    F = pkg.flops
+    log(f"device: {torch.cuda.get_device_name(0)}")
+
+    g = bench_gqa(pkg, ops, args.steps, args.warmup, cpu_baseline=not args.no_cpu_baseline)
+    shape = g["shape"]
+    log(f"gqa_fwd causal S{shape.seq}: mean {g['stats']['mean_ms']:.4f} ms  {g['tflops_mean']:.1f} TFLOPS")
+    others = {} if args.only_headline else bench_others(pkg, ops, args.steps, args.warmup)
+
+    workload = (f"gqa_fwd causal B{shape.batch} Hq{shape.n_q} Hkv{shape.n_kv} S{shape.seq} "
+                f"D{shape.d_head} bf16")
+    achieved = g["tflops_mean"]
+    traffic = load_traffic(workload)
+    line = {
+        "metric": METRIC,
+        "value": round(F.tflops(g["flops"], g["wall_ms"]), 3),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V, seed 0xC0FFEE)",
+        "config": {
+            "workload": workload,
+            "batch": shape.batch, "seq": shape.seq, "n_q": shape.n_q, "n_kv": shape.n_kv,
+            "d_head": shape.d_head, "causal": True, "softmax_scale": shape.d_head ** -0.5,
+            "flops_per_step": g["flops"], "flops_convention": "causal algorithmic 2*B*Hq*D*S*(S+1)",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": F.PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / F.PEAK_BF16_TFLOPS, 5),
+            "traffic": traffic,
+            "kernel": "gqa_fwd_kernel<128, BF16, causal>",
+            "launch_mean_ms": round(g["stats"]["mean_ms"], 5),
+            "launch_best_ms": round(g["stats"]["best_ms"], 5),
+        },
+        "cpu_baseline": g.get("cpu"),
+        "tflops_reference_convention_best": round(g["tflops_ref_convention_best"], 3),
+        "others": others,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
