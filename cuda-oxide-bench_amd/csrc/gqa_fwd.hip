@@ -33,24 +33,48 @@ constexpr int QW = 32;      // queries per wave
 constexpr int NWAVES = 4;
 constexpr int NT = 64 * NWAVES;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 
-// K tile: [BN rows][D] bf16, 16-byte chunks XOR-swizzled by row & 7.
-template <int D>
-__device__ __forceinline__ int k_off(int row, int chunk) {
-  return row * (D * 2) + ((chunk ^ (row & 7)) << 4);
-}
-// V^T tile: [D rows][BN] bf16 (128 B per row), 8-byte chunks swizzled.
-__device__ __forceinline__ int vt_off(int d, int chunk8) {
-  return d * (BN * 2) + ((chunk8 ^ ((d ^ (d >> 3)) & 15)) << 3);
-}
-
+// LDS tiles are row-major copies of the K and V tiles ([BN keys][D]) with
+// padded rows: K rows carry 16 extra bytes, V rows 32, so that the 16-lane
+// phases of every fragment read touch distinct 16-byte bank groups and each
+// read of a lane is its base address plus a compile-time immediate.
 template <int D>
 struct Lds {
-  static constexpr int K_BYTES = BN * D * 2;
-  static constexpr int V_BYTES = D * BN * 2;
+  static constexpr int K_ROW = D * 2 + 16;
+  static constexpr int V_ROW = D * 2 + 32;
+  static constexpr int K_BYTES = BN * K_ROW;
+  static constexpr int V_BYTES = BN * V_ROW;
   static constexpr int STAGE = K_BYTES + V_BYTES;
   static constexpr int TOTAL = 2 * STAGE;
 };
+
+// ds_read_b64_tr_b16 (gfx950 transposing LDS read).  Within each group of
+// 16 lanes, lane 4a+b receives element b of the 8-byte rows addressed by
+// lanes a, 4+a, 8+a, 12+a (in that order).  Pointing lane 4j+a at
+// V[key_j][d0 + 4a] therefore hands lane 4a+b the column d0+4a+b for keys
+// key_0..key_3: a k-contiguous MFMA operand read straight from row-major V.
+__device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(__attribute__((address_space(3))) const unsigned char*)p);
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// Running-sum helper: acc + x.lo + x.hi for a dword of two bf16 / f16.
+template <typename T>
+__device__ __forceinline__ float dot2_ones(uint32_t x, float acc);
+template <>
+__device__ __forceinline__ float dot2_ones<BF16>(uint32_t x, float acc) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, x), bf2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2_ones<F16>(uint32_t x, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x), h2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+}
 
 template <int D, typename T, bool CAUSAL>
 __global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
@@ -95,36 +119,40 @@ __global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restri
   const int qrow = q0w + ql;
   u32x4 qf[DC];
 #pragma unroll
-  for (int dc = 0; dc < DC; ++dc)
-    qf[dc] = (qrow < S) ? ld128(Q + (q_head + qrow) * D + dc * 16 + g * 8) : u32x4{0, 0, 0, 0};
+  for (int dc = 0; dc < DC; ++dc) {
+    const u32x4 x = ld128(Q + (q_head + min(qrow, S - 1)) * D + dc * 16 + g * 8);
+    qf[dc] = (qrow < S) ? x : u32x4{0, 0, 0, 0};
+  }
 
   // ---- kv range ----
   const int kv_end_wg = CAUSAL ? min(S, q0wg + QB) : S;
   const int nblk = (kv_end_wg + BN - 1) / BN;
   const int kv_end_w = CAUSAL ? min(S, q0w + QW) : S;
 
-  // ---- global -> register staging assignments ----
-  // K: chunk q = tid + i*NT -> row q / (D/8), chunk q % (D/8).
-  // V: 4(kv) x 8(d) block per thread: kvb = tid / (D/8), db = tid % (D/8);
-  //    for D=64 only the first half of the threads carry a V block.
+  // ---- global -> register staging: K and V tiles row-major, 16-byte
+  // chunks, chunk q = tid + i*NT -> row q / (D/8), chunk q % (D/8) ----
   constexpr int DB = D / 8;
-  const int v_kvb = tid / DB, v_db = tid % DB;
-  const bool v_active = v_kvb < BN / 4;
-  u32x4 rk[K_LD], rv[4];
+  u32x4 rk[K_LD], rv[K_LD];
 
   auto load_kv = [&](int kv0) {
+    if (kv0 + BN <= S) {  // uniform: every tile but a ragged last one
 #pragma unroll
-    for (int i = 0; i < K_LD; ++i) {
-      const int q = tid + i * NT;
-      const int row = q / DB, c = q % DB;
-      const int kv = kv0 + row;
-      rk[i] = (kv < S) ? ld128(Kh + (size_t)kv * D + c * 8) : u32x4{0, 0, 0, 0};
-    }
-    if (v_active) {
+      for (int i = 0; i < K_LD; ++i) {
+        const int q = tid + i * NT;
+        const size_t off = (size_t)(kv0 + q / DB) * D + (q % DB) * 8;
+        rk[i] = ld128(Kh + off);
+        rv[i] = ld128(Vh + off);
+      }
+    } else {
+      // rows past S are read from row S-1 (in bounds) and zeroed
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int kv = kv0 + v_kvb * 4 + r;
-        rv[r] = (kv < S) ? ld128(Vh + (size_t)kv * D + v_db * 8) : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < K_LD; ++i) {
+        const int q = tid + i * NT;
+        const int kv = kv0 + q / DB;
+        const size_t off = (size_t)min(kv, S - 1) * D + (q % DB) * 8;
+        const u32x4 xk = ld128(Kh + off), xv = ld128(Vh + off);
+        rk[i] = (kv < S) ? xk : u32x4{0, 0, 0, 0};
+        rv[i] = (kv < S) ? xv : u32x4{0, 0, 0, 0};
       }
     }
   };
@@ -134,15 +162,15 @@ __global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restri
 #pragma unroll
     for (int i = 0; i < K_LD; ++i) {
       const int q = tid + i * NT;
-      *reinterpret_cast<u32x4*>(sk + k_off<D>(q / DB, q % DB)) = rk[i];
-    }
-    if (v_active) {
-      u32x2 cols[8];
-      transpose4x8_b16(rv, cols);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) *reinterpret_cast<u32x2*>(sv + vt_off(v_db * 8 + c, v_kvb)) = cols[c];
+      *reinterpret_cast<u32x4*>(sk + (q / DB) * Lds<D>::K_ROW + (q % DB) * 16) = rk[i];
+      *reinterpret_cast<u32x4*>(sv + (q / DB) * Lds<D>::V_ROW + (q % DB) * 16) = rv[i];
     }
   };
+
+  // Transposed V fragment addressing: lane (half g, sub-group sg, 4j+a)
+  // reads key 16c + 8r + 4g + j at column 32dt + 16sg + 4a.
+  const int v_sg = (lane >> 4) & 1, v_j = (lane >> 2) & 3, v_a = lane & 3;
+  const int v_lane_off = (4 * g + v_j) * Lds<D>::V_ROW + (16 * v_sg + 4 * v_a) * 2;
 
   f32x16 acc_o[DT];
 #pragma unroll
@@ -171,61 +199,69 @@ __global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restri
         s[t] = f32x16{};
 #pragma unroll
         for (int dc = 0; dc < DC; ++dc) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(sk + k_off<D>(t * 32 + ql, dc * 2 + g));
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(sk + (t * 32 + ql) * Lds<D>::K_ROW + (dc * 2 + g) * 16);
           s[t] = mfma32<T>(kf, qf[dc], s[t]);
         }
       }
 
-      // ---- scale, mask, online softmax (lane-local + one lane^32 exchange) ----
+      // ---- mask, online softmax (lane-local + one lane^32 exchange) ----
+      // The running max m_run is kept in log2 units (scores * sl2).  It is
+      // only raised when some lane's block max exceeds it by more than
+      // 2^kLazy: below that, p = 2^(s*sl2 - m_run) stays <= 2^kLazy and the
+      // O/l rescale (64 multiplies per lane) is skipped.  The decision is a
+      // wave-wide vote, so the branch is uniform.
       const bool need_mask = (kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0w);
-      float mx = -INFINITY;
+      if (need_mask) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kv = kv0 + t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+            const bool dead = (kv >= S) || (CAUSAL && kv > qrow);
+            s[t][e] = dead ? -INFINITY : s[t][e];
+          }
+      }
+      float mx = s[0][0];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float x = s[t][e] * sl2;
-          if (need_mask) {
-            const int kv = kv0 + t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-            const bool dead = (kv >= S) || (CAUSAL && kv > qrow);
-            x = dead ? -INFINITY : x;
-          }
-          s[t][e] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = max_xor32(mx);
-      const float m_new = fmaxf(m_run, mx);
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
+      mx = max_xor32(mx) * sl2;
+      if (__any(mx > m_run + kLazy)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= corr;
+#pragma unroll
+        for (int i = 0; i < DT; ++i) acc_o[i] *= corr;
+      }
       float lsum = 0.f;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = __builtin_amdgcn_exp2f(s[t][e] - m_new);
-          s[t][e] = p;
-          lsum += p;
-        }
-      l_run = l_run * corr + lsum;
-#pragma unroll
-      for (int i = 0; i < DT; ++i) acc_o[i] *= corr;
+        for (int e = 0; e < 16; ++e) s[t][e] = __builtin_amdgcn_exp2f(fmaf(s[t][e], sl2, -m_run));
 
       // ---- O^T += V^T P^T over 4 key chunks of 16 ----
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int t = c >> 1, i0 = 2 * (c & 1);
+        // P^T operand: keys 16c + 4g + {0..3} then 16c + 8 + 4g + {0..3}
         const u32x4 pf{T::pack2(s[t][4 * i0 + 0], s[t][4 * i0 + 1]), T::pack2(s[t][4 * i0 + 2], s[t][4 * i0 + 3]),
                        T::pack2(s[t][4 * i0 + 4], s[t][4 * i0 + 5]), T::pack2(s[t][4 * i0 + 6], s[t][4 * i0 + 7])};
-        // key positions carried: 16c + 4g + {0..3} and 16c + 8 + 4g + {0..3}
-        const int ch0 = 4 * c + g, ch1 = 4 * c + 2 + g;
+        // the row sum uses the rounded P the MFMA consumes
+        lsum = dot2_ones<T>(pf[0], lsum);
+        lsum = dot2_ones<T>(pf[1], lsum);
+        lsum = dot2_ones<T>(pf[2], lsum);
+        lsum = dot2_ones<T>(pf[3], lsum);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const int d = dt * 32 + ql;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(sv + vt_off(d, ch0));
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(sv + vt_off(d, ch1));
-          const u32x4 vf{lo[0], lo[1], hi[0], hi[1]};
-          acc_o[dt] = mfma32<T>(vf, pf, acc_o[dt]);
+          const unsigned char* vb = sv + v_lane_off + (16 * c) * Lds<D>::V_ROW + dt * 64;
+          const u32x2 lo = lds_read_tr16(vb);
+          const u32x2 hi = lds_read_tr16(vb + 8 * Lds<D>::V_ROW);
+          acc_o[dt] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, acc_o[dt]);
         }
       }
+      l_run += lsum;
     }
 
     if (blk + 1 < nblk) store_kv(cur ^ 1);

@@ -25,25 +25,23 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kWave = 64;
 
 // ---------------------------------------------------------------------------
-// Scalar conversions.  bf16 <-> fp32 by bit manipulation with round-to-
-// nearest-even on the narrowing side (the same rounding torch's CPU cast
-// uses), so device outputs are comparable bit-for-bit with a host cast of
-// the same fp32 value.  NaN inputs keep a quiet NaN.
+// Conversions.  Narrowing to bf16 / f16 uses gfx950's packed converts
+// (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32: two fp32 -> two 16-bit values in
+// one instruction, round-to-nearest-even), the same rounding torch's CPU
+// cast applies, so device outputs are comparable bit-for-bit with a host
+// cast of the same fp32 value.
 // ---------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
-}
-
 // Pack two fp32 into one dword of two bf16 (lo = a, hi = b).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -51,13 +49,8 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return (float)x;
 }
 
-__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
-  _Float16 x = (_Float16)f;  // v_cvt_f16_f32: round-to-nearest-even
-  return (uint32_t)__builtin_bit_cast(uint16_t, x);
-}
-
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
-  return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
 }
 
 // Element-type tags for the 16-bit I/O formats the kernels accept.
