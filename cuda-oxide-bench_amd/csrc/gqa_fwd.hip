@@ -7,42 +7,55 @@
 //
 // MI355X design:
 //  * Scores are computed transposed, S^T = K · Q^T, with 32x32x16 MFMAs.
-//    The query index then runs along lanes (lane l <-> query l%32) and each
-//    lane holds 16 key positions per 32x32 tile, so the row max and row sum
-//    of the softmax are lane-local reductions plus one v_permlane32_swap.
+//    The query index then runs along lanes (lane l <-> query l%32 of a
+//    32-query tile) and each lane holds 16 key positions per 32x32 tile, so
+//    the softmax row max / row sum are lane-local plus one v_permlane32_swap.
 //  * The probabilities never leave registers: the S^T accumulator of a
-//    query is exactly the B operand (k = key position, col = query) of
+//    query tile is exactly the B operand (k = key, col = query) of
 //    O^T = V^T · P^T.  The key order inside the registers is a fixed
-//    permutation, so the V^T operand is fetched in that same order.
-//  * One workgroup = 4 waves = (up to 4 query heads that share a KV head)
-//    x (query sub-blocks of 32 rows).  The K tile [64 x D] and the
-//    transposed V tile [D x 64] are staged once in LDS and used by all four
-//    waves; V is transposed in registers (byte permutes) on its way in.
-//  * K/V tiles are double buffered in LDS; the next tile's global loads are
-//    in flight during the current tile's MFMAs; one barrier per tile.
-//  * Causal: work per query block grows with its index, so workgroups are
-//    launched heaviest-first.  Blocks strictly below the diagonal skip the
-//    mask; kv tiles entirely above a wave's diagonal are skipped.
+//    permutation; V^T fragments are fetched in that order with gfx950's
+//    transposing LDS read (ds_read_b64_tr_b16) from a row-major V tile, so
+//    V is never transposed in registers.
+//  * A wave owns QT tiles of 32 queries of one head; every K and V fragment
+//    read from LDS feeds QT MFMAs, which is what bounds LDS traffic per FLOP.
+//  * One workgroup = 4 waves = (up to 4 query heads sharing a KV head) x
+//    (query sub-blocks).  K and V tiles of 64 keys are staged once in LDS
+//    (double buffered, next tile's global loads in flight during the
+//    current tile's MFMAs, one barrier per tile) and shared by the 4 waves.
+//  * Softmax: the running max only moves when a lane's block max exceeds it
+//    by more than 2^8 (lazy rescale, wave-uniform vote), the scale is folded
+//    into the exp2 argument (one FMA + one exp2 per score), and the row sum
+//    is accumulated with v_dot2 on the rounded P the PV MFMA consumes.
+//  * Causal: workgroups launch heaviest-first; only diagonal / ragged tiles
+//    are masked; tiles entirely above a wave's diagonal are skipped.
 #include "mx_common.h"
+
+// Query tiles (of 32) per wave.  1 keeps two waves per SIMD (the pair hides
+// each other's softmax / LDS latency); 2 halves LDS reads per FLOP but needs
+// about 512 registers and currently spills, so it is not the default.
+#ifndef MX_GQA_QT
+#define MX_GQA_QT 1
+#endif
 
 namespace mx {
 namespace gqa {
 
 constexpr int BN = 64;      // key/value positions per tile
-constexpr int QW = 32;      // queries per wave
 constexpr int NWAVES = 4;
 constexpr int NT = 64 * NWAVES;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 
 // LDS tiles are row-major copies of the K and V tiles ([BN keys][D]) with
-// padded rows: K rows carry 16 extra bytes, V rows 32, so that the 16-lane
-// phases of every fragment read touch distinct 16-byte bank groups and each
-// read of a lane is its base address plus a compile-time immediate.
+// padded rows, so every fragment read of a lane is its base address plus a
+// compile-time immediate and no read phase repeats a bank: K rows carry 16
+// extra bytes (16-lane phases of 16-byte reads hit 16 distinct bank groups),
+// V rows 64 (the 32-lane phases of the 8-byte transposing reads, 4 rows x 2
+// column groups x 4 lanes, hit 32 distinct 8-byte slots).
 template <int D>
 struct Lds {
   static constexpr int K_ROW = D * 2 + 16;
-  static constexpr int V_ROW = D * 2 + 32;
+  static constexpr int V_ROW = D * 2 + 64;
   static constexpr int K_BYTES = BN * K_ROW;
   static constexpr int V_BYTES = BN * V_ROW;
   static constexpr int STAGE = K_BYTES + V_BYTES;
@@ -76,21 +89,22 @@ __device__ __forceinline__ float dot2_ones<F16>(uint32_t x, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x), h2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
 }
 
-template <int D, typename T, bool CAUSAL>
-__global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
-                                                        const uint16_t* __restrict__ K,
-                                                        const uint16_t* __restrict__ V,
-                                                        uint16_t* __restrict__ O, int B, int Hq, int Hkv,
-                                                        int S, float sl2, int hpw) {
+template <int D, typename T, bool CAUSAL, int QT>
+__global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
+                                                                     const uint16_t* __restrict__ K,
+                                                                     const uint16_t* __restrict__ V,
+                                                                     uint16_t* __restrict__ O, int B, int Hq,
+                                                                     int Hkv, int S, float sl2, int hpw) {
+  constexpr int QW = 32 * QT;         // queries per wave
   constexpr int DC = D / 16;          // 16-deep k steps of QK^T
   constexpr int DT = D / 32;          // 32-row d tiles of O^T
-  constexpr int K_LD = BN * D / 8 / NT;   // 16-B chunks of K per thread
+  constexpr int K_LD = BN * D / 8 / NT;   // 16-B chunks of K (and of V) per thread
   static_assert(K_LD >= 1, "K tile split");
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5;      // lane half
-  const int ql = lane & 31;     // query within the wave
+  const int ql = lane & 31;     // query within a 32-query tile
 
   // ---- workgroup -> (qblock, b, kv head, head group) ----
   const int G = Hq / Hkv;
@@ -116,12 +130,16 @@ __global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restri
   const uint16_t* Vh = V + kv_head * D;
 
   // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole loop ----
-  const int qrow = q0w + ql;
-  u32x4 qf[DC];
+  int qrow[QT];
+  u32x4 qf[QT][DC];
 #pragma unroll
-  for (int dc = 0; dc < DC; ++dc) {
-    const u32x4 x = ld128(Q + (q_head + min(qrow, S - 1)) * D + dc * 16 + g * 8);
-    qf[dc] = (qrow < S) ? x : u32x4{0, 0, 0, 0};
+  for (int qt = 0; qt < QT; ++qt) {
+    qrow[qt] = q0w + 32 * qt + ql;
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) {
+      const u32x4 x = ld128(Q + (q_head + min(qrow[qt], S - 1)) * D + dc * 16 + g * 8);
+      qf[qt][dc] = (qrow[qt] < S) ? x : u32x4{0, 0, 0, 0};
+    }
   }
 
   // ---- kv range ----
@@ -172,10 +190,15 @@ __global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restri
   const int v_sg = (lane >> 4) & 1, v_j = (lane >> 2) & 3, v_a = lane & 3;
   const int v_lane_off = (4 * g + v_j) * Lds<D>::V_ROW + (16 * v_sg + 4 * v_a) * 2;
 
-  f32x16 acc_o[DT];
+  f32x16 acc_o[QT][DT];
+  float m_run[QT], l_run[QT];
 #pragma unroll
-  for (int i = 0; i < DT; ++i) acc_o[i] = f32x16{};
-  float m_run = -1e30f, l_run = 0.f;
+  for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int i = 0; i < DT; ++i) acc_o[qt][i] = f32x16{};
+    m_run[qt] = -1e30f;
+    l_run[qt] = 0.f;
+  }
 
   if (nblk > 0) {
     load_kv(0);
@@ -192,76 +215,115 @@ __global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restri
       const unsigned char* sk = smem + cur * Lds<D>::STAGE;
       const unsigned char* sv = sk + Lds<D>::K_BYTES;
 
-      // ---- S^T tiles: rows = keys (2 x 32), cols = this wave's 32 queries ----
-      f32x16 s[2];
+      // ---- S^T tiles: rows = keys (2 x 32), cols = queries (QT x 32) ----
+      // 2*QT independent accumulator chains; each K fragment feeds QT
+      // MFMAs and is read KLA k-steps ahead of its use.
+      auto kread = [&](int t, int dc) {
+        return *reinterpret_cast<const u32x4*>(sk + (t * 32 + ql) * Lds<D>::K_ROW + (dc * 2 + g) * 16);
+      };
+      f32x16 s[QT][2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        s[t] = f32x16{};
+      for (int qt = 0; qt < QT; ++qt) s[qt][0] = s[qt][1] = f32x16{};
+      constexpr int KLA = (QT == 1) ? 2 : 1;  // read lookahead (k-steps)
+      u32x4 kb[KLA + 1][2];
 #pragma unroll
-        for (int dc = 0; dc < DC; ++dc) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(sk + (t * 32 + ql) * Lds<D>::K_ROW + (dc * 2 + g) * 16);
-          s[t] = mfma32<T>(kf, qf[dc], s[t]);
-        }
+      for (int i = 0; i < KLA; ++i) {
+        kb[i][0] = kread(0, i);
+        kb[i][1] = kread(1, i);
       }
-
-      // ---- mask, online softmax (lane-local + one lane^32 exchange) ----
-      // The running max m_run is kept in log2 units (scores * sl2).  It is
-      // only raised when some lane's block max exceeds it by more than
-      // 2^kLazy: below that, p = 2^(s*sl2 - m_run) stays <= 2^kLazy and the
-      // O/l rescale (64 multiplies per lane) is skipped.  The decision is a
-      // wave-wide vote, so the branch is uniform.
-      const bool need_mask = (kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0w);
-      if (need_mask) {
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        if (dc + KLA < DC) {
+          kb[(dc + KLA) % (KLA + 1)][0] = kread(0, dc + KLA);
+          kb[(dc + KLA) % (KLA + 1)][1] = kread(1, dc + KLA);
+        }
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int kv = kv0 + t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-            const bool dead = (kv >= S) || (CAUSAL && kv > qrow);
-            s[t][e] = dead ? -INFINITY : s[t][e];
-          }
+          for (int qt = 0; qt < QT; ++qt) s[qt][t] = mfma32<T>(kb[dc % (KLA + 1)][t], qf[qt][dc], s[qt][t]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the read lookahead
       }
-      float mx = s[0][0];
+
+      // V fragments of the first key chunk do not depend on the softmax:
+      // issue them now so their latency hides under the VALU work below.
+      auto vread = [&](int c, int dt) {
+        const unsigned char* vb = sv + v_lane_off + (16 * c) * Lds<D>::V_ROW + dt * 64;
+        const u32x2 lo = lds_read_tr16(vb);
+        const u32x2 hi = lds_read_tr16(vb + 8 * Lds<D>::V_ROW);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4 vb[2][DT];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int dt = 0; dt < DT; ++dt) vb[0][dt] = vread(0, dt);
+
+      // ---- mask, online softmax (lane-local + one lane^32 exchange) ----
+      // The running max m_run is kept in log2 units (scores * sl2) and is
+      // only raised when some lane's block max exceeds it by more than
+      // 2^kLazy: below that, p = 2^(s*sl2 - m_run) stays <= 2^kLazy and the
+      // O/l rescale is skipped.  The decision is a wave-wide vote.
+      const bool need_mask = (kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0w);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
-      mx = max_xor32(mx) * sl2;
-      if (__any(mx > m_run + kLazy)) {
-        const float m_new = fmaxf(m_run, mx);
-        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        l_run *= corr;
+      for (int qt = 0; qt < QT; ++qt) {
+        if (need_mask) {
 #pragma unroll
-        for (int i = 0; i < DT; ++i) acc_o[i] *= corr;
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int kv = kv0 + t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+              const bool dead = (kv >= S) || (CAUSAL && kv > qrow[qt]);
+              s[qt][t][e] = dead ? -INFINITY : s[qt][t][e];
+            }
+        }
+        float mx = s[qt][0][0];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[qt][t][e]);
+        mx = max_xor32(mx) * sl2;
+        if (__any(mx > m_run[qt] + kLazy)) {
+          const float m_new = fmaxf(m_run[qt], mx);
+          const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+          m_run[qt] = m_new;
+          l_run[qt] *= corr;
+#pragma unroll
+          for (int i = 0; i < DT; ++i) acc_o[qt][i] *= corr;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s[qt][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qt][t][e], sl2, -m_run[qt]));
       }
-      float lsum = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[t][e] = __builtin_amdgcn_exp2f(fmaf(s[t][e], sl2, -m_run));
 
       // ---- O^T += V^T P^T over 4 key chunks of 16 ----
+      float lsum[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) lsum[qt] = 0.f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int t = c >> 1, i0 = 2 * (c & 1);
         // P^T operand: keys 16c + 4g + {0..3} then 16c + 8 + 4g + {0..3}
-        const u32x4 pf{T::pack2(s[t][4 * i0 + 0], s[t][4 * i0 + 1]), T::pack2(s[t][4 * i0 + 2], s[t][4 * i0 + 3]),
-                       T::pack2(s[t][4 * i0 + 4], s[t][4 * i0 + 5]), T::pack2(s[t][4 * i0 + 6], s[t][4 * i0 + 7])};
-        // the row sum uses the rounded P the MFMA consumes
-        lsum = dot2_ones<T>(pf[0], lsum);
-        lsum = dot2_ones<T>(pf[1], lsum);
-        lsum = dot2_ones<T>(pf[2], lsum);
-        lsum = dot2_ones<T>(pf[3], lsum);
+        u32x4 pf[QT];
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const unsigned char* vb = sv + v_lane_off + (16 * c) * Lds<D>::V_ROW + dt * 64;
-          const u32x2 lo = lds_read_tr16(vb);
-          const u32x2 hi = lds_read_tr16(vb + 8 * Lds<D>::V_ROW);
-          acc_o[dt] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, acc_o[dt]);
+        for (int qt = 0; qt < QT; ++qt) {
+          const f32x16& x = s[qt][t];
+          pf[qt] = u32x4{T::pack2(x[4 * i0 + 0], x[4 * i0 + 1]), T::pack2(x[4 * i0 + 2], x[4 * i0 + 3]),
+                         T::pack2(x[4 * i0 + 4], x[4 * i0 + 5]), T::pack2(x[4 * i0 + 6], x[4 * i0 + 7])};
+          // the row sum uses the rounded P the MFMA consumes
+#pragma unroll
+          for (int w = 0; w < 4; ++w) lsum[qt] = dot2_ones<T>(pf[qt][w], lsum[qt]);
         }
+        if (c + 1 < 4) {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) vb[(c + 1) & 1][dt] = vread(c + 1, dt);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) acc_o[qt][dt] = mfma32<T>(vb[c & 1][dt], pf[qt], acc_o[qt][dt]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the one-chunk read lookahead
       }
-      l_run += lsum;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) l_run[qt] += lsum[qt];
     }
 
     if (blk + 1 < nblk) store_kv(cur ^ 1);
@@ -269,30 +331,34 @@ __global__ __launch_bounds__(NT, 2) void gqa_fwd_kernel(const uint16_t* __restri
   }
 
   // ---- normalise and store: lane holds query qrow, d = 32dt + 8i + 4g + j ----
-  const float l_tot = sum_xor32(l_run);
-  const float inv = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
-  if (qrow < S) {
-    uint16_t* orow = O + (q_head + qrow) * D;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int qt = 0; qt < QT; ++qt) {
+    const float l_tot = sum_xor32(l_run[qt]);
+    const float inv = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
+    if (qrow[qt] < S) {
+      uint16_t* orow = O + (q_head + qrow[qt]) * D;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = dt * 32 + 8 * i + 4 * g;
-        const f32x16& a = acc_o[dt];
-        st64(orow + d, u32x2{T::pack2(a[4 * i] * inv, a[4 * i + 1] * inv), T::pack2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)});
-      }
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = dt * 32 + 8 * i + 4 * g;
+          const f32x16& a = acc_o[qt][dt];
+          st64(orow + d, u32x2{T::pack2(a[4 * i] * inv, a[4 * i + 1] * inv),
+                               T::pack2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)});
+        }
+    }
   }
 }
 
-template <int D, typename T, bool CAUSAL>
+template <int D, typename T, bool CAUSAL, int QT>
 static int launch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
                   hipStream_t stream) {
   const int G = Hq / Hkv;
   const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
-  const int QB = QW * (NWAVES / hpw);
+  const int QB = 32 * QT * (NWAVES / hpw);
   const long long grid = (long long)((S + QB - 1) / QB) * B * Hkv * (G / hpw);
   if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
-  auto kern = gqa_fwd_kernel<D, T, CAUSAL>;
+  auto kern = gqa_fwd_kernel<D, T, CAUSAL, QT>;
   MX_RETURN_IF_HIP(
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Lds<D>::TOTAL));
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), Lds<D>::TOTAL, stream, (const uint16_t*)Q,
@@ -301,13 +367,13 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
   return MX_OK;
 }
 
-template <typename T>
+template <typename T, int QT>
 static int dispatch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int D,
                     float scale, int causal, hipStream_t s) {
-  if (D == 128) return causal ? launch<128, T, true>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
-                              : launch<128, T, false>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
-  if (D == 64) return causal ? launch<64, T, true>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
-                             : launch<64, T, false>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+  if (D == 128) return causal ? launch<128, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
+                              : launch<128, T, false, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+  if (D == 64) return causal ? launch<64, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
+                             : launch<64, T, false, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
   return MX_ERR_UNSUPPORTED;
 }
 
@@ -324,6 +390,7 @@ extern "C" int mx_gqa_fwd(const void* Q, const void* K, const void* V, void* O, 
   if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
   if (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)O) & 15) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == MX_DTYPE_BF16) return mx::gqa::dispatch<mx::BF16>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, s);
-  return mx::gqa::dispatch<mx::F16>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, s);
+  constexpr int QT = MX_GQA_QT;
+  if (dtype == MX_DTYPE_BF16) return mx::gqa::dispatch<mx::BF16, QT>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, s);
+  return mx::gqa::dispatch<mx::F16, QT>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, s);
 }
