@@ -1,0 +1,145 @@
+"""Fused GQA forward harness cell: gfx950 HIP flash-attention kernel (mx_gqa_fwd).
+
+Drop-in for cutile-attn-gqa/main.py: flags --smoke (default), --bench,
+--csv-out, --block-m, --block-n, --iters (and --export-cubin / --cubin-out,
+accepted; gfx950 code objects are produced by the in-tree build, so the
+flag prints where the library is).  --smoke checks the reference's
+SHAPE_CORRECTNESS (1,128,4,2,64), f16, reference-distribution inputs
+against the committed golden oracle output with the reference's f16
+allclose gate (atol = rtol = 5e-3, :258-265); --bench times SHAPE_BENCH
+(llama3_8b, B1 S2048 Hq32 Hkv8 D128) with 2 warm-up + 10 timed launches
+and writes results.csv with the reference columns
+(impl,kernel,batch,seq,n_q,n_kv,d_head,block_m,block_n,iter,gpu_ms,tflops)
+plus, at the end, causal,dtype,tflops_causal.  Extra flags select the
+configuration this path is measured on: --shape baseline (S4096, causal,
+bf16, N(0,1) inputs), --causal, --dtype.  TFLOPS uses the reference's
+convention (4*B*Hq*S^2*D, flops.py:31-47); tflops_causal the causal
+algorithmic count 2*B*Hq*D*S*(S+1).
+"""
+from __future__ import annotations
+
+import argparse
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+import importlib  # noqa: E402
+
+H = importlib.import_module("cuda-oxide-bench_amd.harness")
+
+WARMUP = 2
+ITERS = 10
+BLOCK_M, BLOCK_N = 32, 64   # queries per wave tile, keys per LDS tile (fixed in the kernel)
+
+
+def run_smoke() -> bool:
+    import numpy as np
+    import torch
+
+    pkg = H.package()
+    ops = pkg.load_ops()
+    s = pkg.shapes.GQA_CORRECTNESS
+    print(f"[smoke] shape={s.name} B={s.batch} S={s.seq} n_q={s.n_q} n_kv={s.n_kv} d={s.d_head}")
+    g = H.load_golden("gqa_correctness_f16")
+    q, k, v = (H.from_bits(g[x], torch.float16).cuda() for x in "qkv")
+    o = ops.gqa_fwd(q, k, v, causal=False)
+    torch.cuda.synchronize()
+    o32 = o.float().cpu().numpy()
+    expected = g["o"]
+    tol = pkg.tolerances.get("f16")
+    abs_err = np.abs(o32 - expected)
+    max_abs = float(abs_err.max())
+    rel = max_abs / (np.abs(expected).max() + 1e-30)
+    ok = bool(np.allclose(o32, expected, atol=tol.atol, rtol=tol.rtol))
+    print(f"[smoke] max_abs={max_abs:.3e} rel={rel:.3e}  atol={tol.atol} rtol={tol.rtol}  {'OK' if ok else 'FAIL'}")
+    if not ok:
+        worst = np.unravel_index(abs_err.argmax(), abs_err.shape)
+        print(f"        worst offender at {worst}: got={o32[worst]:.4f} expected={expected[worst]:.4f}")
+    return ok
+
+
+def run_bench(shape, dtype, dist, csv_path: str, iters: int) -> None:
+    import torch
+
+    pkg = H.package()
+    ops = pkg.load_ops()
+    F = pkg.flops
+    print(f"[bench] shape={shape.name} B={shape.batch} S={shape.seq} n_q={shape.n_q} n_kv={shape.n_kv} "
+          f"d={shape.d_head} causal={shape.causal} dtype={dtype}")
+    q, k, v = (t.cuda() for t in pkg.inputs.gqa_inputs(shape, dtype=dtype, dist=dist))
+    out = torch.empty_like(q)
+    ms = H.time_iters(lambda: ops.gqa_fwd(q, k, v, causal=shape.causal, out=out), WARMUP, iters)
+    conv = F.gqa_attention_flops(shape)
+    alg = F.gqa_algorithmic_flops(shape)
+    dname = "bf16" if dtype == torch.bfloat16 else "f16"
+    rows = []
+    for i, m in enumerate(ms):
+        print(f"[bench] iter={i} gpu_ms={m:.3f} tflops={F.tflops(conv, m):.3f}")
+        rows.append(["hip", "gqa_fwd_fused", shape.batch, shape.seq, shape.n_q, shape.n_kv, shape.d_head, BLOCK_M,
+                     BLOCK_N, i, f"{m:.6f}", f"{F.tflops(conv, m):.6f}", int(shape.causal), dname,
+                     f"{F.tflops(alg, m):.6f}"])
+    H.write_csv(csv_path, ["impl", "kernel", "batch", "seq", "n_q", "n_kv", "d_head", "block_m", "block_n", "iter",
+                           "gpu_ms", "tflops", "causal", "dtype", "tflops_causal"], rows)
+    st = H.summarize_ms(ms)
+    H.print_summary(f"{shape.name} (algorithmic {'causal' if shape.causal else 'full'} FLOPs)", st,
+                    F.tflops(alg, st["best_ms"]), F.tflops(alg, st["median_ms"]), "TFLOPS", F.PEAK_BF16_TFLOPS)
+    H.write_sidecar(csv_path, {"kernel": "gqa_fwd_fused", "shape": shape.name, "causal": shape.causal,
+                               "dtype": dname, **st, "flops_algorithmic": alg, "flops_reference_convention": conv,
+                               "tflops_algorithmic_median": F.tflops(alg, st["median_ms"]),
+                               "peak_tflops": F.PEAK_BF16_TFLOPS,
+                               "frac_mfma_peak_median": F.tflops(alg, st["median_ms"]) / F.PEAK_BF16_TFLOPS,
+                               "bytes": F.gqa_attention_bytes(shape)})
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--smoke", action="store_true", default=False)
+    ap.add_argument("--bench", action="store_true", default=False)
+    ap.add_argument("--export-cubin", action="store_true", default=False)
+    ap.add_argument("--csv-out", default="results.csv")
+    ap.add_argument("--cubin-out", default="gqa_fwd_fused.cubin")
+    ap.add_argument("--block-m", type=int, default=None)
+    ap.add_argument("--block-n", type=int, default=None)
+    ap.add_argument("--iters", type=int, default=None)
+    ap.add_argument("--shape", choices=["llama3_8b", "baseline"], default="llama3_8b")
+    ap.add_argument("--causal", action="store_true", default=None)
+    ap.add_argument("--dtype", choices=["f16", "bf16"], default=None)
+    args = ap.parse_args()
+    if not (args.smoke or args.bench or args.export_cubin):
+        args.smoke = True
+
+    import dataclasses
+
+    import torch
+
+    H.banner()
+    if args.block_m is not None or args.block_n is not None:
+        print(f"[tile] requested BLOCK_M={args.block_m} BLOCK_N={args.block_n}; the gfx950 kernel uses "
+              f"{BLOCK_M} queries per wave x {BLOCK_N} keys per LDS tile")
+    print()
+    rc = H.EXIT_OK
+    if args.smoke:
+        if not run_smoke():
+            rc = H.EXIT_SMOKE_FAIL
+        print()
+    if args.bench:
+        pkg = H.package()
+        if args.shape == "baseline":
+            shape, dtype, dist = pkg.shapes.GQA_BASELINE, torch.bfloat16, "baseline"
+        else:
+            shape, dtype, dist = pkg.shapes.GQA_LLAMA3_8B, torch.float16, "reference"
+        if args.causal is not None:
+            shape = dataclasses.replace(shape, causal=True)
+        if args.dtype is not None:
+            dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+        run_bench(shape, dtype, dist, args.csv_out, args.iters if args.iters is not None else ITERS)
+        print()
+    if args.export_cubin:
+        lib = importlib.import_module("cuda-oxide-bench_amd._lib")
+        print(f"gfx950 code objects are embedded in {lib.lib_path()} (built in-tree by build.py); "
+              f"no cubin exists on this target")
+    return rc
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,111 @@
+"""MLA harness cell: gfx950 HIP absorbed latent-cache decode (mx_mla_decode).
+
+Keeps the CLI of cutile-attn-mla/main.py (--smoke default, --bench,
+--csv-out, --export-cubin / --cubin-out accepted) and its results.csv
+columns (impl,kernel,batch,seq,n_h,qk_head_dim,qk_pad,d_v,block_m,block_n,
+iter,gpu_ms,tflops) with gpu_us,gbps,frac_hbm,n_split appended.  The
+kernel is the weight-absorbed decode form of the reference's MLA attention
+(one query token per sequence over a 576-wide latent cache, values = the
+first 512 latent columns, scale 1/sqrt(192)), so in the CSV `seq` is the
+context length T, `qk_head_dim` / `qk_pad` are the 576-wide latent dot
+product (no padding) and `d_v` is 512.  --smoke checks the committed
+golden oracle output (H16, T40) with the bf16 normwise bound 2e-2;
+--bench times B32 H128 T4096 (DeepSeek-V3 shape) with 2 warm-up + 10
+timed launches.  GB/s counts the latent cache read once plus Q and O.
+"""
+from __future__ import annotations
+
+import argparse
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+import importlib  # noqa: E402
+
+H = importlib.import_module("cuda-oxide-bench_amd.harness")
+
+WARMUP = 2
+ITERS = 10
+TOL = 2e-2
+
+
+def run_smoke() -> bool:
+    import numpy as np
+    import torch
+
+    pkg = H.package()
+    ops = pkg.load_ops()
+    g = H.load_golden("mla_decode_h16_t40")
+    q, kv = H.from_bits(g["q"], torch.bfloat16).cuda(), H.from_bits(g["kv"], torch.bfloat16).cuda()
+    print(f"[smoke] absorbed decode B={q.shape[0]} H={q.shape[1]} T={kv.shape[1]} d_qk={q.shape[2]} d_v=512")
+    o = ops.mla_decode(q, kv, float(g["scale"][0]))
+    torch.cuda.synchronize()
+    o32 = o.float().cpu().numpy()
+    err = np.abs(o32 - g["o"])
+    rel = float(err.max() / (np.abs(g["o"]).max() + 1e-30))
+    ok = rel <= TOL
+    print(f"[smoke] max_abs={float(err.max()):.3e} rel={rel:.3e}  bound={TOL}  {'OK' if ok else 'FAIL'}")
+    return ok
+
+
+def run_bench(csv_path: str, iters: int) -> None:
+    import torch
+
+    pkg = H.package()
+    ops = pkg.load_ops()
+    F = pkg.flops
+    s = pkg.shapes.MLA_BASELINE
+    print(f"[bench] shape={s.name} B={s.batch} H={s.n_h} T={s.ctx} d_qk={s.d_qk} d_v={s.d_latent}")
+    q, kv = (t.cuda() for t in pkg.inputs.mla_inputs(s))
+    out = torch.empty((s.batch, s.n_h, s.d_latent), dtype=torch.bfloat16, device="cuda")
+    ws_bytes = ops.mla_decode_workspace_bytes(s.batch, s.n_h, s.ctx)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    n_split = ws_bytes // (s.batch * s.n_h * (s.d_latent + 2) * 4) if ws_bytes else 1
+    ms = H.time_iters(lambda: ops.mla_decode(q, kv, s.scale, out=out, workspace=ws), WARMUP, iters)
+    fl, nb = F.mla_decode_flops(s), F.mla_decode_bytes(s)
+    rows = []
+    for i, m in enumerate(ms):
+        print(f"[bench] iter={i} gpu_us={m * 1e3:.2f} gbps={F.gbps(nb, m):.1f} tflops={F.tflops(fl, m):.3f}")
+        rows.append(["hip", "mla_decode_absorbed", s.batch, s.ctx, s.n_h, s.d_qk, s.d_qk, s.d_latent, 64, 32, i,
+                     f"{m:.6f}", f"{F.tflops(fl, m):.6f}", f"{m * 1e3:.3f}", f"{F.gbps(nb, m):.3f}",
+                     f"{F.gbps(nb, m) / F.PEAK_HBM_GBPS:.5f}", n_split])
+    H.write_csv(csv_path, ["impl", "kernel", "batch", "seq", "n_h", "qk_head_dim", "qk_pad", "d_v", "block_m",
+                           "block_n", "iter", "gpu_ms", "tflops", "gpu_us", "gbps", "frac_hbm", "n_split"], rows)
+    st = H.summarize_ms(ms)
+    H.print_summary(f"{s.name} (HBM-bound)", st, F.gbps(nb, st["best_ms"]), F.gbps(nb, st["median_ms"]), "GB/s",
+                    F.PEAK_HBM_GBPS)
+    H.write_sidecar(csv_path, {"kernel": "mla_decode_absorbed", "shape": s.name, **st, "bytes": nb, "flops": fl,
+                               "gbps_median": F.gbps(nb, st["median_ms"]), "peak_gbps": F.PEAK_HBM_GBPS,
+                               "frac_hbm_peak_median": F.gbps(nb, st["median_ms"]) / F.PEAK_HBM_GBPS,
+                               "tflops_median": F.tflops(fl, st["median_ms"]), "n_split": n_split})
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--smoke", action="store_true", default=False)
+    ap.add_argument("--bench", action="store_true", default=False)
+    ap.add_argument("--export-cubin", action="store_true", default=False)
+    ap.add_argument("--csv-out", default="results.csv")
+    ap.add_argument("--cubin-out", default="mla_fwd_fused.cubin")
+    ap.add_argument("--iters", type=int, default=None)
+    args = ap.parse_args()
+    if not (args.smoke or args.bench or args.export_cubin):
+        args.smoke = True
+    H.banner()
+    print()
+    rc = H.EXIT_OK
+    if args.smoke:
+        if not run_smoke():
+            rc = H.EXIT_SMOKE_FAIL
+        print()
+    if args.bench:
+        run_bench(args.csv_out, args.iters if args.iters is not None else ITERS)
+        print()
+    if args.export_cubin:
+        lib = importlib.import_module("cuda-oxide-bench_amd._lib")
+        print(f"gfx950 code objects are embedded in {lib.lib_path()}; no cubin exists on this target")
+    return rc
+
+
+if __name__ == "__main__":
+    sys.exit(main())
