@@ -34,31 +34,27 @@ def log(msg: str) -> None:
 
 
 def time_launches(fn, steps: int, warmup: int):
-    """Run fn warmup times, then time exactly `steps` calls with a HIP event
-    pair around each launch on the current stream.  Returns (per-launch ms
-    list, wall ms per step over the bracketed region)."""
+    """Run fn `warmup` times, then time exactly `steps` back-to-back calls,
+    bracketed by torch.cuda.synchronize() and one HIP event pair on the
+    current stream (the stream the kernels are launched on).  Returns
+    (mean ms per launch from the events, wall ms per step from the host
+    clock).  One pair around the whole timed region instead of a pair per
+    launch: per-launch event pairs add ~10 us each on ROCm."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record()
+    start.record()
+    for _ in range(steps):
         fn()
-        ends[i].record()
+    end.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return per, wall_ms
-
-
-def summarize(per: list[float]) -> dict:
-    srt = sorted(per)
-    return {"mean_ms": sum(per) / len(per), "median_ms": srt[len(srt) // 2], "best_ms": srt[0]}
+    return start.elapsed_time(end) / steps, wall_ms
 
 
 def cpu_info() -> str:
@@ -80,18 +76,15 @@ def bench_gqa(pkg, ops, steps, warmup, cpu_baseline: bool):
     qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
     out = torch.empty_like(qd)
     fn = lambda: ops.gqa_fwd(qd, kd, vd, causal=True, out=out)  # noqa: E731
-    per, wall_ms = time_launches(fn, steps, warmup)
-    st = summarize(per)
+    mean_ms, wall_ms = time_launches(fn, steps, warmup)
     flops = F.gqa_causal_flops(shape)
     res = {
         "shape": shape,
-        "per": per,
         "wall_ms": wall_ms,
-        "stats": st,
+        "mean_ms": mean_ms,
         "flops": flops,
-        "tflops_mean": F.tflops(flops, st["mean_ms"]),
-        "tflops_best": F.tflops(flops, st["best_ms"]),
-        "tflops_ref_convention_best": F.tflops(F.gqa_attention_flops(shape), st["best_ms"]),
+        "tflops_mean": F.tflops(flops, mean_ms),
+        "tflops_ref_convention_mean": F.tflops(F.gqa_attention_flops(shape), mean_ms),
     }
     if cpu_baseline:
         res["cpu"] = cpu_baseline_gqa(shape, q, k, v, out)
@@ -149,13 +142,11 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
         a, b = I.gemm_inputs(shape)
         ad, bd = a.cuda(), b.cuda()
         c = torch.empty((shape.m, shape.n), dtype=torch.bfloat16, device="cuda")
-        per, _ = time_launches(lambda: ops.gemm_bf16(ad, bd, out=c), steps, warmup)
-        st = summarize(per)
+        ms, _ = time_launches(lambda: ops.gemm_bf16(ad, bd, out=c), steps, warmup)
         fl = F.gemm_flops(shape)
         res[f"gemm_bf16_{shape.m}"] = {
-            "unit": "TFLOPS", "mean_ms": st["mean_ms"], "best_ms": st["best_ms"],
-            "tflops_mean": F.tflops(fl, st["mean_ms"]), "tflops_best": F.tflops(fl, st["best_ms"]),
-            "frac_mfma_peak_mean": F.tflops(fl, st["mean_ms"]) / F.PEAK_BF16_TFLOPS,
+            "unit": "TFLOPS", "mean_ms": ms, "tflops_mean": F.tflops(fl, ms),
+            "frac_mfma_peak_mean": F.tflops(fl, ms) / F.PEAK_BF16_TFLOPS,
         }
         del ad, bd, c
         log(f"gemm_bf16 {shape.m}^3: {res[f'gemm_bf16_{shape.m}']['tflops_mean']:.1f} TFLOPS mean")
@@ -164,13 +155,11 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
     a8, sa, b8, sb = I.fp8_gemm_inputs(shape)
     a8d, sad, b8d, sbd = a8.cuda(), sa.cuda(), b8.cuda(), sb.cuda()
     c = torch.empty((shape.m, shape.n), dtype=torch.bfloat16, device="cuda")
-    per, _ = time_launches(lambda: ops.gemm_fp8_bs(a8d, sad, b8d, sbd, out=c), steps, warmup)
-    st = summarize(per)
+    ms, _ = time_launches(lambda: ops.gemm_fp8_bs(a8d, sad, b8d, sbd, out=c), steps, warmup)
     fl = F.gemm_flops(shape)
     res["gemm_fp8_bs_8192"] = {
-        "unit": "TFLOPS", "mean_ms": st["mean_ms"], "best_ms": st["best_ms"],
-        "tflops_mean": F.tflops(fl, st["mean_ms"]), "tflops_best": F.tflops(fl, st["best_ms"]),
-        "frac_mfma_peak_mean": F.tflops(fl, st["mean_ms"]) / F.PEAK_FP8_TFLOPS,
+        "unit": "TFLOPS", "mean_ms": ms, "tflops_mean": F.tflops(fl, ms),
+        "frac_mfma_peak_mean": F.tflops(fl, ms) / F.PEAK_FP8_TFLOPS,
     }
     del a8d, sad, b8d, sbd, c
     log(f"gemm_fp8_bs 8192^3: {res['gemm_fp8_bs_8192']['tflops_mean']:.1f} TFLOPS mean")
@@ -181,14 +170,11 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
     o = torch.empty((shape.batch, shape.n_h, shape.d_latent), dtype=torch.bfloat16, device="cuda")
     ws = torch.empty(max(1, ops.mla_decode_workspace_bytes(shape.batch, shape.n_h, shape.ctx)),
                      dtype=torch.uint8, device="cuda")
-    per, _ = time_launches(lambda: ops.mla_decode(qd, kvd, shape.scale, out=o, workspace=ws), steps, warmup)
-    st = summarize(per)
+    ms, _ = time_launches(lambda: ops.mla_decode(qd, kvd, shape.scale, out=o, workspace=ws), steps, warmup)
     nb, fl = F.mla_decode_bytes(shape), F.mla_decode_flops(shape)
     res["mla_decode"] = {
-        "unit": "GB/s", "mean_us": st["mean_ms"] * 1e3, "best_us": st["best_ms"] * 1e3,
-        "gbps_mean": F.gbps(nb, st["mean_ms"]), "gbps_best": F.gbps(nb, st["best_ms"]),
-        "frac_hbm_peak_mean": F.gbps(nb, st["mean_ms"]) / F.PEAK_HBM_GBPS,
-        "tflops_mean": F.tflops(fl, st["mean_ms"]),
+        "unit": "GB/s", "mean_us": ms * 1e3, "gbps_mean": F.gbps(nb, ms),
+        "frac_hbm_peak_mean": F.gbps(nb, ms) / F.PEAK_HBM_GBPS, "tflops_mean": F.tflops(fl, ms),
     }
     del qd, kvd, o, ws
     log(f"mla_decode: {res['mla_decode']['gbps_mean']:.0f} GB/s mean")
@@ -197,14 +183,12 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
     x = {n: t.cuda() for n, t in I.gdn_inputs(shape).items()}
     so = torch.empty_like(x["S_in"])
     od = torch.empty((shape.batch, shape.n_heads, shape.d_v), dtype=torch.bfloat16, device="cuda")
-    per, _ = time_launches(lambda: ops.gdn_decode(x["q"], x["k"], x["v"], x["alpha"], x["beta"], x["S_in"],
-                                                  S_out=so, o=od), steps, warmup)
-    st = summarize(per)
+    ms, _ = time_launches(lambda: ops.gdn_decode(x["q"], x["k"], x["v"], x["alpha"], x["beta"], x["S_in"],
+                                                 S_out=so, o=od), steps, warmup)
     nb = F.gdn_decode_bytes(shape)
     res["gdn_decode"] = {
-        "unit": "GB/s", "mean_us": st["mean_ms"] * 1e3, "best_us": st["best_ms"] * 1e3,
-        "gbps_mean": F.gbps(nb, st["mean_ms"]), "gbps_best": F.gbps(nb, st["best_ms"]),
-        "frac_hbm_peak_mean": F.gbps(nb, st["mean_ms"]) / F.PEAK_HBM_GBPS,
+        "unit": "GB/s", "mean_us": ms * 1e3, "gbps_mean": F.gbps(nb, ms),
+        "frac_hbm_peak_mean": F.gbps(nb, ms) / F.PEAK_HBM_GBPS,
     }
     log(f"gdn_decode: {res['gdn_decode']['gbps_mean']:.0f} GB/s mean")
     return res
@@ -250,7 +234,7 @@ def main() -> int:
 
     g = bench_gqa(pkg, ops, args.steps, args.warmup, cpu_baseline=not args.no_cpu_baseline)
     shape = g["shape"]
-    log(f"gqa_fwd causal S{shape.seq}: mean {g['stats']['mean_ms']:.4f} ms  {g['tflops_mean']:.1f} TFLOPS")
+    log(f"gqa_fwd causal S{shape.seq}: mean {g['mean_ms']:.4f} ms  {g['tflops_mean']:.1f} TFLOPS")
     others = {} if args.only_headline else bench_others(pkg, ops, args.steps, args.warmup)
 
     workload = (f"gqa_fwd causal B{shape.batch} Hq{shape.n_q} Hkv{shape.n_kv} S{shape.seq} "
@@ -284,11 +268,10 @@ def main() -> int:
             "frac": round(achieved / F.PEAK_BF16_TFLOPS, 5),
             "traffic": traffic,
             "kernel": "gqa_fwd_kernel<128, BF16, causal>",
-            "launch_mean_ms": round(g["stats"]["mean_ms"], 5),
-            "launch_best_ms": round(g["stats"]["best_ms"], 5),
+            "launch_mean_ms": round(g["mean_ms"], 5),
         },
         "cpu_baseline": g.get("cpu"),
-        "tflops_reference_convention_best": round(g["tflops_ref_convention_best"], 3),
+        "tflops_reference_convention": round(g["tflops_ref_convention_mean"], 3),
         "others": others,
     }
     print(json.dumps(line), flush=True)

@@ -12,41 +12,47 @@
 // so both reductions (k^T S and q^T S) come out of the single read of S.
 //
 // Layout and schedule (bandwidth-bound: 2 x d_k x d_v x 4 bytes per head):
-//  * one workgroup per (b, hv); NT = d_k*d_v/64 threads so that every thread
-//    keeps exactly 16 rows x 4 columns (64 fp32) of the state in VGPRs
-//    between the read and the write — S is read once and written once;
-//  * a thread's 4 columns are one 128-bit load/store; TC = d_v/4 threads
-//    cover a full row, so each wave-wide load touches whole 512-byte rows;
-//  * the d_v-wide partial reductions over each thread's 16 rows meet in LDS
-//    (RG = d_k/16 row groups), one barrier, then every thread forms u, r, o
-//    for its own columns and streams its rows of S' back out.
+//  * one workgroup per (b, hv, column block of BV values of d_v) — every
+//    column of S is independent, so the d_v split needs no cross-workgroup
+//    reduction (the reference tiles d_v the same way, main.py:228-246).  BV
+//    is chosen at launch so that small batches still spread over the CUs;
+//  * NT = d_k*BV/64 threads so every thread keeps exactly 16 rows x 4
+//    columns (64 fp32) of the state in VGPRs between the read and the
+//    write — S is read once and written once, with 128-bit non-temporal
+//    loads/stores, BV/4 threads covering a row segment;
+//  * the BV-wide partial reductions over each thread's 16 rows meet in LDS
+//    (d_k/16 row groups), one barrier, then every thread forms u, r, o for
+//    its own columns and streams its rows of S' back out.
 #include "mx_common.h"
 
 namespace mx {
 namespace gdn {
 
-template <int DK, int DV, typename T>
-__global__ __launch_bounds__(DK * DV / 64) void gdn_decode_kernel(
+template <int DK, int BV, typename T>
+__global__ __launch_bounds__(DK * BV / 64) void gdn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const float* __restrict__ alpha, const float* __restrict__ beta, const float* S_in, float* S_out,
-    uint16_t* __restrict__ o, int Hk, int Hv) {
-  constexpr int NT = DK * DV / 64;
-  constexpr int TC = DV / 4;   // threads across a row
+    uint16_t* __restrict__ o, int Hk, int Hv, int DV) {
+  constexpr int NT = DK * BV / 64;
+  constexpr int TC = BV / 4;   // threads across a row segment
   constexpr int RG = NT / TC;  // row groups (= DK / 16)
   constexpr int RPT = DK / RG; // rows per thread (= 16)
   static_assert(RPT == 16, "16 rows per thread");
 
   __shared__ float qs[DK], ks[DK];
-  __shared__ __align__(16) float red_u[RG][DV];
-  __shared__ __align__(16) float red_w[RG][DV];
+  __shared__ __align__(16) float red_u[RG][BV];
+  __shared__ __align__(16) float red_w[RG][BV];
   __shared__ float red_qk[RG];
 
-  const int bh = blockIdx.x;  // b * Hv + hv
+  const int nvb = DV / BV;
+  const int bh = blockIdx.x / nvb;  // b * Hv + hv
+  const int vblk = blockIdx.x % nvb;
   const int b = bh / Hv, hv = bh % Hv;
   const int hk = hv / (Hv / Hk);
   const int t = threadIdx.x;
   const int cg = t % TC, rg = t / TC;
-  const int c0 = cg * 4;
+  const int cl = cg * 4;              // column within the block
+  const int c0 = vblk * BV + cl;      // column within d_v
 
   const size_t sbase = (size_t)bh * DK * DV;
   const float* Sin = S_in + sbase;
@@ -87,18 +93,18 @@ __global__ __launch_bounds__(DK * DV / 64) void gdn_decode_kernel(
       w[c] = fmaf(qi, s[r][c], w[c]);
     }
   }
-  *reinterpret_cast<f32x4*>(&red_u[rg][c0]) = f32x4{u[0], u[1], u[2], u[3]};
-  *reinterpret_cast<f32x4*>(&red_w[rg][c0]) = f32x4{w[0], w[1], w[2], w[3]};
+  *reinterpret_cast<f32x4*>(&red_u[rg][cl]) = f32x4{u[0], u[1], u[2], u[3]};
+  *reinterpret_cast<f32x4*>(&red_w[rg][cl]) = f32x4{w[0], w[1], w[2], w[3]};
   if (cg == 0) red_qk[rg] = qk;
   __syncthreads();
 
   f32x4 ut{0.f, 0.f, 0.f, 0.f}, wt{0.f, 0.f, 0.f, 0.f};
   float qkt = 0.f;
 #pragma unroll
-  for (int g = 0; g < RG; ++g) {
-    ut += *reinterpret_cast<const f32x4*>(&red_u[g][c0]);
-    wt += *reinterpret_cast<const f32x4*>(&red_w[g][c0]);
-    qkt += red_qk[g];
+  for (int gi = 0; gi < RG; ++gi) {
+    ut += *reinterpret_cast<const f32x4*>(&red_u[gi][cl]);
+    wt += *reinterpret_cast<const f32x4*>(&red_w[gi][cl]);
+    qkt += red_qk[gi];
   }
 
   float res[4], of[4];
@@ -122,32 +128,52 @@ __global__ __launch_bounds__(DK * DV / 64) void gdn_decode_kernel(
   }
 }
 
-template <int DK, int DV, typename T>
+template <int DK, int BV, typename T>
 static int launch(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
-                  const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, hipStream_t s) {
-  hipLaunchKernelGGL((gdn_decode_kernel<DK, DV, T>), dim3(B * Hv), dim3(DK * DV / 64), 0, s,
+                  const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dv, hipStream_t s) {
+  const long long grid = (long long)B * Hv * (dv / BV);
+  if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
+  hipLaunchKernelGGL((gdn_decode_kernel<DK, BV, T>), dim3((unsigned)grid), dim3(DK * BV / 64), 0, s,
                      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, alpha, beta, S_in, S_out,
-                     (uint16_t*)o, Hk, Hv);
+                     (uint16_t*)o, Hk, Hv, dv);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
+}
+
+// Column-block width: the widest of {d_v, d_v/2, ...} (>= 16 and >= 4096/d_k,
+// i.e. at least one wave per workgroup) that still gives >= 1024 workgroups;
+// the narrowest allowed one otherwise.
+static int pick_bv(int B, int Hv, int dk, int dv) {
+  const int min_bv = (4096 / dk > 16) ? 4096 / dk : 16;
+  int bv = dv;
+  while (bv / 2 >= min_bv && (long long)B * Hv * (dv / bv) < 1024) bv /= 2;
+  return bv;
+}
+
+template <int DK, typename T>
+static int dispatch_dk(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
+                       const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dv, hipStream_t s) {
+  const int bv = pick_bv(B, Hv, DK, dv);
+#define MX_GDN_BV(BV_)                                                                             \
+  if (bv == BV_) {                                                                                 \
+    if constexpr (DK * BV_ >= 4096) return launch<DK, BV_, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dv, s); \
+  }
+  MX_GDN_BV(16)
+  MX_GDN_BV(32)
+  MX_GDN_BV(64)
+  MX_GDN_BV(128)
+  MX_GDN_BV(256)
+#undef MX_GDN_BV
+  return MX_ERR_UNSUPPORTED;
 }
 
 template <typename T>
 static int dispatch(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
                     const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dk, int dv,
                     hipStream_t s) {
-#define MX_GDN_CASE(DK_, DV_) \
-  if (dk == DK_ && dv == DV_) return launch<DK_, DV_, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, s);
-  MX_GDN_CASE(64, 64)
-  MX_GDN_CASE(64, 128)
-  MX_GDN_CASE(64, 256)
-  MX_GDN_CASE(128, 64)
-  MX_GDN_CASE(128, 128)
-  MX_GDN_CASE(128, 256)
-  MX_GDN_CASE(256, 64)
-  MX_GDN_CASE(256, 128)
-  MX_GDN_CASE(256, 256)
-#undef MX_GDN_CASE
+  if (dk == 64) return dispatch_dk<64, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dv, s);
+  if (dk == 128) return dispatch_dk<128, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dv, s);
+  if (dk == 256) return dispatch_dk<256, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dv, s);
   return MX_ERR_UNSUPPORTED;
 }
 
@@ -162,7 +188,7 @@ extern "C" int mx_gdn_decode(const void* q, const void* k, const void* v, const 
   if (!q || !k || !v || !alpha || !beta || !S_in || !S_out || !o) return MX_ERR_NULL;
   if (B <= 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return MX_ERR_SHAPE;
   if (!mx_is_dim(dk) || !mx_is_dim(dv)) return MX_ERR_SHAPE;
-  if ((long long)B * Hv > 0x7fffffffLL) return MX_ERR_SHAPE;
+  if ((long long)B * Hv > 0x7fffffffLL / 16) return MX_ERR_SHAPE;
   if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
   if (((uintptr_t)S_in | (uintptr_t)S_out) & 15) return MX_ERR_ALIGN;
   if (((uintptr_t)v | (uintptr_t)o) & 7) return MX_ERR_ALIGN;

@@ -46,21 +46,58 @@ def banner() -> None:
     print(f"package: {pkg.__name__} {pkg.__version__}")
 
 
-def time_iters(fn, warmup: int, iters: int) -> list[float]:
-    """warmup untimed calls, then `iters` calls each bracketed by an event pair."""
+def time_iters(fn, warmup: int, iters: int, min_group_ms: float = 0.5, graph: bool = True) -> list[float]:
+    """warmup untimed calls, then `iters` timed samples of the per-launch time.
+
+    Each sample is one event pair around a group of back-to-back launches,
+    divided by the group size; the group is sized (from an untimed probe)
+    to last at least `min_group_ms`.  With graph=True the group is captured
+    once into a HIP graph (torch.cuda.CUDAGraph) and replayed, so the
+    sample measures the kernels rather than the host cost of issuing them
+    (~10 us per operator call from Python).  An event pair around every
+    single launch, as the reference's CUDA harnesses use, also adds ~10 us
+    per launch on ROCm, which would swamp the few-microsecond decode kernels.
+    """
+    import time
+
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize()
+    est_ms = max((time.perf_counter() - t0) * 1e3, 1e-3)
+    reps = max(1, min(200, int(min_group_ms / est_ms + 0.999)))
+    run_group = None
+    if graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()  # first call on the capture stream outside the capture
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        run_group = g.replay
+    else:
+        def run_group():
+            for _ in range(reps):
+                fn()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     for i in range(iters):
         starts[i].record()
-        fn()
+        run_group()
         ends[i].record()
     torch.cuda.synchronize()
-    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return [s.elapsed_time(e) / reps for s, e in zip(starts, ends)]
 
 
 def summarize_ms(ms: list[float]) -> dict:
