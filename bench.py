@@ -194,6 +194,26 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
     return res
 
 
+def calibrate_copy(steps: int) -> int:
+    """A plain device-to-device copy of a known size (1 GiB read + 1 GiB
+    written per launch), for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE
+    readings of the kernels above to bytes."""
+    import torch
+
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read_per_launch": n, "bytes_written_per_launch": n,
+                      "launches": steps}), flush=True)
+    return 0
+
+
 def load_traffic(workload: str):
     """HBM bytes per launch of the headline kernel from the committed rocprofv3
     PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated), if it covers this workload."""
@@ -214,6 +234,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a 1 GiB device copy (profiler calibration of byte counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -227,6 +249,8 @@ def main() -> int:
 
     import torch
 
+    if args.calibrate_copy:
+        return calibrate_copy(args.steps)
     pkg = importlib.import_module("cuda-oxide-bench_amd")
     ops = pkg.load_ops()
     F = pkg.flops
