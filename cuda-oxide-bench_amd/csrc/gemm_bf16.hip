@@ -32,14 +32,6 @@ namespace gemm {
 constexpr int BK = 64;  // K tile depth (bf16 elements)
 constexpr int GROUP_M = 8;
 
-__device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
-  typedef short v4i16 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16*)(__attribute__((address_space(3))) const unsigned char*)p);
-  return __builtin_bit_cast(u32x2, r);
-}
-
 template <int BM, int BN, int WM, int WN>
 struct Cfg {
   static constexpr int NT = 64 * WM * WN;          // threads

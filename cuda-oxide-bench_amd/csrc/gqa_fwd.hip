@@ -62,33 +62,6 @@ struct Lds {
   static constexpr int TOTAL = 2 * STAGE;
 };
 
-// ds_read_b64_tr_b16 (gfx950 transposing LDS read).  Within each group of
-// 16 lanes, lane 4a+b receives element b of the 8-byte rows addressed by
-// lanes a, 4+a, 8+a, 12+a (in that order).  Pointing lane 4j+a at
-// V[key_j][d0 + 4a] therefore hands lane 4a+b the column d0+4a+b for keys
-// key_0..key_3: a k-contiguous MFMA operand read straight from row-major V.
-__device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
-  typedef short v4i16 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16*)(__attribute__((address_space(3))) const unsigned char*)p);
-  return __builtin_bit_cast(u32x2, r);
-}
-
-// Running-sum helper: acc + x.lo + x.hi for a dword of two bf16 / f16.
-template <typename T>
-__device__ __forceinline__ float dot2_ones(uint32_t x, float acc);
-template <>
-__device__ __forceinline__ float dot2_ones<BF16>(uint32_t x, float acc) {
-  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, x), bf2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
-}
-template <>
-__device__ __forceinline__ float dot2_ones<F16>(uint32_t x, float acc) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x), h2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
-}
-
 template <int D, typename T, bool CAUSAL, int QT>
 __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
                                                                      const uint16_t* __restrict__ K,

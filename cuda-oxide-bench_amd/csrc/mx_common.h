@@ -168,6 +168,71 @@ __device__ __forceinline__ void transpose4x8_b16(const u32x4 in[4], u32x2 out[8]
 }
 
 // ---------------------------------------------------------------------------
+// LDS helpers.
+// ---------------------------------------------------------------------------
+// ds_read_b64_tr_b16 (gfx950 transposing LDS read).  Within each group of
+// 16 lanes, lane 4a+b receives element b of the 8-byte rows addressed by
+// lanes a, 4+a, 8+a, 12+a (in that order).  Pointing lane 4j+a at
+// V[key_j][d0 + 4a] therefore hands lane 4a+b the column d0+4a+b for keys
+// key_0..key_3: a k-contiguous MFMA operand read straight from row-major V.
+__device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(__attribute__((address_space(3))) const unsigned char*)p);
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// Running-sum helper: acc + x.lo + x.hi for a dword of two bf16 / f16.
+template <typename T>
+__device__ __forceinline__ float dot2_ones(uint32_t x, float acc);
+template <>
+__device__ __forceinline__ float dot2_ones<BF16>(uint32_t x, float acc) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, x), bf2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2_ones<F16>(uint32_t x, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x), h2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+}
+
+// Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4).
+// Lane i reads 16 bytes at sbase + voff_i and they land at LDS byte address
+// lds_addr + 16*i: one instruction fills 1 KB of LDS in lane order without
+// passing through VGPRs.  sbase and lds_addr are wave-uniform (SGPRs).
+//
+// Issued as inline asm on purpose: the compiler then does not know that
+// LDS is written behind its back, so it inserts none of its conservative
+// vmcnt(0) waits before LDS reads.  The caller owns the synchronisation:
+// wait_vmcnt<n>() until the loads of a stage have landed, then a barrier
+// before other waves read them, and nothing of its own may be outstanding
+// on vmcnt that the compiler would wait for with a smaller count (complete
+// compiler-visible global loads with wait_vmcnt<0>() before issuing these).
+// M0 is clobbered; no code here relies on M0 across the statement.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  // s_nop: one wait state between an SALU write of M0 and an LDS-DMA load.
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %0" ::"s"(sbase), "v"(voff), "s"(lds_addr)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// 32-bit LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) unsigned char*)p);
+}
+
+// s_waitcnt vmcnt(n) with the other counters untouched (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// ---------------------------------------------------------------------------
 // Global memory helpers.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ u32x4 ld128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
