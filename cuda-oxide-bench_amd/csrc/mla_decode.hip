@@ -9,27 +9,34 @@
 // which is the weight-absorbed decode form of
 // analysis/wave15-attention-research/MECHANISMS.md:91-94, 115-120.
 //
-// MI355X design.  With 128 heads the work is close to the HBM/MFMA ridge
-// (about 240 flop per cache byte), so both the single read of the cache and
-// the matrix-core rate matter:
-//  * a wave owns 32 heads and 32 tokens of each stage and runs 32x32x16
-//    MFMAs: S^T = K . Q^T (Q^T for its heads stays in VGPRs, 36 k-steps),
-//    then O^T += V^T . P^T with P^T straight from the score registers and
-//    V^T read from the row-major cache tile with ds_read_b64_tr_b16;
-//  * a workgroup (4 waves) owns one sequence, one slice of T ("split") and
-//    NHG head groups; the NTP = 4/NHG waves of one head group take
-//    different tokens of each stage and are merged at the end;
+// MI355X design.  With 128 heads the work sits near the HBM/MFMA ridge
+// (about 240 flop per cache byte) and LDS fragment traffic is the tightest
+// resource, so the two matrix products are partitioned differently across
+// the 4 waves of a workgroup (one sequence, 128 heads, one slice of T):
+//  * scores: wave g owns heads 32g..32g+31.  S^T = K . Q^T with 32x32x16
+//    MFMAs, Q^T in VGPRs (36 k-steps), K fragments read from LDS; online
+//    softmax with a lazily raised running max (the value accumulators are
+//    rescaled only when a block max exceeds it by more than 2^16).  The
+//    bf16 P^T fragments, already in MFMA B-operand layout, go to LDS (2 KB
+//    per wave per stage);
+//  * values: wave v owns latent columns 128v..128v+127 for all 128 heads:
+//    O^T += V^T . P^T, where each V^T fragment (ds_read_b64_tr_b16 straight
+//    from the row-major cache rows) serves the 4 head groups.  Per stage a
+//    wave reads 8 KB of V and 8 KB of P instead of 32 KB of V;
+//  * software pipeline: iteration i computes the scores of stage i and the
+//    values of stage i-1, even waves in that order and odd waves the other
+//    way round, so at any time about half the SIMDs run the LDS-heavy
+//    score phase and half the MFMA-heavy value phase (one barrier per
+//    stage);
 //  * cache rows go HBM -> LDS with global_load_lds_dwordx4 (no VGPR
-//    staging) into a ring of stages, 147 KB in all; the 16-byte chunks of
-//    a row are XOR-swizzled inside groups of 8 so that both the K reads
-//    (8 consecutive tokens, one chunk) and the transposing V reads (4
-//    consecutive tokens, two chunks) hit distinct banks;
-//  * the running max is raised lazily (only when a block max exceeds it by
-//    more than 2^8), so the 256-register O accumulator is rarely rescaled;
+//    staging): latent rows into a 4-slot ring (a stage is read by the
+//    scores of one iteration and the values of the next), rope rows into a
+//    3-slot ring; 16-byte chunks are XOR-swizzled so both the K reads and
+//    the transposing V reads are bank-conflict free;
 //  * T is split across workgroups to fill the 256 CUs; each split writes
-//    (m, l, unnormalised o) to the workspace in a lane-major layout (1 KB
-//    coalesced stores) and a second kernel merges the splits with the
-//    log-sum-exp rule.  With one split, O is written directly.
+//    its normalised partial output (bf16, coalesced 512 B stores) and
+//    (m, l) to the workspace, and a second kernel merges the splits with
+//    the log-sum-exp rule.  With one split, O is written directly.
 #include "mx_common.h"
 
 namespace mx {
@@ -37,29 +44,31 @@ namespace mla {
 
 constexpr int DQK = 576;
 constexpr int DV = 512;
-constexpr int CH = DQK / 8;             // 72 sixteen-byte chunks per cache row
-constexpr int ROW_B = DQK * 2;          // 1152 bytes per cache row in LDS
-constexpr int HPW = 32;                 // heads per wave
-constexpr int TPW = 32;                 // tokens per wave per stage
+constexpr int ROW_B = DQK * 2;          // 1152 bytes per cache row in HBM
+constexpr int HPW = 32;                 // heads per score wave
 constexpr int NWAVES = 4;
 constexpr int NT = 64 * NWAVES;
+constexpr int HPG = HPW * NWAVES;       // 128 heads per workgroup
+constexpr int BT = 32;                  // tokens per stage
 constexpr int KS = DQK / 16;            // 36 k-steps of S^T
-constexpr int VT = DV / 32;             // 16 dv tiles of O^T
-constexpr int LDS_BYTES = NWAVES * TPW * ROW_B;  // 147456
+constexpr int VT = DV / 32;             // 16 latent tiles of O^T
+constexpr int VTW = VT / NWAVES;        // 4 latent tiles per value wave
+constexpr int NLAT = 4;                 // latent ring slots (32 rows x 1 KB)
+constexpr int NROPE = 3;                // rope ring slots (32 rows x 128 B)
+constexpr int LPW = BT / NWAVES + 1;    // 1 KB loads per wave per stage (8 latent rows + 8 rope rows)
+constexpr int LAT_B = BT * 1024;
+constexpr int ROPE_B = BT * 128;
+constexpr int ROPE_OFF = NLAT * LAT_B;                 // 131072
+constexpr int P_OFF = ROPE_OFF + NROPE * ROPE_B;       // P^T fragments: [2 buf][4 group][2 k-half][64 lanes] x 16 B
+constexpr int P_BUF = NWAVES * 2 * 64 * 16;
+constexpr int C_OFF = P_OFF + 2 * P_BUF;               // rescale factors: [2 buf][4 group][32] fp32
+constexpr int F_OFF = C_OFF + 2 * NWAVES * 32 * 4;     // rescale flags: [2 buf][4 group] int
+constexpr int L_OFF = F_OFF + 2 * NWAVES * 4;          // final row sums: [4 group][32] fp32
+constexpr int LDS_BYTES = L_OFF + NWAVES * 32 * 4;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLazy = 8.0f;           // log2 headroom before a rescale
-
-template <int NTP>
-struct Cfg {
-  static constexpr int NHG = NWAVES / NTP;              // head groups per workgroup
-  static constexpr int HPG = NHG * HPW;                 // heads per workgroup
-  static constexpr int BT = NTP * TPW;                  // tokens per stage
-  static constexpr int STAGE_B = BT * ROW_B;
-  static constexpr int NS = LDS_BYTES / STAGE_B;        // ring depth
-  static constexpr int LPW = BT / NWAVES + NTP;         // 1 KB loads per wave per stage
-  static_assert(BT * CH == 64 * NWAVES * LPW, "stage splits into whole wave loads");
-  static_assert(NS >= 2, "double buffering at least");
-};
+constexpr float kLazy = 16.0f;          // log2 headroom before a rescale
+static_assert(BT * DQK / 8 == 64 * NWAVES * LPW, "a stage splits into whole wave loads");
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 // Chunk c of row t sits at chunk position c ^ swz(t) of its row.  swz maps
 // t%8 to 0,2,4,6,1,3,5,7: distinct over 8 rows (K reads: 8 consecutive
@@ -87,168 +96,146 @@ struct Split {
   int tps;  // tokens per split (multiple of the stage)
 };
 
-template <int NTP>
 __host__ __device__ inline Split pick_split(int B, int H, int T) {
-  using C = Cfg<NTP>;
-  const int hg = (H + C::HPG - 1) / C::HPG;
-  const int nblk = (T + C::BT - 1) / C::BT;
+  const int hg = (H + HPG - 1) / HPG;
+  const int nblk = (T + BT - 1) / BT;
   // Aim for >= 256 workgroups (one per CU) with at least 2 stages per split.
   int ns = 1;
   while ((long long)B * hg * ns < 256 && ns * 2 <= nblk / 2) ns *= 2;
   const int blocks_per = (nblk + ns - 1) / ns;
   Split s;
   s.nsplit = (nblk + blocks_per - 1) / blocks_per;
-  s.tps = blocks_per * C::BT;
+  s.tps = blocks_per * BT;
   return s;
 }
 
-// Stage layout in LDS: BT latent rows of 1024 B (64 chunks), then BT rope
-// rows of 128 B (8 chunks), chunk c of row t at position c ^ swz(t).
-// Issue the direct loads of one stage: each 1 KB wave load fills one latent
-// row (lane i <- chunk i ^ swz(t), from a wave-uniform row address) or
-// eight rope rows.  Rows past the end of the split re-read the last valid
-// row (finite data whose scores are masked).
-template <int NTP>
-__device__ __forceinline__ void issue_stage(const unsigned char* kvb, int tok0, int t1, uint32_t stage, int wave,
-                                            int lane) {
-  using C = Cfg<NTP>;
-  constexpr int LR = C::BT / NWAVES;  // latent rows per wave
+// Stage i of a split: 32 latent rows of 1024 B (64 chunks) in latent slot
+// i%4 and 32 rope rows of 128 B (8 chunks) in rope slot i%3, chunk c of row
+// t at position c ^ swz(t).  Each 1 KB wave load fills one latent row (lane
+// j <- chunk j ^ swz(t), from a wave-uniform row address) or eight rope
+// rows.  Rows past the end of the split re-read the last valid row (finite
+// data whose scores are masked).
+__device__ __forceinline__ void issue_stage(const unsigned char* kvb, int tok0, int t1, uint32_t lat, uint32_t rope,
+                                            int wave, int lane) {
+  constexpr int LR = BT / NWAVES;  // latent rows per wave
   uint32_t l16 = lane * 16;
-  asm volatile("" : "+v"(l16));  // keep the per-row XORs in the loop instead of 8 hoisted VGPRs
+  asm volatile("" : "+v"(l16));  // keep the per-row XORs here instead of 8 hoisted VGPRs
 #pragma unroll
   for (int n = 0; n < LR; ++n) {
     const int r = wave * LR + n;
     const int tok = min(tok0 + r, t1 - 1);
-    dma16(kvb + (size_t)tok * ROW_B, l16 ^ (uint32_t)(16 * swz(r)), stage + r * 1024);
+    dma16(kvb + (size_t)tok * ROW_B, l16 ^ (uint32_t)(16 * swz(r)), lat + r * 1024);
   }
-  const bool full = tok0 + C::BT <= t1;
-#pragma unroll
-  for (int n = 0; n < NTP; ++n) {
-    const int r0 = (wave * NTP + n) * 8;
-    const int tb = min(tok0 + r0, t1 - 1);
-    int tok = tok0 + r0 + (lane >> 3);
-    if (!full) tok = min(tok, t1 - 1);
-    const uint32_t off = (uint32_t)(tok - tb) * ROW_B + 16 * (64 + ((lane & 7) ^ swz(lane >> 3)));
-    dma16(kvb + (size_t)tb * ROW_B, off, stage + C::BT * 1024 + r0 * 128);
-  }
+  const int r0 = wave * 8;
+  const int tb = min(tok0 + r0, t1 - 1);
+  const int tok = min(tok0 + r0 + (lane >> 3), t1 - 1);
+  const uint32_t off = (uint32_t)(tok - tb) * ROW_B + 16 * (64 + ((lane & 7) ^ swz(lane >> 3)));
+  dma16(kvb + (size_t)tb * ROW_B, off, rope + r0 * 128);
 }
 
-// Wait until at most `ahead` stages of this wave's loads are outstanding.
-template <int LPW, int NS>
-__device__ __forceinline__ void wait_stages(int ahead) {
-  if constexpr (NS >= 4) {
-    if (ahead >= 2) {
-      wait_vmcnt<2 * LPW>();
-      return;
-    }
-  }
-  if constexpr (NS >= 3) {
-    if (ahead >= 1) {
-      wait_vmcnt<LPW>();
-      return;
-    }
-  }
-  wait_vmcnt<0>();
-}
+// Partial tile of one (sequence, split, 32-head group): 64 slots (latent
+// tile vt, row quad i) x 64 lanes x 4 bf16 = 32 KB, normalised by its own
+// row sum; (m, l) per head in ws_ml.
+constexpr int PT_U32 = VT * 4 * 64 * 2;  // uint32 words per partial tile
 
-template <int NTP>
 __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __restrict__ Q,
                                                           const uint16_t* __restrict__ KV,
-                                                          uint16_t* __restrict__ O, float* __restrict__ ws_o,
+                                                          uint16_t* __restrict__ O, uint32_t* __restrict__ ws_o,
                                                           float* __restrict__ ws_ml, int B, int H, int T,
                                                           float sl2, int nsplit, int tps) {
-  using C = Cfg<NTP>;
   extern __shared__ __align__(1024) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int hgi = wave % C::NHG;  // head group of this wave
-  const int tp = wave / C::NHG;   // token part of each stage
   const int hsel = lane >> 5, l32 = lane & 31;
 
-  const int HGB = (H + C::HPG - 1) / C::HPG;
+  const int HGB = (H + HPG - 1) / HPG;
   const int nwg = B * HGB * nsplit;
   const int id = xcd_remap(blockIdx.x, nwg);
   const int hgb = id % HGB;
   const int s = (id / HGB) % nsplit;
   const int b = id / (HGB * nsplit);
 
-  const int hw = hgb * C::NHG + hgi;  // 32-head group index
-  const int head = hw * HPW + l32;
-  const bool head_ok = head < H;
   const int t0 = s * tps;
   const int t1 = min(T, t0 + tps);
-  const int nblk = (t1 - t0 + C::BT - 1) / C::BT;
+  const int nblk = (t1 - t0 + BT - 1) / BT;
 
-  // Q^T fragments (B operand): lane holds head `head`, features 16 ks + 8 hsel .. +7.
-  // Padding heads (head >= H) reuse the last real head's row; their
-  // results are never stored.
+  // Score role: heads hgb*128 + 32*wave + l32.  Padding heads (>= H) reuse
+  // the last real head's row; their results are never stored.
+  const int head_s = hgb * HPG + wave * HPW + l32;
   u32x4 qf[KS];
   {
-    const uint16_t* qrow = Q + ((size_t)b * H + min(head, H - 1)) * DQK + 8 * hsel;
+    const uint16_t* qrow = Q + ((size_t)b * H + min(head_s, H - 1)) * DQK + 8 * hsel;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = ld128(qrow + 16 * ks);
   }
 
-  // Ring prologue.  The Q loads are completed together with stage 0, so no
-  // compiler-visible load is outstanding once the cache loads stream.
   const unsigned char* kvb = reinterpret_cast<const unsigned char*>(KV + (size_t)b * T * DQK);
   const uint32_t lds0 = lds_addr(smem);
-  issue_stage<NTP>(kvb, t0, t1, lds0, wave, lane);
-  wait_vmcnt<0>();
-#pragma unroll
-  for (int p = 1; p < C::NS - 1; ++p)
-    if (p < nblk) issue_stage<NTP>(kvb, t0 + p * C::BT, t1, lds0 + p * C::STAGE_B, wave, lane);
-
-  // K fragment (A operand): row tp*32 + l32, chunk 2 ks + hsel.
-  const int krow = tp * TPW + l32;
-  const int kx = swz(krow);
-  const int k_lat = krow * 1024;
-  const int k_rope = C::BT * 1024 + krow * 128;
-  auto kread = [&](const unsigned char* st, int ks) {
-    const int c = 2 * ks + hsel;
-    return ks < 32 ? ld128(st + k_lat + 16 * (c ^ kx)) : ld128(st + k_rope + 16 * ((c - 64) ^ kx));
+  auto issue = [&](int i) {
+    issue_stage(kvb, t0 + i * BT, t1, lds0 + (i & (NLAT - 1)) * LAT_B, lds0 + ROPE_OFF + (i % NROPE) * ROPE_B, wave,
+                lane);
   };
+  // Ring prologue.  The Q loads complete together with stage 0, so no
+  // compiler-visible load is outstanding once the cache loads stream.
+  issue(0);
+  wait_vmcnt<0>();
+  if (nblk > 1) issue(1);
+
+  // K fragment (A operand): row l32, chunk c = 2 ks + hsel at position
+  // 8 (ks/4) + ((2 (ks%4) + hsel) ^ swz(l32)): four lane offsets plus an
+  // immediate per k-step; the rope rows (ks >= 32) are 128 B apart.
+  const int kx = swz(l32);
+  int koff[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) koff[m] = l32 * 1024 + 16 * ((2 * m + hsel) ^ kx);
   // V^T fragment via transposing reads: in lane group q = lane/16, lane
-  // 4j + a addresses row tp*32 + 16 k2 + 4 (q>>1) + j (+8 for the upper
-  // half of k) and dv 32 vt + 16 (q&1) + 4a, i.e. chunk 4 vt + vw.
+  // 4j + a addresses row 16 k2 + 4 (q>>1) + j (+8 for the upper half of
+  // k) and latent column 128 wave + 32 dt + 16 (q&1) + 4a.
   const int q4 = lane >> 4, ja = lane & 15;
   const int vj = ja >> 2, va = ja & 3;
-  const int vrow = tp * TPW + 4 * (q4 >> 1) + vj;
+  const int vrow = 4 * (q4 >> 1) + vj;
   const int vw = 2 * (q4 & 1) + (va >> 1);
-  const int v_off_e = vrow * 1024 + 16 * (vw ^ swz(vrow)) + 8 * (va & 1);
-  const int v_off_o = vrow * 1024 + 16 * ((vw + 4) ^ swz(vrow)) + 8 * (va & 1);
+  const int v_base = vrow * 1024 + 256 * wave + 8 * (va & 1);
+  const int v_off_e = v_base + 16 * (vw ^ swz(vrow));
+  const int v_off_o = v_base + 16 * ((vw + 4) ^ swz(vrow));
 
-  f32x16 acc[VT];
+  // Value role accumulators: head group g, latent tile dt of this wave.
+  f32x16 acc[NWAVES][VTW];
 #pragma unroll
-  for (int i = 0; i < VT; ++i) acc[i] = f32x16{};
+  for (int g = 0; g < NWAVES; ++g)
+#pragma unroll
+    for (int dt = 0; dt < VTW; ++dt) acc[g][dt] = f32x16{};
   float m_run = -1e30f, l_run = 0.f;
 
-  for (int blk = 0; blk < nblk; ++blk) {
-    wait_stages<C::LPW, C::NS>(min(C::NS - 2, nblk - 1 - blk));
-    __syncthreads();  // stage blk visible to all waves; stage blk-1 free
-    if (blk + C::NS - 1 < nblk)
-      issue_stage<NTP>(kvb, t0 + (blk + C::NS - 1) * C::BT, t1, lds0 + ((blk + C::NS - 1) % C::NS) * C::STAGE_B,
-                       wave, lane);
-    const unsigned char* st = smem + (blk % C::NS) * C::STAGE_B;
-
-    // ---- S^T (32 tokens x 32 heads) ----
-    f32x16 sc = f32x16{};
-    {
-      u32x4 kf[4];
+  // ---- scores of stage si for head group `wave`, then the online softmax;
+  // P^T (bf16, B-operand layout, k order: tokens 4 hsel + j then
+  // 8 + 4 hsel + j), the rescale flag and factors go to buffer si&1 ----
+  auto scores = [&](int si) {
+    const unsigned char* lat = smem + (si & (NLAT - 1)) * LAT_B;
+    const unsigned char* rope = smem + ROPE_OFF + (si % NROPE) * ROPE_B - l32 * (1024 - 128);
+    auto kread = [&](int ks) {
+      return ks < 32 ? ld128(lat + koff[ks & 3] + 128 * (ks >> 2)) : ld128(rope + koff[ks & 3]);
+    };
+    // K reads run KLA k-steps ahead of the MFMAs; two accumulation chains.
+    constexpr int KLA = 6;
+    f32x16 sa = f32x16{}, sb = f32x16{};
+    u32x4 kf[8];
 #pragma unroll
-      for (int ks = 0; ks < 3; ++ks) kf[ks] = kread(st, ks);
+    for (int ks = 0; ks < KLA; ++ks) kf[ks] = kread(ks);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 3 < KS) kf[(ks + 3) & 3] = kread(st, ks + 3);
-        sc = mfma32<BF16>(kf[ks & 3], qf[ks], sc);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + KLA < KS) kf[(ks + KLA) & 7] = kread(ks + KLA);
+      if (ks & 1)
+        sb = mfma32<BF16>(kf[ks & 7], qf[ks], sb);
+      else
+        sa = mfma32<BF16>(kf[ks & 7], qf[ks], sa);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    f32x16 sc = sa + sb;
 
-    // ---- online softmax over this wave's 32 tokens ----
-    // lane holds head `head`, tokens tb + 8 i + 4 hsel + j for sc[4 i + j]
-    const int tb = t0 + blk * C::BT + tp * TPW;
-    const bool need_mask = tb + TPW > t1;
+    // lane holds head l32, tokens tb + 8 i + 4 hsel + j for sc[4 i + j]
+    const int tb = t0 + si * BT;
+    const bool need_mask = tb + BT > t1;
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -258,179 +245,207 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
       mx = fmaxf(mx, x);
     }
     mx = max_xor32(mx);
+    int* flags = reinterpret_cast<int*>(smem + F_OFF) + (si & 1) * NWAVES;
+    float* corrs = reinterpret_cast<float*>(smem + C_OFF) + ((si & 1) * NWAVES + wave) * 32;
+    int flag = 0;
     if (__any(mx > m_run + kLazy)) {
       const float m_new = fmaxf(m_run, mx);
       const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= corr;
-#pragma unroll
-      for (int vt = 0; vt < VT; ++vt) scale_acc(acc[vt], corr);
+      if (hsel == 0) corrs[l32] = corr;
+      flag = si > 0;  // at stage 0 the value accumulators are still zero
     }
-    u32x4 pf[2];
+    if (lane == 0) flags[wave] = flag;
+    u32x4* pbuf = reinterpret_cast<u32x4*>(smem + P_OFF + (si & 1) * P_BUF);
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
       float p[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(sc[8 * k2 + e] - m_run);
-      pf[k2] = u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+      const u32x4 pf{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                      pack_bf16x2(p[6], p[7])};
 #pragma unroll
-      for (int w = 0; w < 4; ++w) l_run = dot2_ones<BF16>(pf[k2][w], l_run);
+      for (int w = 0; w < 4; ++w) l_run = dot2_ones<BF16>(pf[w], l_run);
+      pbuf[(wave * 2 + k2) * 64 + lane] = pf;
     }
+  };
 
-    // ---- O^T += V^T . P^T  (k order: tokens 4 hsel + j, then 8 + 4 hsel + j) ----
+  // ---- values of stage pi: O^T[128 wave + 32 dt .., heads] += V^T . P^T ----
+  auto values = [&](int pi) {
+#pragma unroll
+    for (int g = 0; g < NWAVES; ++g) {
+      const int f = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int*>(smem + F_OFF)[(pi & 1) * NWAVES + g]);
+      if (f) {
+        const float c = reinterpret_cast<const float*>(smem + C_OFF)[((pi & 1) * NWAVES + g) * 32 + l32];
+#pragma unroll
+        for (int dt = 0; dt < VTW; ++dt) scale_acc(acc[g][dt], c);
+      }
+    }
+    const unsigned char* lat = smem + (pi & (NLAT - 1)) * LAT_B;
+    const u32x4* pbuf = reinterpret_cast<const u32x4*>(smem + P_OFF + (pi & 1) * P_BUF);
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
-      const unsigned char* vb = st + 16 * k2 * 1024;
-      auto vread = [&](int vt) {
-        const unsigned char* p = vb + ((vt & 1) ? v_off_o : v_off_e) + 128 * (vt >> 1);
+      const unsigned char* vb = lat + 16 * k2 * 1024;
+      u32x4 vf[VTW];
+#pragma unroll
+      for (int dt = 0; dt < VTW; ++dt) {
+        const unsigned char* p = vb + ((dt & 1) ? v_off_o : v_off_e) + 128 * (dt >> 1);
         const u32x2 lo = lds_read_tr16(p);
         const u32x2 hi = lds_read_tr16(p + 8 * 1024);
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
-      };
-      u32x4 vf[3];
-      vf[0] = vread(0);
-      vf[1] = vread(1);
+        vf[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+      u32x4 pb[2];
+      pb[0] = pbuf[k2 * 64 + lane];
 #pragma unroll
-      for (int vt = 0; vt < VT; ++vt) {
-        if (vt + 2 < VT) vf[(vt + 2) % 3] = vread(vt + 2);
-        acc[vt] = mfma32<BF16>(vf[vt % 3], pf[k2], acc[vt]);
+      for (int g = 0; g < NWAVES; ++g) {
+        if (g + 1 < NWAVES) pb[(g + 1) & 1] = pbuf[((g + 1) * 2 + k2) * 64 + lane];
+#pragma unroll
+        for (int dt = 0; dt < VTW; ++dt) acc[g][dt] = mfma32<BF16>(vf[dt], pb[g & 1], acc[g][dt]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-  }
+  };
 
-  float l_tot = sum_xor32(l_run);
-
-  if constexpr (NTP > 1) {
-    // Merge the token parts of each head group through LDS (the ring is
-    // free once every wave is past its last stage).
-    static_assert(NTP == 2, "two token parts");
-    __syncthreads();
-    float* xo = reinterpret_cast<float*>(smem) + hgi * (VT * 16 * 64);
-    float* xml = reinterpret_cast<float*>(smem) + C::NHG * VT * 16 * 64 + hgi * 128;
-    if (tp == 1) {
-#pragma unroll
-      for (int vt = 0; vt < VT; ++vt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) xo[(vt * 16 + e) * 64 + lane] = acc[vt][e];
-      xml[lane] = m_run;
-      xml[64 + lane] = l_tot;
+  // Iteration i: scores of stage i and values of stage i-1 (either order
+  // per wave).  Slot reuse: stage i+2 overwrites latent slot (i+2)%4
+  // (stage i-2, whose values finished before this iteration's barrier) and
+  // rope slot (i+2)%3 (stage i-1, whose scores did); the P^T/flag buffers
+  // alternate by stage.
+  auto sync = [&](int i) {
+    if (i + 1 < nblk)
+      wait_vmcnt<LPW>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();  // stage i landed for all waves; P^T of stage i-1 visible
+    if (i + 2 < nblk) issue(i + 2);
+  };
+  if (wave & 1) {
+    sync(0);
+    scores(0);
+    for (int i = 1; i < nblk; ++i) {
+      sync(i);
+      values(i - 1);
+      scores(i);
     }
-    __syncthreads();
-    if (tp == 1) return;
-    const float m_o = xml[lane], l_o = xml[64 + lane];
-    const float m_new = fmaxf(m_run, m_o);
-    const float ws = __builtin_amdgcn_exp2f(m_run - m_new), wo = __builtin_amdgcn_exp2f(m_o - m_new);
-#pragma unroll
-    for (int vt = 0; vt < VT; ++vt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[vt][e] = acc[vt][e] * ws + xo[(vt * 16 + e) * 64 + lane] * wo;
-    l_tot = l_tot * ws + l_o * wo;
-    m_run = m_new;
+  } else {
+    sync(0);
+    scores(0);
+    for (int i = 1; i < nblk; ++i) {
+      sync(i);
+      scores(i);
+      values(i - 1);
+    }
   }
+  sync(nblk);
+  values(nblk - 1);
 
-  // lane holds head `head`, dv = 32 vt + 8 i + 4 hsel + j for acc[vt][4 i + j]
-  if (nsplit == 1) {
-    if (!head_ok) return;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    uint16_t* orow = O + ((size_t)b * H + head) * DV + 4 * hsel;
-#pragma unroll
-    for (int vt = 0; vt < VT; ++vt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        st64(orow + 32 * vt + 8 * i, u32x2{pack_bf16x2(acc[vt][4 * i] * inv, acc[vt][4 * i + 1] * inv),
-                                           pack_bf16x2(acc[vt][4 * i + 2] * inv, acc[vt][4 * i + 3] * inv)});
-    return;
-  }
-  // Partials, lane-major: ws_o[((b * nsplit + s) * HW + hw) * 64 (vt, i) slots][lane] as float4.
+  // Row sums to the value waves; (m, l) of each split to the workspace.
+  const float l_tot = sum_xor32(l_run);
+  float* lsum = reinterpret_cast<float*>(smem + L_OFF);
+  if (hsel == 0) lsum[wave * 32 + l32] = l_tot;
   const int HW = (H + HPW - 1) / HPW;
-  if (hw >= HW) return;  // a wave whose 32 heads are all padding
-  float* po = ws_o + (((size_t)b * nsplit + s) * HW + hw) * (VT * 4 * 64 * 4);
-#pragma unroll
-  for (int vt = 0; vt < VT; ++vt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<f32x4*>(po + ((vt * 4 + i) * 64 + lane) * 4) =
-          f32x4{acc[vt][4 * i], acc[vt][4 * i + 1], acc[vt][4 * i + 2], acc[vt][4 * i + 3]};
-  if (hsel == 0) {
-    float* pml = ws_ml + (((size_t)b * nsplit + s) * HW + hw) * 64 + 2 * l32;
+  if (nsplit > 1 && hgb * NWAVES + wave < HW && hsel == 0) {
+    float* pml = ws_ml + (((size_t)b * nsplit + s) * HW + hgb * NWAVES + wave) * 64 + 2 * l32;
     *reinterpret_cast<float2*>(pml) = float2{m_run, l_tot};
   }
+  __syncthreads();
+
+  // lane holds head hgb*128 + 32 g + l32, latent column 128 wave + 32 dt + 8 i + 4 hsel + j
+#pragma unroll
+  for (int g = 0; g < NWAVES; ++g) {
+    const int hw = hgb * NWAVES + g;
+    if (hw >= HW) break;  // the remaining head groups are all padding
+    const float l = lsum[g * 32 + l32];
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    if (nsplit == 1) {
+      const int head = hw * HPW + l32;
+      if (head < H) {
+        uint16_t* orow = O + ((size_t)b * H + head) * DV + 128 * wave + 4 * hsel;
+#pragma unroll
+        for (int dt = 0; dt < VTW; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x16& a = acc[g][dt];
+            st64(orow + 32 * dt + 8 * i, u32x2{pack_bf16x2(a[4 * i] * inv, a[4 * i + 1] * inv),
+                                               pack_bf16x2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)});
+          }
+      }
+    } else {
+      uint32_t* po = ws_o + (((size_t)b * nsplit + s) * HW + hw) * PT_U32;
+#pragma unroll
+      for (int dt = 0; dt < VTW; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x16& a = acc[g][dt];
+          const int slot = (wave * VTW + dt) * 4 + i;
+          st64(po + (slot * 64 + lane) * 2, u32x2{pack_bf16x2(a[4 * i] * inv, a[4 * i + 1] * inv),
+                                                  pack_bf16x2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)});
+        }
+    }
+  }
 }
 
-// Merge the per-split softmax states:  o = sum_s w_s o_s / sum_s w_s l_s,
-// w_s = 2^(m_s - max_s m_s).  One workgroup per (b, 32-head group); wave w
-// merges dv tiles 4w .. 4w+3 in the lane-major partial layout.
-__global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restrict__ ws_o,
-                                                         const float* __restrict__ ws_ml,
-                                                         uint16_t* __restrict__ O, int H, int nsplit) {
+// Merge the per-split softmax states:  o = sum_s w_s o_s / sum_s w_s,
+// w_s = l_s 2^(m_s - max_s m_s), o_s the normalised split output.  One
+// thread per 4 latent columns of a (b, 32-head group) tile (4096 of them,
+// 16 workgroups of 256), so the merge spreads over the whole GPU; the
+// split loop is batched for memory parallelism.
+constexpr int CMB_WG = 256;
+constexpr int CMB_PER = VT * 4 * 64 / CMB_WG;  // workgroups per (b, 32-head group) = 16
+
+__global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __restrict__ ws_o,
+                                                            const float* __restrict__ ws_ml,
+                                                            uint16_t* __restrict__ O, int H, int nsplit) {
   const int HW = (H + HPW - 1) / HPW;
-  const int b = blockIdx.x / HW, hw = blockIdx.x % HW;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int gi = blockIdx.x / CMB_PER;          // b * HW + hw
+  const int part = blockIdx.x % CMB_PER;
+  const int b = gi / HW, hw = gi % HW;
+  const int idx = part * CMB_WG + threadIdx.x;  // slot * 64 + lane
+  const int lane = idx & 63, slot = idx >> 6;
   const int l32 = lane & 31, hsel = lane >> 5;
   const int head = hw * HPW + l32;
+  const size_t g0 = (size_t)b * nsplit * HW + hw;  // tile of split 0; split stride HW
+  const float* ml = ws_ml + g0 * 64 + 2 * l32;
   float mmax = -1e30f;
-  for (int s = 0; s < nsplit; ++s)
-    mmax = fmaxf(mmax, ws_ml[(((size_t)b * nsplit + s) * HW + hw) * 64 + 2 * l32]);
-  f32x4 o[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) o[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < nsplit; ++s) mmax = fmaxf(mmax, ml[(size_t)s * HW * 64]);
+  f32x4 o{0.f, 0.f, 0.f, 0.f};
   float l = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const size_t g = ((size_t)b * nsplit + s) * HW + hw;
-    const float2 ml = *reinterpret_cast<const float2*>(ws_ml + g * 64 + 2 * l32);
-    const float w = __builtin_amdgcn_exp2f(ml.x - mmax);
-    l = fmaf(w, ml.y, l);
-    const float* po = ws_o + g * (VT * 4 * 64 * 4) + (size_t)wave * 16 * 64 * 4;
+  const uint32_t* po = ws_o + g0 * PT_U32 + (size_t)idx * 2;
+  const size_t sstride = (size_t)HW * PT_U32;
+  auto acc1 = [&](const u32x2 p, const float2 mlv) {
+    const float w = mlv.y * __builtin_amdgcn_exp2f(mlv.x - mmax);
+    l += w;
+    o += w * f32x4{bf16_bits_to_f32(p[0] & 0xffffu), bf16_bits_to_f32(p[0] >> 16), bf16_bits_to_f32(p[1] & 0xffffu),
+                   bf16_bits_to_f32(p[1] >> 16)};
+  };
+  // Eight splits per batch of loads: all independent, issued together.
+  int s = 0;
+  for (; s + 8 <= nsplit; s += 8) {
+    u32x2 p[8];
+    float2 mlv[8];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) o[k] += w * *reinterpret_cast<const f32x4*>(po + (k * 64 + lane) * 4);
+    for (int u = 0; u < 8; ++u) {
+      p[u] = ld64(po + (size_t)(s + u) * sstride);
+      mlv[u] = *reinterpret_cast<const float2*>(ml + (size_t)(s + u) * HW * 64);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc1(p[u], mlv[u]);
   }
+  for (; s < nsplit; ++s)
+    acc1(ld64(po + (size_t)s * sstride), *reinterpret_cast<const float2*>(ml + (size_t)s * HW * 64));
   if (head >= H) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t* orow = O + ((size_t)b * H + head) * DV + 4 * hsel;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int vt = wave * 4 + k / 4, i = k % 4;
-    st64(orow + 32 * vt + 8 * i,
-         u32x2{pack_bf16x2(o[k][0] * inv, o[k][1] * inv), pack_bf16x2(o[k][2] * inv, o[k][3] * inv)});
-  }
+  const int vt = slot >> 2, i = slot & 3;
+  st64(O + ((size_t)b * H + head) * DV + 32 * vt + 8 * i + 4 * hsel,
+       u32x2{pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)});
 }
-
-// Token parts per head group: two (64-token stages, 64 heads per
-// workgroup) when the heads alone give at least two 64-head groups per
-// sequence, which halves the split partials; one otherwise.
-inline int pick_ntp(int H) { return H >= 128 ? 2 : 1; }
 
 inline size_t workspace_bytes(int B, int H, int T) {
-  const Split sp = pick_ntp(H) == 2 ? pick_split<2>(B, H, T) : pick_split<1>(B, H, T);
+  const Split sp = pick_split(B, H, T);
   if (sp.nsplit <= 1) return 0;
   const size_t HW = (size_t)(H + HPW - 1) / HPW;
-  return (size_t)B * sp.nsplit * HW * (HPW * DV + 2 * HPW) * sizeof(float);
-}
-
-template <int NTP>
-static int launch(const void* Q, const void* KV, void* O, int B, int H, int T, float sl2, void* workspace,
-                  hipStream_t s) {
-  using C = Cfg<NTP>;
-  const Split sp = pick_split<NTP>(B, H, T);
-  const int HGB = (H + C::HPG - 1) / C::HPG;
-  const long long grid = (long long)B * HGB * sp.nsplit;
-  if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
-  const size_t HW = (size_t)(H + HPW - 1) / HPW;
-  float* ws_o = (float*)workspace;
-  float* ws_ml = sp.nsplit > 1 ? ws_o + (size_t)B * sp.nsplit * HW * HPW * DV : nullptr;
-  MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)mla_decode_kernel<NTP>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
-  hipLaunchKernelGGL(mla_decode_kernel<NTP>, dim3((unsigned)grid), dim3(NT), LDS_BYTES, s, (const uint16_t*)Q,
-                     (const uint16_t*)KV, (uint16_t*)O, ws_o, ws_ml, B, H, T, sl2, sp.nsplit, sp.tps);
-  MX_RETURN_IF_HIP(hipGetLastError());
-  if (sp.nsplit > 1) {
-    hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)(B * HW)), dim3(256), 0, s, ws_o, ws_ml, (uint16_t*)O, H,
-                       sp.nsplit);
-    MX_RETURN_IF_HIP(hipGetLastError());
-  }
-  return MX_OK;
+  return (size_t)B * sp.nsplit * HW * (PT_U32 * sizeof(uint32_t) + 2 * HPW * sizeof(float));
 }
 
 }  // namespace mla
@@ -454,7 +469,22 @@ extern "C" int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int 
   if (need > 0 && (!workspace || ws_bytes < need)) return MX_ERR_WORKSPACE;
   if (need > 0 && ((uintptr_t)workspace & 15)) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  const float sl2 = scale * kLog2e;
-  if (pick_ntp(H) == 2) return launch<2>(Q, KV, O, B, H, T, sl2, workspace, s);
-  return launch<1>(Q, KV, O, B, H, T, sl2, workspace, s);
+  const Split sp = pick_split(B, H, T);
+  const long long HGB = (H + HPG - 1) / HPG;
+  const long long HW = (H + HPW - 1) / HPW;
+  const long long grid = (long long)B * HGB * sp.nsplit;
+  if (grid > 0x7fffffffLL || (long long)B * HW * CMB_PER > 0x7fffffffLL) return MX_ERR_SHAPE;
+  uint32_t* ws_o = (uint32_t*)workspace;
+  float* ws_ml = sp.nsplit > 1 ? reinterpret_cast<float*>(ws_o + (size_t)B * sp.nsplit * HW * PT_U32) : nullptr;
+  MX_RETURN_IF_HIP(
+      hipFuncSetAttribute((const void*)mla_decode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
+  hipLaunchKernelGGL(mla_decode_kernel, dim3((unsigned)grid), dim3(NT), LDS_BYTES, s, (const uint16_t*)Q,
+                     (const uint16_t*)KV, (uint16_t*)O, ws_o, ws_ml, B, H, T, scale * kLog2e, sp.nsplit, sp.tps);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  if (sp.nsplit > 1) {
+    hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)(B * HW * CMB_PER)), dim3(CMB_WG), 0, s, ws_o, ws_ml,
+                       (uint16_t*)O, H, sp.nsplit);
+    MX_RETURN_IF_HIP(hipGetLastError());
+  }
+  return MX_OK;
 }
