@@ -31,8 +31,9 @@
 #include "mx_common.h"
 
 // Query tiles (of 32) per wave.  1 keeps two waves per SIMD (the pair hides
-// each other's softmax / LDS latency); 2 halves LDS reads per FLOP but needs
-// about 512 registers and currently spills, so it is not the default.
+// each other's softmax and LDS latency); 2 halves LDS fragment reads per
+// FLOP (each K and V fragment feeds two MFMAs) but runs one wave per SIMD
+// and is slower on MI355X, so it is not the default.
 #ifndef MX_GQA_QT
 #define MX_GQA_QT 1
 #endif
@@ -46,20 +47,26 @@ constexpr int NT = 64 * NWAVES;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 
-// LDS tiles are row-major copies of the K and V tiles ([BN keys][D]) with
-// padded rows, so every fragment read of a lane is its base address plus a
-// compile-time immediate and no read phase repeats a bank: K rows carry 16
-// extra bytes (16-lane phases of 16-byte reads hit 16 distinct bank groups),
-// V rows 64 (the 32-lane phases of the 8-byte transposing reads, 4 rows x 2
-// column groups x 4 lanes, hit 32 distinct 8-byte slots).
+// Chunk position of 16-byte chunk c in row r: c ^ swz(r).  swz maps r%8 to
+// 0,2,4,6,1,3,5,7: distinct over 8 consecutive rows (K fragment reads: 8
+// lanes, 8 keys, one chunk) and with distinct halves over an aligned group
+// of 4 rows (transposing V reads: 4 keys x two adjacent chunks), so both
+// read patterns are bank-conflict free on unpadded 128/256-byte rows.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// One stage = K tile then V tile, [BN keys][D] each, unpadded swizzled rows.
 template <int D>
 struct Lds {
-  static constexpr int K_ROW = D * 2 + 16;
-  static constexpr int V_ROW = D * 2 + 64;
-  static constexpr int K_BYTES = BN * K_ROW;
-  static constexpr int V_BYTES = BN * V_ROW;
-  static constexpr int STAGE = K_BYTES + V_BYTES;
-  static constexpr int TOTAL = 2 * STAGE;
+  static constexpr int ROW = D * 2;
+  static constexpr int TILE = BN * ROW;
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int RPL = 1024 / ROW;           // rows per 1 KB direct load
+  static constexpr int LPW = STAGE / 1024 / NWAVES;  // direct loads per wave per stage
+};
+
+template <int QT>
+struct Ring {
+  static constexpr int NS = QT == 1 ? 2 : 3;  // stages (QT=1 runs two workgroups per CU)
 };
 
 template <int D, typename T, bool CAUSAL, int QT>
@@ -71,11 +78,12 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   constexpr int QW = 32 * QT;         // queries per wave
   constexpr int DC = D / 16;          // 16-deep k steps of QK^T
   constexpr int DT = D / 32;          // 32-row d tiles of O^T
-  constexpr int K_LD = BN * D / 8 / NT;   // 16-B chunks of K (and of V) per thread
-  static_assert(K_LD >= 1, "K tile split");
-  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NS = Ring<QT>::NS;
+  using L = Lds<D>;
+  extern __shared__ __align__(1024) unsigned char smem[];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5;      // lane half
   const int ql = lane & 31;     // query within a 32-query tile
 
@@ -99,20 +107,18 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 
   const size_t q_head = ((size_t)b * Hq + head) * S;
   const size_t kv_head = ((size_t)b * Hkv + kvh) * S;
-  const uint16_t* Kh = K + kv_head * D;
-  const uint16_t* Vh = V + kv_head * D;
+  const unsigned char* Kh = reinterpret_cast<const unsigned char*>(K + kv_head * D);
+  const unsigned char* Vh = reinterpret_cast<const unsigned char*>(V + kv_head * D);
 
-  // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole loop ----
+  // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole loop.
+  // Rows past S read row S-1; their outputs are never stored. ----
   int qrow[QT];
   u32x4 qf[QT][DC];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     qrow[qt] = q0w + 32 * qt + ql;
 #pragma unroll
-    for (int dc = 0; dc < DC; ++dc) {
-      const u32x4 x = ld128(Q + (q_head + min(qrow[qt], S - 1)) * D + dc * 16 + g * 8);
-      qf[qt][dc] = (qrow[qt] < S) ? x : u32x4{0, 0, 0, 0};
-    }
+    for (int dc = 0; dc < DC; ++dc) qf[qt][dc] = ld128(Q + (q_head + min(qrow[qt], S - 1)) * D + dc * 16 + g * 8);
   }
 
   // ---- kv range ----
@@ -120,48 +126,46 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   const int nblk = (kv_end_wg + BN - 1) / BN;
   const int kv_end_w = CAUSAL ? min(S, q0w + QW) : S;
 
-  // ---- global -> register staging: K and V tiles row-major, 16-byte
-  // chunks, chunk q = tid + i*NT -> row q / (D/8), chunk q % (D/8) ----
-  constexpr int DB = D / 8;
-  u32x4 rk[K_LD], rv[K_LD];
-
-  auto load_kv = [&](int kv0) {
-    if (kv0 + BN <= S) {  // uniform: every tile but a ragged last one
+  // ---- HBM -> LDS with direct loads: wave load n of a stage fills rows
+  // RPL*n .. RPL*n+RPL-1 of the K tile (n < BN/RPL) or of the V tile; lane i
+  // takes row RPL*n + i/(D/8), chunk (i%(D/8)) ^ swz(row).  Rows past S
+  // re-read row S-1 (finite data that the mask or a zero P cancels). ----
+  const uint32_t lds0 = lds_addr(smem);
+  const int l_row = lane / (D / 8);
+  const int l_pos = lane % (D / 8);
+  auto issue = [&](int blk) {
+    const int kv0 = blk * BN;
+    const uint32_t st = lds0 + (blk % NS) * L::STAGE;
 #pragma unroll
-      for (int i = 0; i < K_LD; ++i) {
-        const int q = tid + i * NT;
-        const size_t off = (size_t)(kv0 + q / DB) * D + (q % DB) * 8;
-        rk[i] = ld128(Kh + off);
-        rv[i] = ld128(Vh + off);
-      }
-    } else {
-      // rows past S are read from row S-1 (in bounds) and zeroed
-#pragma unroll
-      for (int i = 0; i < K_LD; ++i) {
-        const int q = tid + i * NT;
-        const int kv = kv0 + q / DB;
-        const size_t off = (size_t)min(kv, S - 1) * D + (q % DB) * 8;
-        const u32x4 xk = ld128(Kh + off), xv = ld128(Vh + off);
-        rk[i] = (kv < S) ? xk : u32x4{0, 0, 0, 0};
-        rv[i] = (kv < S) ? xv : u32x4{0, 0, 0, 0};
-      }
+    for (int n = 0; n < L::LPW; ++n) {
+      const int ld = wave * L::LPW + n;                  // 0 .. 2*BN/RPL - 1
+      const int tile = ld / (BN / L::RPL);               // 0 = K, 1 = V
+      const int r = (ld % (BN / L::RPL)) * L::RPL + l_row;
+      const int kv = min(kv0 + r, S - 1);
+      const uint32_t off = (uint32_t)kv * L::ROW + 16 * (l_pos ^ swz(r));
+      dma16(tile ? Vh : Kh, off, st + ld * 1024);
     }
   };
-  auto store_kv = [&](int stage) {
-    unsigned char* sk = smem + stage * Lds<D>::STAGE;
-    unsigned char* sv = sk + Lds<D>::K_BYTES;
+  issue(0);
+  wait_vmcnt<0>();  // the Q loads and stage 0 complete together
 #pragma unroll
-    for (int i = 0; i < K_LD; ++i) {
-      const int q = tid + i * NT;
-      *reinterpret_cast<u32x4*>(sk + (q / DB) * Lds<D>::K_ROW + (q % DB) * 16) = rk[i];
-      *reinterpret_cast<u32x4*>(sv + (q / DB) * Lds<D>::V_ROW + (q % DB) * 16) = rv[i];
-    }
-  };
+  for (int p = 1; p < NS - 1; ++p)
+    if (p < nblk) issue(p);
 
-  // Transposed V fragment addressing: lane (half g, sub-group sg, 4j+a)
-  // reads key 16c + 8r + 4g + j at column 32dt + 16sg + 4a.
+  // K fragment (A operand of S^T): key row 32t + ql, chunk 2dc + g at
+  // position 8 (dc/4) + ((2 (dc%4) + g) ^ swz(ql)): four lane offsets plus
+  // an immediate per (t, dc).
+  int koff[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) koff[m] = ql * L::ROW + 16 * ((2 * m + g) ^ swz(ql));
+  // Transposed V fragment: lane (half g, sub-group sg, 4j+a) reads key
+  // 16c + 8r + 4g + j at column 32dt + 16sg + 4a, i.e. chunk 4dt + 2sg +
+  // a/2 of a row whose swizzle is swz(4g + j).
   const int v_sg = (lane >> 4) & 1, v_j = (lane >> 2) & 3, v_a = lane & 3;
-  const int v_lane_off = (4 * g + v_j) * Lds<D>::V_ROW + (16 * v_sg + 4 * v_a) * 2;
+  const int vrow = 4 * g + v_j;
+  const int vw = 2 * v_sg + (v_a >> 1);
+  const int v_off_e = L::TILE + vrow * L::ROW + 16 * ((vw ^ swz(vrow)) & 7) + 8 * (v_a & 1);
+  const int v_off_o = L::TILE + vrow * L::ROW + 16 * (((vw + 4) ^ swz(vrow)) & 7) + 8 * (v_a & 1);
 
   f32x16 acc_o[QT][DT];
   float m_run[QT], l_run[QT];
@@ -173,31 +177,34 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
     l_run[qt] = 0.f;
   }
 
-  if (nblk > 0) {
-    load_kv(0);
-    store_kv(0);
-  }
-  __syncthreads();
-
   for (int blk = 0; blk < nblk; ++blk) {
-    const int cur = blk & 1;
+    // stage blk landed (this wave's loads), then visible to all waves;
+    // the stage read in iteration blk-1 is free for stage blk+NS-1.
+    if constexpr (NS == 3) {
+      if (blk + 1 < nblk)
+        wait_vmcnt<L::LPW>();
+      else
+        wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();
+    if (blk + NS - 1 < nblk) issue(blk + NS - 1);
     const int kv0 = blk * BN;
-    if (blk + 1 < nblk) load_kv(kv0 + BN);
 
     if (kv0 < kv_end_w) {
-      const unsigned char* sk = smem + cur * Lds<D>::STAGE;
-      const unsigned char* sv = sk + Lds<D>::K_BYTES;
+      const unsigned char* st = smem + (blk % NS) * L::STAGE;
 
       // ---- S^T tiles: rows = keys (2 x 32), cols = queries (QT x 32) ----
       // 2*QT independent accumulator chains; each K fragment feeds QT
       // MFMAs and is read KLA k-steps ahead of its use.
       auto kread = [&](int t, int dc) {
-        return *reinterpret_cast<const u32x4*>(sk + (t * 32 + ql) * Lds<D>::K_ROW + (dc * 2 + g) * 16);
+        return ld128(st + t * 32 * L::ROW + koff[dc & 3] + 128 * (dc >> 2));
       };
       f32x16 s[QT][2];
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) s[qt][0] = s[qt][1] = f32x16{};
-      constexpr int KLA = (QT == 1) ? 2 : 1;  // read lookahead (k-steps)
+      constexpr int KLA = 2;  // read lookahead (k-steps)
       u32x4 kb[KLA + 1][2];
 #pragma unroll
       for (int i = 0; i < KLA; ++i) {
@@ -220,9 +227,9 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       // V fragments of the first key chunk do not depend on the softmax:
       // issue them now so their latency hides under the VALU work below.
       auto vread = [&](int c, int dt) {
-        const unsigned char* vb = sv + v_lane_off + (16 * c) * Lds<D>::V_ROW + dt * 64;
+        const unsigned char* vb = st + ((dt & 1) ? v_off_o : v_off_e) + 128 * (dt >> 1) + (16 * c) * L::ROW;
         const u32x2 lo = lds_read_tr16(vb);
-        const u32x2 hi = lds_read_tr16(vb + 8 * Lds<D>::V_ROW);
+        const u32x2 hi = lds_read_tr16(vb + 8 * L::ROW);
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4 vb[2][DT];
@@ -259,7 +266,12 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
           m_run[qt] = m_new;
           l_run[qt] *= corr;
 #pragma unroll
-          for (int i = 0; i < DT; ++i) acc_o[qt][i] *= corr;
+          for (int i = 0; i < DT; ++i) {
+            if constexpr (QT == 1)
+              acc_o[qt][i] *= corr;
+            else
+              scale_acc(acc_o[qt][i], corr);
+          }
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -298,9 +310,6 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) l_run[qt] += lsum[qt];
     }
-
-    if (blk + 1 < nblk) store_kv(cur ^ 1);
-    __syncthreads();
   }
 
   // ---- normalise and store: lane holds query qrow, d = 32dt + 8i + 4g + j ----
@@ -333,8 +342,8 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
   if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
   auto kern = gqa_fwd_kernel<D, T, CAUSAL, QT>;
   MX_RETURN_IF_HIP(
-      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Lds<D>::TOTAL));
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), Lds<D>::TOTAL, stream, (const uint16_t*)Q,
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Ring<QT>::NS * Lds<D>::STAGE));
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), Ring<QT>::NS * Lds<D>::STAGE, stream, (const uint16_t*)Q,
                      (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, B, Hq, Hkv, S, scale * kLog2e, hpw);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;

@@ -77,20 +77,6 @@ static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 // both read patterns are bank-conflict free on 1024 B and 128 B rows.
 __device__ __forceinline__ int swz(int t) { return ((t & 3) << 1) | ((t >> 2) & 1); }
 
-// acc *= c for an accumulator held in AGPRs: read, multiply, write back one
-// register at a time (VALU cannot read AGPRs), without ever materialising
-// the whole tile in VGPRs.
-__device__ __forceinline__ void scale_acc(f32x16& acc, float c) {
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    float x = acc[e], t;
-    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
-                 : "+a"(x), "=&v"(t)
-                 : "v"(c));
-    acc[e] = x;
-  }
-}
-
 struct Split {
   int nsplit;
   int tps;  // tokens per split (multiple of the stage)

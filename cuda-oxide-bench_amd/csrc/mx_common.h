@@ -112,6 +112,20 @@ __device__ __forceinline__ f32x4 mfma16_fp8(const i32x8& a, const i32x8& b, cons
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
+// acc *= c for an accumulator held in AGPRs: read, multiply, write back one
+// register at a time (VALU cannot read AGPRs), without ever materialising
+// the whole tile in VGPRs.
+__device__ __forceinline__ void scale_acc(f32x16& acc, float c) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    float x = acc[e], t;
+    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+                 : "+a"(x), "=&v"(t)
+                 : "v"(c));
+    acc[e] = x;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane reductions inside a wave.
 // ---------------------------------------------------------------------------
