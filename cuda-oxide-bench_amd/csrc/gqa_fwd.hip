@@ -26,8 +26,10 @@
 //    by more than 2^8 (lazy rescale, wave-uniform vote), the scale is folded
 //    into the exp2 argument (one FMA + one exp2 per score), and the row sum
 //    is accumulated with v_dot2 on the rounded P the PV MFMA consumes.
-//  * Causal: workgroups launch heaviest-first; only diagonal / ragged tiles
-//    are masked; tiles entirely above a wave's diagonal are skipped.
+//  * Causal: each workgroup takes a heavy and a light query block (block p
+//    and its mirror nqb-1-p), so all workgroups carry the same number of
+//    key tiles and finish together; only diagonal / ragged tiles are
+//    masked; tiles entirely above a wave's diagonal are skipped.
 #include "mx_common.h"
 
 // Query tiles (of 32) per wave.  1 keeps two waves per SIMD (the pair hides
@@ -94,7 +96,10 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   const int hgroups = G / hpw;
   const int nqb = (S + QB - 1) / QB;
   const int per_q = B * Hkv * hgroups;
-  const int qb = nqb - 1 - (int)(blockIdx.x / per_q);  // heaviest first
+  // Causal: workgroup p takes query block nqb-1-p, then its mirror p, so
+  // every workgroup carries about the same number of key tiles.
+  const int p = (int)(blockIdx.x / per_q);
+  const int nrep = (CAUSAL && nqb - 1 - p != p) ? 2 : 1;
   int rest = blockIdx.x % per_q;
   const int hg = rest % hgroups;
   rest /= hgroups;
@@ -102,13 +107,15 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   const int b = rest / Hkv;
 
   const int head = kvh * G + hg * hpw + (wave % hpw);
-  const int q0w = qb * QB + (wave / hpw) * QW;   // this wave's first query
-  const int q0wg = qb * QB;
-
   const size_t q_head = ((size_t)b * Hq + head) * S;
   const size_t kv_head = ((size_t)b * Hkv + kvh) * S;
   const unsigned char* Kh = reinterpret_cast<const unsigned char*>(K + kv_head * D);
   const unsigned char* Vh = reinterpret_cast<const unsigned char*>(V + kv_head * D);
+
+  for (int rep = 0; rep < nrep; ++rep) {
+  const int qb = CAUSAL ? (rep == 0 ? nqb - 1 - p : p) : p;
+  const int q0w = qb * QB + (wave / hpw) * QW;   // this wave's first query
+  const int q0wg = qb * QB;
 
   // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole loop.
   // Rows past S read row S-1; their outputs are never stored. ----
@@ -146,6 +153,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       dma16(tile ? Vh : Kh, off, st + ld * 1024);
     }
   };
+  if (rep > 0) __syncthreads();  // every wave is done with the previous block's ring
   issue(0);
   wait_vmcnt<0>();  // the Q loads and stage 0 complete together
 #pragma unroll
@@ -330,6 +338,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
         }
     }
   }
+}  // q-block loop
 }
 
 template <int D, typename T, bool CAUSAL, int QT>
@@ -338,7 +347,8 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
   const int G = Hq / Hkv;
   const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
   const int QB = 32 * QT * (NWAVES / hpw);
-  const long long grid = (long long)((S + QB - 1) / QB) * B * Hkv * (G / hpw);
+  const int nqb = (S + QB - 1) / QB;
+  const long long grid = (long long)(CAUSAL ? (nqb + 1) / 2 : nqb) * B * Hkv * (G / hpw);
   if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
   auto kern = gqa_fwd_kernel<D, T, CAUSAL, QT>;
   MX_RETURN_IF_HIP(
