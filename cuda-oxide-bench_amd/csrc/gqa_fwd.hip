@@ -49,12 +49,24 @@ constexpr int NT = 64 * NWAVES;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 
-// Chunk position of 16-byte chunk c in row r: c ^ swz(r).  swz maps r%8 to
-// 0,2,4,6,1,3,5,7: distinct over 8 consecutive rows (K fragment reads: 8
-// lanes, 8 keys, one chunk) and with distinct halves over an aligned group
-// of 4 rows (transposing V reads: 4 keys x two adjacent chunks), so both
-// read patterns are bank-conflict free on unpadded 128/256-byte rows.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// Chunk positions inside LDS rows (16-byte chunk c of row r): K rows hold
+// chunk c at c ^ kswz(r), V rows at c ^ vswz(r).  The LDS serves 256 B per
+// clock (64 banks); a 16-byte read phase is 16 lanes, an 8-byte phase 32.
+//  * K fragment reads: 16 lanes read one chunk of 16 consecutive rows, so
+//    kswz spreads those rows over 16 distinct 16-byte slots (mod 256 B):
+//    r&15 for 256-byte rows, (r>>1)&7 for 128-byte rows (two per 256 B).
+//  * transposing V reads: 32 lanes read 4 consecutive rows x one aligned
+//    quad of chunks (64 B), so vswz gives each of the 4 rows its own quad:
+//    (r&3)<<2 for 256-byte rows, ((r>>1)&1)<<2 for 128-byte rows.  Rows 8
+//    and 16 apart share the swizzle, so fragment offsets stay immediates.
+template <int D>
+__device__ __forceinline__ int kswz(int r) {
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int vswz(int r) {
+  return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
+}
 
 // One stage = K tile then V tile, [BN keys][D] each, unpadded swizzled rows.
 template <int D>
@@ -135,7 +147,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 
   // ---- HBM -> LDS with direct loads: wave load n of a stage fills rows
   // RPL*n .. RPL*n+RPL-1 of the K tile (n < BN/RPL) or of the V tile; lane i
-  // takes row RPL*n + i/(D/8), chunk (i%(D/8)) ^ swz(row).  Rows past S
+  // takes row RPL*n + i/(D/8), chunk (i%(D/8)) ^ k/vswz(row).  Rows past S
   // re-read row S-1 (finite data that the mask or a zero P cancels). ----
   const uint32_t lds0 = lds_addr(smem);
   const int l_row = lane / (D / 8);
@@ -149,7 +161,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       const int tile = ld / (BN / L::RPL);               // 0 = K, 1 = V
       const int r = (ld % (BN / L::RPL)) * L::RPL + l_row;
       const int kv = min(kv0 + r, S - 1);
-      const uint32_t off = (uint32_t)kv * L::ROW + 16 * (l_pos ^ swz(r));
+      const uint32_t off = (uint32_t)kv * L::ROW + 16 * (l_pos ^ (tile ? vswz<D>(r) : kswz<D>(r)));
       dma16(tile ? Vh : Kh, off, st + ld * 1024);
     }
   };
@@ -161,19 +173,20 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
     if (p < nblk) issue(p);
 
   // K fragment (A operand of S^T): key row 32t + ql, chunk 2dc + g at
-  // position 8 (dc/4) + ((2 (dc%4) + g) ^ swz(ql)): four lane offsets plus
-  // an immediate per (t, dc).
-  int koff[4];
+  // position (2dc + g) ^ kswz(ql): one lane offset per dc, t an immediate.
+  int koff[DC];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) koff[m] = ql * L::ROW + 16 * ((2 * m + g) ^ swz(ql));
+  for (int dc = 0; dc < DC; ++dc) koff[dc] = ql * L::ROW + 16 * ((2 * dc + g) ^ kswz<D>(ql));
   // Transposed V fragment: lane (half g, sub-group sg, 4j+a) reads key
   // 16c + 8r + 4g + j at column 32dt + 16sg + 4a, i.e. chunk 4dt + 2sg +
-  // a/2 of a row whose swizzle is swz(4g + j).
+  // a/2 of a row whose swizzle is vswz(4g + j): one lane offset per dt.
   const int v_sg = (lane >> 4) & 1, v_j = (lane >> 2) & 3, v_a = lane & 3;
   const int vrow = 4 * g + v_j;
   const int vw = 2 * v_sg + (v_a >> 1);
-  const int v_off_e = L::TILE + vrow * L::ROW + 16 * ((vw ^ swz(vrow)) & 7) + 8 * (v_a & 1);
-  const int v_off_o = L::TILE + vrow * L::ROW + 16 * (((vw + 4) ^ swz(vrow)) & 7) + 8 * (v_a & 1);
+  int v_off[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    v_off[dt] = L::TILE + vrow * L::ROW + 16 * ((4 * dt + vw) ^ vswz<D>(vrow)) + 8 * (v_a & 1);
 
   f32x16 acc_o[QT][DT];
   float m_run[QT], l_run[QT];
@@ -207,7 +220,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       // 2*QT independent accumulator chains; each K fragment feeds QT
       // MFMAs and is read KLA k-steps ahead of its use.
       auto kread = [&](int t, int dc) {
-        return ld128(st + t * 32 * L::ROW + koff[dc & 3] + 128 * (dc >> 2));
+        return ld128(st + t * 32 * L::ROW + koff[dc]);
       };
       f32x16 s[QT][2];
 #pragma unroll
@@ -235,7 +248,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       // V fragments of the first key chunk do not depend on the softmax:
       // issue them now so their latency hides under the VALU work below.
       auto vread = [&](int c, int dt) {
-        const unsigned char* vb = st + ((dt & 1) ? v_off_o : v_off_e) + 128 * (dt >> 1) + (16 * c) * L::ROW;
+        const unsigned char* vb = st + v_off[dt] + (16 * c) * L::ROW;
         const u32x2 lo = lds_read_tr16(vb);
         const u32x2 hi = lds_read_tr16(vb + 8 * L::ROW);
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
@@ -258,7 +271,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
               const int kv = kv0 + t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-              const bool dead = (kv >= S) || (CAUSAL && kv > qrow[qt]);
+              const bool dead = (kv >= S) | (CAUSAL & (kv > qrow[qt]));
               s[qt][t][e] = dead ? -INFINITY : s[qt][t][e];
             }
         }
@@ -341,6 +354,270 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 }  // q-block loop
 }
 
+// Software-pipelined variant: a wave owns QTP 32-query tiles of one head.
+// Iteration i issues the score MFMAs of tile i+1 interleaved with the
+// softmax VALU work of tile i, then the PV MFMAs of tile i, so the matrix
+// pipe stays busy while the wave computes exponentials.  K and V have
+// separate 2-slot rings: iteration i reads K(i+1) and V(i) and loads K(i+2)
+// and V(i+1) behind them.
+template <int D, typename T, bool CAUSAL, int QTP>
+__global__ __launch_bounds__(NT, QTP == 1 ? 2 : 1) void gqa_fwd_pipe_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    uint16_t* __restrict__ O, int B, int Hq, int Hkv, int S, float sl2, int hpw) {
+  constexpr int QT = QTP;
+  constexpr int QW = 32 * QT;         // queries per wave
+  constexpr int DC = D / 16;          // 16-deep k steps of QK^T
+  constexpr int DT = D / 32;          // 32-row d tiles of O^T
+  using L = Lds<D>;
+  constexpr int TLD = BN / L::RPL / NWAVES;  // direct loads per wave per tile
+  extern __shared__ __align__(1024) unsigned char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;      // lane half
+  const int ql = lane & 31;     // query within a 32-query tile
+
+  const int G = Hq / Hkv;
+  const int qsb = NWAVES / hpw;
+  const int QB = QW * qsb;
+  const int hgroups = G / hpw;
+  const int nqb = (S + QB - 1) / QB;
+  const int per_q = B * Hkv * hgroups;
+  const int p = (int)(blockIdx.x / per_q);
+  const int nrep = (CAUSAL && nqb - 1 - p != p) ? 2 : 1;
+  int rest = blockIdx.x % per_q;
+  const int hg = rest % hgroups;
+  rest /= hgroups;
+  const int kvh = rest % Hkv;
+  const int b = rest / Hkv;
+  const int head = kvh * G + hg * hpw + (wave % hpw);
+  const size_t q_head = ((size_t)b * Hq + head) * S;
+  const size_t kv_head = ((size_t)b * Hkv + kvh) * S;
+  const unsigned char* Kh = reinterpret_cast<const unsigned char*>(K + kv_head * D);
+  const unsigned char* Vh = reinterpret_cast<const unsigned char*>(V + kv_head * D);
+  const uint32_t lds0 = lds_addr(smem);
+  const int l_row = lane / (D / 8);
+  const int l_pos = lane % (D / 8);
+  int koff[DC];
+#pragma unroll
+  for (int dc = 0; dc < DC; ++dc) koff[dc] = ql * L::ROW + 16 * ((2 * dc + g) ^ kswz<D>(ql));
+  const int v_sg = (lane >> 4) & 1, v_j = (lane >> 2) & 3, v_a = lane & 3;
+  const int vrow = 4 * g + v_j;
+  const int vw = 2 * v_sg + (v_a >> 1);
+  int v_off[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) v_off[dt] = vrow * L::ROW + 16 * ((4 * dt + vw) ^ vswz<D>(vrow)) + 8 * (v_a & 1);
+
+  // LDS: K slots 0, 1 then V slots 0, 1, one tile each.
+  auto issue_tile = [&](const unsigned char* src, int blk, int slot) {
+    const int kv0 = blk * BN;
+    const uint32_t st = lds0 + slot * L::TILE;
+#pragma unroll
+    for (int n = 0; n < TLD; ++n) {
+      const int ld = wave * TLD + n;
+      const int r = ld * L::RPL + l_row;
+      const int kv = min(kv0 + r, S - 1);
+      const int sw = (slot >= 2) ? vswz<D>(r) : kswz<D>(r);
+      dma16(src, (uint32_t)kv * L::ROW + 16 * (l_pos ^ sw), st + ld * 1024);
+    }
+  };
+  auto issue_k = [&](int blk) { issue_tile(Kh, blk, blk & 1); };
+  auto issue_v = [&](int blk) { issue_tile(Vh, blk, 2 + (blk & 1)); };
+
+  for (int rep = 0; rep < nrep; ++rep) {
+    const int qb = CAUSAL ? (rep == 0 ? nqb - 1 - p : p) : p;
+    const int q0wg = qb * QB;
+    const int q0w = q0wg + (wave / hpw) * QW;
+    int qrow[QT];
+    u32x4 qf[QT][DC];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      qrow[qt] = q0w + 32 * qt + ql;
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) qf[qt][dc] = ld128(Q + (q_head + min(qrow[qt], S - 1)) * D + dc * 16 + g * 8);
+    }
+    const int kv_end_wg = CAUSAL ? min(S, q0wg + QB) : S;
+    const int nblk = (kv_end_wg + BN - 1) / BN;
+    const int kv_end_w = CAUSAL ? min(S, q0w + QW) : S;
+
+    if (rep > 0) __syncthreads();  // every wave is done with the previous block's rings
+    issue_k(0);
+    issue_v(0);
+    wait_vmcnt<0>();  // the Q loads, K(0) and V(0) complete together
+    if (nblk > 1) issue_k(1);
+
+    f32x16 acc_o[QT][DT];
+    float m_run[QT], l_run[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+      for (int i = 0; i < DT; ++i) acc_o[qt][i] = f32x16{};
+      m_run[qt] = -1e30f;
+      l_run[qt] = 0.f;
+    }
+    f32x16 sc[QT][2];  // scores of tile i
+    f32x16 sn[QT][2];  // scores of tile i+1
+    u32x4 pf[QT][4];   // P^T fragments of tile i, 4 key chunks of 16
+
+    auto kread = [&](int blk, int t, int dc) {
+      return ld128(smem + (blk & 1) * L::TILE + t * 32 * L::ROW + koff[dc]);
+    };
+    // S^T MFMAs of tile blk into dst; `sm(k)` is issued after the k-th
+    // K fragment's MFMAs (2*DC steps).
+    auto scores = [&](int blk, f32x16 (&dst)[QT][2], auto&& sm) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) dst[qt][0] = dst[qt][1] = f32x16{};
+      constexpr int KLA = 2;
+      u32x4 kb[KLA + 1];
+#pragma unroll
+      for (int k = 0; k < KLA; ++k) kb[k] = kread(blk, k & 1, k >> 1);
+#pragma unroll
+      for (int k = 0; k < 2 * DC; ++k) {
+        if (k + KLA < 2 * DC) kb[(k + KLA) % (KLA + 1)] = kread(blk, (k + KLA) & 1, (k + KLA) >> 1);
+        const int t = k & 1, dc = k >> 1;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) dst[qt][t] = mfma32<T>(kb[k % (KLA + 1)], qf[qt][dc], dst[qt][t]);
+        sm(k);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
+    // Softmax of tile blk (scores in sc) in 2*DC steps: steps 0..2QT-1 mask
+    // and reduce the block max of one (qt, t) 16-value group each, step 2QT
+    // finishes the max and the lazy rescale, the remaining steps produce
+    // the exponentials, P^T fragments and row sums one 8-key piece at a time.
+    float mx[QT];
+    float corr[QT];
+    float lsum[QT];
+    auto softmax_step = [&](int blk, int k) {
+      const int kv0 = blk * BN;
+      if (k < 2 * QT) {
+        const int qt = k >> 1, t = k & 1;
+        const bool need_mask = (kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0w + 32 * qt);
+        if (need_mask) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kv = kv0 + t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+            const bool dead = (kv >= S) | (CAUSAL & (kv > qrow[qt]));
+            sc[qt][t][e] = dead ? -INFINITY : sc[qt][t][e];
+          }
+        }
+        float m = (t == 0) ? -INFINITY : mx[qt];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m = fmaxf(m, sc[qt][t][e]);
+        mx[qt] = m;
+      } else if (k == 2 * QT) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const float m = max_xor32(mx[qt]) * sl2;
+          const bool up = __any(m > m_run[qt] + kLazy);
+          const float m_new = up ? fmaxf(m_run[qt], m) : m_run[qt];
+          corr[qt] = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+          m_run[qt] = m_new;
+          l_run[qt] *= corr[qt];
+          lsum[qt] = 0.f;
+        }
+      } else {
+        constexpr int NSTEP = 2 * DC - 2 * QT - 1;
+#pragma unroll
+        for (int piece = 0; piece < QT * 4; ++piece) {
+          if (piece * NSTEP / (QT * 4) != k - 2 * QT - 1) continue;
+          const int qt = piece >> 2, c = piece & 3;
+          const int t = c >> 1, i0 = 2 * (c & 1);
+          float x[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(sc[qt][t][4 * i0 + e], sl2, -m_run[qt]));
+          const u32x4 pv{T::pack2(x[0], x[1]), T::pack2(x[2], x[3]), T::pack2(x[4], x[5]), T::pack2(x[6], x[7])};
+          pf[qt][c] = pv;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) lsum[qt] = dot2_ones<T>(pv[w], lsum[qt]);
+        }
+      }
+    };
+
+    auto vread = [&](int blk, int c, int dt) {
+      const unsigned char* vb = smem + (2 + (blk & 1)) * L::TILE + v_off[dt] + (16 * c) * L::ROW;
+      const u32x2 lo = lds_read_tr16(vb);
+      const u32x2 hi = lds_read_tr16(vb + 8 * L::ROW);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    auto values = [&](int blk) {
+      u32x4 vb[2][DT];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) vb[0][dt] = vread(blk, 0, dt);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (c + 1 < 4) {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) vb[(c + 1) & 1][dt] = vread(blk, c + 1, dt);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) acc_o[qt][dt] = mfma32<T>(vb[c & 1][dt], pf[qt][c], acc_o[qt][dt]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
+    __syncthreads();  // K(0), V(0) visible to all waves
+    if (0 < kv_end_w) scores(0, sc, [](int) {});
+    for (int i = 0; i < nblk; ++i) {
+      // K(i+1) and V(i) landed for all waves; K(i) and V(i-1) slots free
+      wait_vmcnt<0>();
+      __syncthreads();
+      if (i + 2 < nblk) issue_k(i + 2);
+      if (i + 1 < nblk) issue_v(i + 1);
+      const bool do_i = i * BN < kv_end_w;
+      const bool do_n = i + 1 < nblk && (i + 1) * BN < kv_end_w;
+      if (do_n) {
+        scores(i + 1, sn, [&](int k) { softmax_step(i, k); });
+      } else if (do_i) {
+#pragma unroll
+        for (int k = 0; k < 2 * DC; ++k) softmax_step(i, k);
+      }
+      if (do_i) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          if (__any(corr[qt] != 1.f)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+              if constexpr (QT == 1)
+                acc_o[qt][dt] *= corr[qt];
+              else
+                scale_acc(acc_o[qt][dt], corr[qt]);
+            }
+          }
+          l_run[qt] += lsum[qt];
+        }
+        values(i);
+      }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        sc[qt][0] = sn[qt][0];
+        sc[qt][1] = sn[qt][1];
+      }
+    }
+
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float l_tot = sum_xor32(l_run[qt]);
+      const float inv = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
+      if (qrow[qt] < S) {
+        uint16_t* orow = O + (q_head + qrow[qt]) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int d = dt * 32 + 8 * i + 4 * g;
+            const f32x16& a = acc_o[qt][dt];
+            st64(orow + d, u32x2{T::pack2(a[4 * i] * inv, a[4 * i + 1] * inv),
+                                 T::pack2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)});
+          }
+      }
+    }
+  }
+}
+
 template <int D, typename T, bool CAUSAL, int QT>
 static int launch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
                   hipStream_t stream) {
@@ -359,9 +636,39 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
   return MX_OK;
 }
 
+template <int D, typename T, bool CAUSAL, int QTP>
+static int launch_pipe(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
+                       hipStream_t stream) {
+  const int G = Hq / Hkv;
+  const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
+  const int QB = 32 * QTP * (NWAVES / hpw);
+  const int nqb = (S + QB - 1) / QB;
+  const long long grid = (long long)(CAUSAL ? (nqb + 1) / 2 : nqb) * B * Hkv * (G / hpw);
+  if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
+  auto kern = gqa_fwd_pipe_kernel<D, T, CAUSAL, QTP>;
+  constexpr int lds = 4 * Lds<D>::TILE;
+  MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), lds, stream, (const uint16_t*)Q, (const uint16_t*)K,
+                     (const uint16_t*)V, (uint16_t*)O, B, Hq, Hkv, S, scale * kLog2e, hpw);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+#ifndef MX_GQA_PIPE
+#define MX_GQA_PIPE 0
+#endif
+
 template <typename T, int QT>
 static int dispatch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int D,
                     float scale, int causal, hipStream_t s) {
+  if constexpr (MX_GQA_PIPE > 0) {
+    if (D == 128)
+      return causal ? launch_pipe<128, T, true, MX_GQA_PIPE>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
+                    : launch_pipe<128, T, false, MX_GQA_PIPE>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+    if (D == 64)
+      return causal ? launch_pipe<64, T, true, MX_GQA_PIPE>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
+                    : launch_pipe<64, T, false, MX_GQA_PIPE>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+  }
   if (D == 128) return causal ? launch<128, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
                               : launch<128, T, false, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
   if (D == 64) return causal ? launch<64, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
