@@ -30,6 +30,8 @@
 //    and its mirror nqb-1-p), so all workgroups carry the same number of
 //    key tiles and finish together; only diagonal / ragged tiles are
 //    masked; tiles entirely above a wave's diagonal are skipped.
+#include <type_traits>
+
 #include "mx_common.h"
 
 // Query tiles (of 32) per wave.  1 keeps two waves per SIMD (the pair hides
@@ -152,17 +154,36 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   const uint32_t lds0 = lds_addr(smem);
   const int l_row = lane / (D / 8);
   const int l_pos = lane % (D / 8);
+  // Lane offsets of the wave's loads relative to the tile's first row, so a
+  // full tile needs no VALU work: a scalar row base plus these.
+  uint32_t ld_off[L::LPW];
+#pragma unroll
+  for (int n = 0; n < L::LPW; ++n) {
+    const int ld = wave * L::LPW + n;                  // 0 .. 2*BN/RPL - 1
+    const int tile = ld / (BN / L::RPL);               // 0 = K, 1 = V
+    const int r = (ld % (BN / L::RPL)) * L::RPL + l_row;
+    ld_off[n] = (uint32_t)r * L::ROW + 16 * (l_pos ^ (tile ? vswz<D>(r) : kswz<D>(r)));
+  }
   auto issue = [&](int blk) {
     const int kv0 = blk * BN;
     const uint32_t st = lds0 + (blk % NS) * L::STAGE;
+    if (kv0 + BN <= S) {
 #pragma unroll
-    for (int n = 0; n < L::LPW; ++n) {
-      const int ld = wave * L::LPW + n;                  // 0 .. 2*BN/RPL - 1
-      const int tile = ld / (BN / L::RPL);               // 0 = K, 1 = V
-      const int r = (ld % (BN / L::RPL)) * L::RPL + l_row;
-      const int kv = min(kv0 + r, S - 1);
-      const uint32_t off = (uint32_t)kv * L::ROW + 16 * (l_pos ^ (tile ? vswz<D>(r) : kswz<D>(r)));
-      dma16(tile ? Vh : Kh, off, st + ld * 1024);
+      for (int n = 0; n < L::LPW; ++n) {
+        const int ld = wave * L::LPW + n;
+        const int tile = ld / (BN / L::RPL);
+        dma16((tile ? Vh : Kh) + (size_t)kv0 * L::ROW, ld_off[n], st + ld * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int n = 0; n < L::LPW; ++n) {
+        const int ld = wave * L::LPW + n;
+        const int tile = ld / (BN / L::RPL);
+        const int r = (ld % (BN / L::RPL)) * L::RPL + l_row;
+        const int kv = min(kv0 + r, S - 1);
+        const uint32_t off = (uint32_t)kv * L::ROW + 16 * (l_pos ^ (tile ? vswz<D>(r) : kswz<D>(r)));
+        dma16(tile ? Vh : Kh, off, st + ld * 1024);
+      }
     }
   };
   if (rep > 0) __syncthreads();  // every wave is done with the previous block's ring
@@ -174,19 +195,19 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 
   // K fragment (A operand of S^T): key row 32t + ql, chunk 2dc + g at
   // position (2dc + g) ^ kswz(ql): one lane offset per dc, t an immediate.
-  int koff[DC];
+  uint32_t koff[DC];  // absolute LDS addresses in stage 0
 #pragma unroll
-  for (int dc = 0; dc < DC; ++dc) koff[dc] = ql * L::ROW + 16 * ((2 * dc + g) ^ kswz<D>(ql));
+  for (int dc = 0; dc < DC; ++dc) koff[dc] = lds0 + ql * L::ROW + 16 * ((2 * dc + g) ^ kswz<D>(ql));
   // Transposed V fragment: lane (half g, sub-group sg, 4j+a) reads key
   // 16c + 8r + 4g + j at column 32dt + 16sg + 4a, i.e. chunk 4dt + 2sg +
   // a/2 of a row whose swizzle is vswz(4g + j): one lane offset per dt.
   const int v_sg = (lane >> 4) & 1, v_j = (lane >> 2) & 3, v_a = lane & 3;
   const int vrow = 4 * g + v_j;
   const int vw = 2 * v_sg + (v_a >> 1);
-  int v_off[DT];
+  uint32_t v_off[DT];  // absolute LDS addresses in stage 0
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
-    v_off[dt] = L::TILE + vrow * L::ROW + 16 * ((4 * dt + vw) ^ vswz<D>(vrow)) + 8 * (v_a & 1);
+    v_off[dt] = lds0 + L::TILE + vrow * L::ROW + 16 * ((4 * dt + vw) ^ vswz<D>(vrow)) + 8 * (v_a & 1);
 
   f32x16 acc_o[QT][DT];
   float m_run[QT], l_run[QT];
@@ -198,7 +219,10 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
     l_run[qt] = 0.f;
   }
 
-  for (int blk = 0; blk < nblk; ++blk) {
+  // One key tile; STG = blk % NS is a compile-time constant so every LDS
+  // fragment address is a lane offset plus an immediate.
+  auto tile = [&](int blk, auto stg_tag) {
+    constexpr int STG = decltype(stg_tag)::value;
     // stage blk landed (this wave's loads), then visible to all waves;
     // the stage read in iteration blk-1 is free for stage blk+NS-1.
     if constexpr (NS == 3) {
@@ -214,13 +238,13 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
     const int kv0 = blk * BN;
 
     if (kv0 < kv_end_w) {
-      const unsigned char* st = smem + (blk % NS) * L::STAGE;
+      constexpr uint32_t st = STG * L::STAGE;
 
       // ---- S^T tiles: rows = keys (2 x 32), cols = queries (QT x 32) ----
       // 2*QT independent accumulator chains; each K fragment feeds QT
       // MFMAs and is read KLA k-steps ahead of its use.
       auto kread = [&](int t, int dc) {
-        return ld128(st + t * 32 * L::ROW + koff[dc]);
+        return lds_ld128(koff[dc] + st + t * 32 * L::ROW);
       };
       f32x16 s[QT][2];
 #pragma unroll
@@ -248,9 +272,9 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       // V fragments of the first key chunk do not depend on the softmax:
       // issue them now so their latency hides under the VALU work below.
       auto vread = [&](int c, int dt) {
-        const unsigned char* vb = st + v_off[dt] + (16 * c) * L::ROW;
-        const u32x2 lo = lds_read_tr16(vb);
-        const u32x2 hi = lds_read_tr16(vb + 8 * L::ROW);
+        const uint32_t vb = v_off[dt] + st + (16 * c) * L::ROW;
+        const u32x2 lo = lds_read_tr16_at(vb);
+        const u32x2 hi = lds_read_tr16_at(vb + 8 * L::ROW);
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4 vb[2][DT];
@@ -331,6 +355,12 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) l_run[qt] += lsum[qt];
     }
+  };
+  for (int blk = 0; blk < nblk; blk += NS) {
+    tile(blk, std::integral_constant<int, 0>{});
+    if (blk + 1 < nblk) tile(blk + 1, std::integral_constant<int, 1>{});
+    if constexpr (NS == 3)
+      if (blk + 2 < nblk) tile(blk + 2, std::integral_constant<int, 2>{});
   }
 
   // ---- normalise and store: lane holds query qrow, d = 32dt + 8i + 4g + j ----

@@ -197,6 +197,17 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
+// LDS reads from a 32-bit LDS byte address (see lds_addr), for kernels
+// that precompute lane addresses once: the compiler then folds the
+// remaining compile-time offsets into the instruction's offset field.
+typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+__device__ __forceinline__ u32x4 lds_ld128(uint32_t addr) { return *(lds_u32x4*)(uintptr_t)addr; }
+__device__ __forceinline__ u32x2 lds_read_tr16_at(uint32_t addr) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)addr));
+}
+
 // Running-sum helper: acc + x.lo + x.hi for a dword of two bf16 / f16.
 template <typename T>
 __device__ __forceinline__ float dot2_ones(uint32_t x, float acc);
