@@ -139,7 +139,15 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   for (int qt = 0; qt < QT; ++qt) {
     qrow[qt] = q0w + 32 * qt + ql;
 #pragma unroll
-    for (int dc = 0; dc < DC; ++dc) qf[qt][dc] = ld128(Q + (q_head + min(qrow[qt], S - 1)) * D + dc * 16 + g * 8);
+    for (int dc = 0; dc < DC; ++dc) {
+      // Fold the softmax scale (in log2 units) into Q once, so the score
+      // MFMAs produce log2-domain scores directly.
+      const u32x4 x = ld128(Q + (q_head + min(qrow[qt], S - 1)) * D + dc * 16 + g * 8);
+      u32x4 y;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) y[w] = T::pack2(T::to_f32(x[w] & 0xffffu) * sl2, T::to_f32(x[w] >> 16) * sl2);
+      qf[qt][dc] = y;
+    }
   }
 
   // ---- kv range ----
@@ -209,14 +217,18 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   for (int dt = 0; dt < DT; ++dt)
     v_off[dt] = lds0 + L::TILE + vrow * L::ROW + 16 * ((4 * dt + vw) ^ vswz<D>(vrow)) + 8 * (v_a & 1);
 
+  // Softmax state per query (log2 units).  The score MFMAs start from
+  // neg_m = -m_run instead of zero, so they return s - m_run directly.
   f32x16 acc_o[QT][DT];
   float m_run[QT], l_run[QT];
+  f32x16 neg_m[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
     for (int i = 0; i < DT; ++i) acc_o[qt][i] = f32x16{};
-    m_run[qt] = -1e30f;
+    m_run[qt] = 0.f;
     l_run[qt] = 0.f;
+    neg_m[qt] = f32x16{};
   }
 
   // One key tile; STG = blk % NS is a compile-time constant so every LDS
@@ -247,8 +259,6 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
         return lds_ld128(koff[dc] + st + t * 32 * L::ROW);
       };
       f32x16 s[QT][2];
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) s[qt][0] = s[qt][1] = f32x16{};
       constexpr int KLA = 2;  // read lookahead (k-steps)
       u32x4 kb[KLA + 1][2];
 #pragma unroll
@@ -265,7 +275,8 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) s[qt][t] = mfma32<T>(kb[dc % (KLA + 1)][t], qf[qt][dc], s[qt][t]);
+          for (int qt = 0; qt < QT; ++qt)
+            s[qt][t] = mfma32<T>(kb[dc % (KLA + 1)][t], qf[qt][dc], dc == 0 ? neg_m[qt] : s[qt][t]);
         __builtin_amdgcn_sched_barrier(0);  // keep the read lookahead
       }
 
@@ -282,10 +293,11 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       for (int dt = 0; dt < DT; ++dt) vb[0][dt] = vread(0, dt);
 
       // ---- mask, online softmax (lane-local + one lane^32 exchange) ----
-      // The running max m_run is kept in log2 units (scores * sl2) and is
-      // only raised when some lane's block max exceeds it by more than
-      // 2^kLazy: below that, p = 2^(s*sl2 - m_run) stays <= 2^kLazy and the
-      // O/l rescale is skipped.  The decision is a wave-wide vote.
+      // s holds s - m_run (log2 units).  The running max is set from the
+      // first tile and afterwards only raised when some lane's block max
+      // exceeds it by more than 2^kLazy: below that, p = 2^(s - m_run)
+      // stays <= 2^kLazy and neither O, l nor the scores are touched.  The
+      // decision is a wave-wide vote.
       const bool need_mask = (kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0w);
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
@@ -304,11 +316,13 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[qt][t][e]);
-        mx = max_xor32(mx) * sl2;
-        if (__any(mx > m_run[qt] + kLazy)) {
-          const float m_new = fmaxf(m_run[qt], mx);
-          const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
-          m_run[qt] = m_new;
+        mx = max_xor32(mx);
+        const bool first = blk == 0;  // every wave processes tile 0
+        if (first || __any(mx > kLazy)) {
+          // first tile: the max itself; later: only upward moves
+          const float shift = first ? mx : fmaxf(mx, 0.f);
+          const float corr = __builtin_amdgcn_exp2f(-shift);
+          m_run[qt] += shift;
           l_run[qt] *= corr;
 #pragma unroll
           for (int i = 0; i < DT; ++i) {
@@ -317,11 +331,17 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
             else
               scale_acc(acc_o[qt][i], corr);
           }
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[qt][t][e] -= shift;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) neg_m[qt][e] = -m_run[qt];
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) s[qt][t][e] = __builtin_amdgcn_exp2f(fmaf(s[qt][t][e], sl2, -m_run[qt]));
+          for (int e = 0; e < 16; ++e) s[qt][t][e] = __builtin_amdgcn_exp2f(s[qt][t][e]);
       }
 
       // ---- O^T += V^T P^T over 4 key chunks of 16 ----
@@ -384,270 +404,6 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 }  // q-block loop
 }
 
-// Software-pipelined variant: a wave owns QTP 32-query tiles of one head.
-// Iteration i issues the score MFMAs of tile i+1 interleaved with the
-// softmax VALU work of tile i, then the PV MFMAs of tile i, so the matrix
-// pipe stays busy while the wave computes exponentials.  K and V have
-// separate 2-slot rings: iteration i reads K(i+1) and V(i) and loads K(i+2)
-// and V(i+1) behind them.
-template <int D, typename T, bool CAUSAL, int QTP>
-__global__ __launch_bounds__(NT, QTP == 1 ? 2 : 1) void gqa_fwd_pipe_kernel(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    uint16_t* __restrict__ O, int B, int Hq, int Hkv, int S, float sl2, int hpw) {
-  constexpr int QT = QTP;
-  constexpr int QW = 32 * QT;         // queries per wave
-  constexpr int DC = D / 16;          // 16-deep k steps of QK^T
-  constexpr int DT = D / 32;          // 32-row d tiles of O^T
-  using L = Lds<D>;
-  constexpr int TLD = BN / L::RPL / NWAVES;  // direct loads per wave per tile
-  extern __shared__ __align__(1024) unsigned char smem[];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = lane >> 5;      // lane half
-  const int ql = lane & 31;     // query within a 32-query tile
-
-  const int G = Hq / Hkv;
-  const int qsb = NWAVES / hpw;
-  const int QB = QW * qsb;
-  const int hgroups = G / hpw;
-  const int nqb = (S + QB - 1) / QB;
-  const int per_q = B * Hkv * hgroups;
-  const int p = (int)(blockIdx.x / per_q);
-  const int nrep = (CAUSAL && nqb - 1 - p != p) ? 2 : 1;
-  int rest = blockIdx.x % per_q;
-  const int hg = rest % hgroups;
-  rest /= hgroups;
-  const int kvh = rest % Hkv;
-  const int b = rest / Hkv;
-  const int head = kvh * G + hg * hpw + (wave % hpw);
-  const size_t q_head = ((size_t)b * Hq + head) * S;
-  const size_t kv_head = ((size_t)b * Hkv + kvh) * S;
-  const unsigned char* Kh = reinterpret_cast<const unsigned char*>(K + kv_head * D);
-  const unsigned char* Vh = reinterpret_cast<const unsigned char*>(V + kv_head * D);
-  const uint32_t lds0 = lds_addr(smem);
-  const int l_row = lane / (D / 8);
-  const int l_pos = lane % (D / 8);
-  int koff[DC];
-#pragma unroll
-  for (int dc = 0; dc < DC; ++dc) koff[dc] = ql * L::ROW + 16 * ((2 * dc + g) ^ kswz<D>(ql));
-  const int v_sg = (lane >> 4) & 1, v_j = (lane >> 2) & 3, v_a = lane & 3;
-  const int vrow = 4 * g + v_j;
-  const int vw = 2 * v_sg + (v_a >> 1);
-  int v_off[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) v_off[dt] = vrow * L::ROW + 16 * ((4 * dt + vw) ^ vswz<D>(vrow)) + 8 * (v_a & 1);
-
-  // LDS: K slots 0, 1 then V slots 0, 1, one tile each.
-  auto issue_tile = [&](const unsigned char* src, int blk, int slot) {
-    const int kv0 = blk * BN;
-    const uint32_t st = lds0 + slot * L::TILE;
-#pragma unroll
-    for (int n = 0; n < TLD; ++n) {
-      const int ld = wave * TLD + n;
-      const int r = ld * L::RPL + l_row;
-      const int kv = min(kv0 + r, S - 1);
-      const int sw = (slot >= 2) ? vswz<D>(r) : kswz<D>(r);
-      dma16(src, (uint32_t)kv * L::ROW + 16 * (l_pos ^ sw), st + ld * 1024);
-    }
-  };
-  auto issue_k = [&](int blk) { issue_tile(Kh, blk, blk & 1); };
-  auto issue_v = [&](int blk) { issue_tile(Vh, blk, 2 + (blk & 1)); };
-
-  for (int rep = 0; rep < nrep; ++rep) {
-    const int qb = CAUSAL ? (rep == 0 ? nqb - 1 - p : p) : p;
-    const int q0wg = qb * QB;
-    const int q0w = q0wg + (wave / hpw) * QW;
-    int qrow[QT];
-    u32x4 qf[QT][DC];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      qrow[qt] = q0w + 32 * qt + ql;
-#pragma unroll
-      for (int dc = 0; dc < DC; ++dc) qf[qt][dc] = ld128(Q + (q_head + min(qrow[qt], S - 1)) * D + dc * 16 + g * 8);
-    }
-    const int kv_end_wg = CAUSAL ? min(S, q0wg + QB) : S;
-    const int nblk = (kv_end_wg + BN - 1) / BN;
-    const int kv_end_w = CAUSAL ? min(S, q0w + QW) : S;
-
-    if (rep > 0) __syncthreads();  // every wave is done with the previous block's rings
-    issue_k(0);
-    issue_v(0);
-    wait_vmcnt<0>();  // the Q loads, K(0) and V(0) complete together
-    if (nblk > 1) issue_k(1);
-
-    f32x16 acc_o[QT][DT];
-    float m_run[QT], l_run[QT];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-      for (int i = 0; i < DT; ++i) acc_o[qt][i] = f32x16{};
-      m_run[qt] = -1e30f;
-      l_run[qt] = 0.f;
-    }
-    f32x16 sc[QT][2];  // scores of tile i
-    f32x16 sn[QT][2];  // scores of tile i+1
-    u32x4 pf[QT][4];   // P^T fragments of tile i, 4 key chunks of 16
-
-    auto kread = [&](int blk, int t, int dc) {
-      return ld128(smem + (blk & 1) * L::TILE + t * 32 * L::ROW + koff[dc]);
-    };
-    // S^T MFMAs of tile blk into dst; `sm(k)` is issued after the k-th
-    // K fragment's MFMAs (2*DC steps).
-    auto scores = [&](int blk, f32x16 (&dst)[QT][2], auto&& sm) {
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) dst[qt][0] = dst[qt][1] = f32x16{};
-      constexpr int KLA = 2;
-      u32x4 kb[KLA + 1];
-#pragma unroll
-      for (int k = 0; k < KLA; ++k) kb[k] = kread(blk, k & 1, k >> 1);
-#pragma unroll
-      for (int k = 0; k < 2 * DC; ++k) {
-        if (k + KLA < 2 * DC) kb[(k + KLA) % (KLA + 1)] = kread(blk, (k + KLA) & 1, (k + KLA) >> 1);
-        const int t = k & 1, dc = k >> 1;
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) dst[qt][t] = mfma32<T>(kb[k % (KLA + 1)], qf[qt][dc], dst[qt][t]);
-        sm(k);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-
-    // Softmax of tile blk (scores in sc) in 2*DC steps: steps 0..2QT-1 mask
-    // and reduce the block max of one (qt, t) 16-value group each, step 2QT
-    // finishes the max and the lazy rescale, the remaining steps produce
-    // the exponentials, P^T fragments and row sums one 8-key piece at a time.
-    float mx[QT];
-    float corr[QT];
-    float lsum[QT];
-    auto softmax_step = [&](int blk, int k) {
-      const int kv0 = blk * BN;
-      if (k < 2 * QT) {
-        const int qt = k >> 1, t = k & 1;
-        const bool need_mask = (kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0w + 32 * qt);
-        if (need_mask) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int kv = kv0 + t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-            const bool dead = (kv >= S) | (CAUSAL & (kv > qrow[qt]));
-            sc[qt][t][e] = dead ? -INFINITY : sc[qt][t][e];
-          }
-        }
-        float m = (t == 0) ? -INFINITY : mx[qt];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) m = fmaxf(m, sc[qt][t][e]);
-        mx[qt] = m;
-      } else if (k == 2 * QT) {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          const float m = max_xor32(mx[qt]) * sl2;
-          const bool up = __any(m > m_run[qt] + kLazy);
-          const float m_new = up ? fmaxf(m_run[qt], m) : m_run[qt];
-          corr[qt] = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
-          m_run[qt] = m_new;
-          l_run[qt] *= corr[qt];
-          lsum[qt] = 0.f;
-        }
-      } else {
-        constexpr int NSTEP = 2 * DC - 2 * QT - 1;
-#pragma unroll
-        for (int piece = 0; piece < QT * 4; ++piece) {
-          if (piece * NSTEP / (QT * 4) != k - 2 * QT - 1) continue;
-          const int qt = piece >> 2, c = piece & 3;
-          const int t = c >> 1, i0 = 2 * (c & 1);
-          float x[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(sc[qt][t][4 * i0 + e], sl2, -m_run[qt]));
-          const u32x4 pv{T::pack2(x[0], x[1]), T::pack2(x[2], x[3]), T::pack2(x[4], x[5]), T::pack2(x[6], x[7])};
-          pf[qt][c] = pv;
-#pragma unroll
-          for (int w = 0; w < 4; ++w) lsum[qt] = dot2_ones<T>(pv[w], lsum[qt]);
-        }
-      }
-    };
-
-    auto vread = [&](int blk, int c, int dt) {
-      const unsigned char* vb = smem + (2 + (blk & 1)) * L::TILE + v_off[dt] + (16 * c) * L::ROW;
-      const u32x2 lo = lds_read_tr16(vb);
-      const u32x2 hi = lds_read_tr16(vb + 8 * L::ROW);
-      return u32x4{lo[0], lo[1], hi[0], hi[1]};
-    };
-    auto values = [&](int blk) {
-      u32x4 vb[2][DT];
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) vb[0][dt] = vread(blk, 0, dt);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (c + 1 < 4) {
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) vb[(c + 1) & 1][dt] = vread(blk, c + 1, dt);
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) acc_o[qt][dt] = mfma32<T>(vb[c & 1][dt], pf[qt][c], acc_o[qt][dt]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-
-    __syncthreads();  // K(0), V(0) visible to all waves
-    if (0 < kv_end_w) scores(0, sc, [](int) {});
-    for (int i = 0; i < nblk; ++i) {
-      // K(i+1) and V(i) landed for all waves; K(i) and V(i-1) slots free
-      wait_vmcnt<0>();
-      __syncthreads();
-      if (i + 2 < nblk) issue_k(i + 2);
-      if (i + 1 < nblk) issue_v(i + 1);
-      const bool do_i = i * BN < kv_end_w;
-      const bool do_n = i + 1 < nblk && (i + 1) * BN < kv_end_w;
-      if (do_n) {
-        scores(i + 1, sn, [&](int k) { softmax_step(i, k); });
-      } else if (do_i) {
-#pragma unroll
-        for (int k = 0; k < 2 * DC; ++k) softmax_step(i, k);
-      }
-      if (do_i) {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          if (__any(corr[qt] != 1.f)) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-              if constexpr (QT == 1)
-                acc_o[qt][dt] *= corr[qt];
-              else
-                scale_acc(acc_o[qt][dt], corr[qt]);
-            }
-          }
-          l_run[qt] += lsum[qt];
-        }
-        values(i);
-      }
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        sc[qt][0] = sn[qt][0];
-        sc[qt][1] = sn[qt][1];
-      }
-    }
-
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const float l_tot = sum_xor32(l_run[qt]);
-      const float inv = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
-      if (qrow[qt] < S) {
-        uint16_t* orow = O + (q_head + qrow[qt]) * D;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int d = dt * 32 + 8 * i + 4 * g;
-            const f32x16& a = acc_o[qt][dt];
-            st64(orow + d, u32x2{T::pack2(a[4 * i] * inv, a[4 * i + 1] * inv),
-                                 T::pack2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)});
-          }
-      }
-    }
-  }
-}
-
 template <int D, typename T, bool CAUSAL, int QT>
 static int launch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
                   hipStream_t stream) {
@@ -666,39 +422,9 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
   return MX_OK;
 }
 
-template <int D, typename T, bool CAUSAL, int QTP>
-static int launch_pipe(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
-                       hipStream_t stream) {
-  const int G = Hq / Hkv;
-  const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
-  const int QB = 32 * QTP * (NWAVES / hpw);
-  const int nqb = (S + QB - 1) / QB;
-  const long long grid = (long long)(CAUSAL ? (nqb + 1) / 2 : nqb) * B * Hkv * (G / hpw);
-  if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
-  auto kern = gqa_fwd_pipe_kernel<D, T, CAUSAL, QTP>;
-  constexpr int lds = 4 * Lds<D>::TILE;
-  MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), lds, stream, (const uint16_t*)Q, (const uint16_t*)K,
-                     (const uint16_t*)V, (uint16_t*)O, B, Hq, Hkv, S, scale * kLog2e, hpw);
-  MX_RETURN_IF_HIP(hipGetLastError());
-  return MX_OK;
-}
-
-#ifndef MX_GQA_PIPE
-#define MX_GQA_PIPE 0
-#endif
-
 template <typename T, int QT>
 static int dispatch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int D,
                     float scale, int causal, hipStream_t s) {
-  if constexpr (MX_GQA_PIPE > 0) {
-    if (D == 128)
-      return causal ? launch_pipe<128, T, true, MX_GQA_PIPE>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
-                    : launch_pipe<128, T, false, MX_GQA_PIPE>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
-    if (D == 64)
-      return causal ? launch_pipe<64, T, true, MX_GQA_PIPE>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
-                    : launch_pipe<64, T, false, MX_GQA_PIPE>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
-  }
   if (D == 128) return causal ? launch<128, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
                               : launch<128, T, false, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
   if (D == 64) return causal ? launch<64, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
