@@ -259,6 +259,9 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
         return lds_ld128(koff[dc] + st + t * 32 * L::ROW);
       };
       f32x16 s[QT][2];
+      // Wave priority: the two waves sharing a SIMD issue their MFMA phases
+      // ahead of the other's softmax VALU work, which then fills the gaps.
+      __builtin_amdgcn_s_setprio(1);
       constexpr int KLA = 2;  // read lookahead (k-steps)
       u32x4 kb[KLA + 1][2];
 #pragma unroll
@@ -292,6 +295,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) vb[0][dt] = vread(0, dt);
 
+      __builtin_amdgcn_s_setprio(0);
       // ---- mask, online softmax (lane-local + one lane^32 exchange) ----
       // s holds s - m_run (log2 units).  The running max is set from the
       // first tile and afterwards only raised when some lane's block max
@@ -344,6 +348,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
           for (int e = 0; e < 16; ++e) s[qt][t][e] = __builtin_amdgcn_exp2f(s[qt][t][e]);
       }
 
+      __builtin_amdgcn_s_setprio(1);
       // ---- O^T += V^T P^T over 4 key chunks of 16 ----
       float lsum[QT];
 #pragma unroll
@@ -374,6 +379,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       }
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) l_run[qt] += lsum[qt];
+      __builtin_amdgcn_s_setprio(0);
     }
   };
   for (int blk = 0; blk < nblk; blk += NS) {
