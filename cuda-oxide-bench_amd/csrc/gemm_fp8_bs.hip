@@ -8,74 +8,94 @@
 // style 1x128 activation / 128x128 weight blocks).
 //
 // MI355X design:
-//  * 16x16x128 f8f6f4 MFMA: one instruction consumes exactly one 128-deep
-//    scale block, so each K tile (BK = 128) produces a fresh fp32 partial per
-//    16x16 fragment which is promoted into the running accumulator with one
-//    FMA per element:  acc += (sA[m,kb] * sB[kb,nb]) * partial.  The block
-//    scales are arbitrary fp32, so the E8M0 (power-of-two) hardware scales
-//    cannot carry them; software promotion keeps the result exact to fp32.
-//  * Tiles, LDS double buffering, the in-register B transpose (here a
-//    4(k) x 16(n) byte transpose with v_perm) and the XOR-swizzled 128-byte
-//    LDS rows follow the bf16 kernel; every operand fetch is ds_read_b128.
-//  * sB is uniform over a wave's n range (<= 128 columns, block aligned) and
-//    is read once per K tile; sA is read per fragment row.
+//  * The kernel computes C^T = B^T . A^T with 32x32x64 f8f6f4 MFMAs: the
+//    B^T fragment (rows n) is the A operand, the A^T fragment (columns m)
+//    the B operand.  A lane of the result then holds one m and 16 n, so the
+//    1x128 activation scale is one per-lane value per fragment and the
+//    128x128 weight scale one wave-uniform value.
+//  * Each K tile is one 128-deep scale block: two MFMAs build a fresh fp32
+//    partial per 32x32 fragment, promoted with one FMA per element,
+//    acc += (sA[m,kb] * sB[kb,nb]) * partial (arbitrary fp32 scales, so the
+//    power-of-two E8M0 hardware scales cannot carry them).  The promotion
+//    of one fragment is issued behind the MFMAs of the next.
+//  * 256x256 tiles, 8 waves (2 in m x 4 in n, two per SIMD), each wave
+//    128(m) x 64(n): the fp32 accumulators stay in architectural VGPRs,
+//    where the promotion FMAs can reach them.  Grids under 256 such tiles
+//    use 128x128 tiles.
+//  * A and B tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR
+//    staging) in their natural row-major layouts, double buffered.  A^T
+//    fragments are plain ds_read_b128; B^T fragments come from k-major B
+//    rows through gfx950's transposing read ds_read_b64_tr_b8: in each
+//    16-lane group, lane 8h+b receives byte b of the 8-byte rows addressed
+//    by lanes 2j+h, so pointing lane 2j+h at k-row j, columns 8h..8h+7
+//    gives every lane 8 consecutive k-bytes of its own column.  No VALU
+//    transposes.
+//  * 16-byte chunks are XOR-swizzled per row so every fragment read phase
+//    is bank-conflict free.
 #include "mx_common.h"
 
 namespace mx {
 namespace gemm8 {
 
 constexpr int BK = 128;   // bytes of K per tile = one scale block
-constexpr int ROW_B = BK;
+constexpr int NWAVES = 8;  // 2 (m) x 4 (n), two waves per SIMD
+constexpr int NT = 64 * NWAVES;
 constexpr int GROUP_M = 8;
 
-__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
-__device__ __forceinline__ int lds_off(int row, int c) { return row * ROW_B + ((c ^ swz(row)) << 4); }
-
-template <int BM, int BN, int WM, int WN>
-struct Cfg {
-  static constexpr int NT = 64 * WM * WN;
-  static constexpr int TM = BM / WM, TN = BN / WN;
-  static constexpr int FM = TM / 16, FN = TN / 16;
-  static constexpr int A_CHUNKS = BM * BK / 16 / NT;
-  static constexpr int NB = BN / 16;                 // 16-column blocks of B
-  static constexpr int KR = BK * BN / 16 / NT;       // k rows per B block
-  static constexpr int LDS_A = BM * ROW_B;
-  static constexpr int LDS_B = BN * ROW_B;
-  static constexpr int LDS_STAGE = LDS_A + LDS_B;
-  static_assert(KR == 4 || KR == 8, "4x16 byte transposes per thread");
-  static_assert(A_CHUNKS >= 1, "A split");
-  static_assert(128 % TN == 0, "wave n-range inside one scale block");
-};
-
-// 4 rows x 16 bytes -> 16 columns x 4 bytes (column c gets rows 0..3 at byte c).
-__device__ __forceinline__ void transpose4x16_b8(const u32x4 in[4], uint32_t out[16]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t a = in[0][j], b = in[1][j], c = in[2][j], d = in[3][j];
-    const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);
-    const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);
-    const uint32_t cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);
-    const uint32_t cd_hi = __builtin_amdgcn_perm(d, c, 0x07030602u);
-    out[4 * j + 0] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);
-    out[4 * j + 1] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);
-    out[4 * j + 2] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
-    out[4 * j + 3] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
-  }
+// 32x32x64 e4m3 x e4m3 -> fp32 (scaled form with unit E8M0 scales).
+// A: lane l holds row l%32, k = 32(l/32)..+31; B: column l%32, same k;
+// D: lane l holds column l%32, rows 8i + 4(l/32) + j in d[4i + j].
+__device__ __forceinline__ f32x16 mfma32_fp8(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_fp8_bs_kernel(const uint8_t* __restrict__ A,
-                                                                  const float* __restrict__ sA,
-                                                                  const uint8_t* __restrict__ B,
-                                                                  const float* __restrict__ sB,
-                                                                  uint16_t* __restrict__ C, int M, int N, int K) {
-  using CF = Cfg<BM, BN, WM, WN>;
-  constexpr int NT = CF::NT, FM = CF::FM, FN = CF::FN;
-  extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ u32x2 lds_read_tr8_at(uint32_t addr) {
+  typedef int v2i32 __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32*)(uintptr_t)addr));
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
+template <int BM, int BN>
+struct Cfg {
+  static constexpr int WM = 2, WN = 4;
+  static constexpr int TM = BM / WM, TN = BN / WN;   // wave tile
+  static constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments
+  static constexpr int A_B = BM * BK;                // A stage: BM rows of 128 B
+  static constexpr int B_B = BK * BN;                // B stage: 128 k-rows of BN B
+  static constexpr int STAGE = A_B + B_B;
+  static constexpr int A_LPW = A_B / 1024 / NWAVES;  // 1 KB direct loads per wave
+  static constexpr int B_LPW = B_B / 1024 / NWAVES;
+  static constexpr int B_CH = BN / 16;               // 16-byte chunks per B row
+  static constexpr int B_RPL = 1024 / BN;            // B rows per 1 KB load
+  static_assert(FM >= 1 && FN >= 1 && A_LPW >= 1 && B_LPW >= 1, "tile split");
+  static_assert(TN <= 128 && 128 % TN == 0, "a wave's columns share one weight-scale block");
+  static_assert(BN == 128 || BN == 256, "B row swizzle");
+};
 
+// Chunk position swizzles.  A rows (128 B): a 16-lane b128 phase reads one
+// chunk of 16 consecutive rows, two rows per 256 B.  B rows: a 32-lane
+// transposing phase reads 8 consecutive k-rows x 2 adjacent chunks.
+__device__ __forceinline__ int swz_a(int m) { return (m >> 1) & 7; }
+template <int BN>
+__device__ __forceinline__ int swz_b(int k) {
+  return BN == 256 ? ((k & 7) << 1) : (((k >> 1) & 3) << 1);
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __restrict__ A,
+                                                           const float* __restrict__ sA,
+                                                           const uint8_t* __restrict__ B,
+                                                           const float* __restrict__ sB,
+                                                           uint16_t* __restrict__ C, int M, int N, int K) {
+  using CF = Cfg<BM, BN>;
+  constexpr int FM = CF::FM, FN = CF::FN;
+  extern __shared__ __align__(1024) unsigned char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / CF::WN, wn = wave % CF::WN;
+
+  // ---- tile -> (tm, tn), grouped for L2 reuse, XCD-aware ----
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
   const int per_group = GROUP_M * tiles_n;
@@ -85,131 +105,171 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_fp8_bs_kernel(const uint
   const int tm = first_m + (id % per_group) % gsz;
   const int tn = (id % per_group) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
-
   const int kblocks = K / BK;
   const int nblocks_n = (N + 127) / 128;
 
-  const int b_nb = tid % CF::NB, b_kb = tid / CF::NB;
-  constexpr int KR = CF::KR;
-  u32x4 ra[CF::A_CHUNKS], rb[KR];
-
-  auto load_tile = [&](int k0) {
+  // ---- direct loads.  A load n: rows 8n .. 8n+7 (lane i: row 8n + i/8,
+  // chunk (i%8) ^ swz_a(row)); B load n: k-rows B_RPL*n .. (lane i: k-row
+  // B_RPL*n + i/B_CH, chunk (i%B_CH) ^ swz_b(row)).  Rows past M and
+  // columns past N re-read the last valid ones (never stored). ----
+  const uint32_t lds0 = lds_addr(smem);
+  const bool full_m = m0 + BM <= M, full_n = n0 + BN <= N;
+  uint32_t a_off[CF::A_LPW], b_off[CF::B_LPW];
 #pragma unroll
-    for (int i = 0; i < CF::A_CHUNKS; ++i) {
-      const int q = tid + i * NT;
-      const int row = q >> 3, c = q & 7;
-      const int gm = m0 + row;
-      ra[i] = (gm < M) ? ld128(A + (size_t)gm * K + k0 + c * 16) : u32x4{0, 0, 0, 0};
-    }
-    const int gn = n0 + b_nb * 16;
+  for (int n = 0; n < CF::A_LPW; ++n) {
+    const int row = 8 * (wave * CF::A_LPW + n) + (lane >> 3);
+    const int gm = full_m ? m0 + row : min(m0 + row, M - 1);
+    a_off[n] = (uint32_t)(gm - m0) * K + 16 * ((lane & 7) ^ swz_a(row));
+  }
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-      const int gk = k0 + b_kb * KR + r;
-      rb[r] = (gn < N) ? ld128(B + (size_t)gk * N + gn) : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto store_tile = [&](int stage) {
-    unsigned char* sa = smem + stage * CF::LDS_STAGE;
-    unsigned char* sb = sa + CF::LDS_A;
+  for (int n = 0; n < CF::B_LPW; ++n) {
+    const int row = CF::B_RPL * (wave * CF::B_LPW + n) + lane / CF::B_CH;
+    int col = 16 * ((lane % CF::B_CH) ^ swz_b<BN>(row));
+    if (!full_n) col = min(n0 + col, N - 16) - n0;
+    b_off[n] = (uint32_t)row * N + col;
+  }
+  auto issue = [&](int kb, int stage) {
+    const uint32_t st = lds0 + stage * CF::STAGE;
+    const uint8_t* abase = A + (size_t)m0 * K + (size_t)kb * BK;
+    const uint8_t* bbase = B + (size_t)kb * BK * N + n0;
 #pragma unroll
-    for (int i = 0; i < CF::A_CHUNKS; ++i) {
-      const int q = tid + i * NT;
-      *reinterpret_cast<u32x4*>(sa + lds_off(q >> 3, q & 7)) = ra[i];
-    }
-    uint32_t cols[KR / 4][16];
+    for (int n = 0; n < CF::A_LPW; ++n) dma16(abase, a_off[n], st + (wave * CF::A_LPW + n) * 1024);
 #pragma unroll
-    for (int h = 0; h < KR / 4; ++h) transpose4x16_b8(rb + 4 * h, cols[h]);
-    const int kbyte = b_kb * KR;
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const int n = b_nb * 16 + c;
-      unsigned char* dst = sb + lds_off(n, kbyte >> 4) + (kbyte & 15);
-      if constexpr (KR == 8) {
-        *reinterpret_cast<u32x2*>(dst) = u32x2{cols[0][c], cols[1][c]};
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = cols[0][c];
-      }
-    }
+    for (int n = 0; n < CF::B_LPW; ++n)
+      dma16(bbase, b_off[n], st + CF::A_B + (wave * CF::B_LPW + n) * 1024);
   };
 
-  f32x4 acc[FM][FN];
+  // ---- fragment lane addresses (stage 0) ----
+  // A^T (B operand): row m = wm*TM + 32 mf + l%32, chunks 4 ks + 2 (l/32) + {0,1}.
+  const int am = wm * CF::TM + (lane & 31);
+  const uint32_t a_row = lds0 + am * BK;
+  const int a_x = swz_a(am);  // same for every mf (32 rows apart)
+  // B^T (A operand) via tr_b8: in 16-lane group q, lane 2j+h reads k-row
+  // 64 ks + 32 (q>>1) + 8 r + j, columns wn*TN + 32 nf + 16 (q&1) + 8 h.
+  const int q = lane >> 4, jj = (lane & 15) >> 1, hh = lane & 1;
+  const int b_k0 = 32 * (q >> 1) + jj;                       // plus 64 ks + 8 r
+  const int b_c0 = wn * CF::TN + 16 * (q & 1) + 8 * hh;      // plus 32 nf
+  const uint32_t b_row = lds0 + CF::A_B + b_k0 * BN;
+  const int b_x = swz_b<BN>(b_k0);  // rows 8 apart share it
+  uint32_t b_col[FN];
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int nf = 0; nf < FN; ++nf) {
+    const int col = b_c0 + 32 * nf;
+    b_col[nf] = b_row + 16 * ((col >> 4) ^ b_x) + (col & 15);
+  }
+  const int a_c = 2 * (lane >> 5);
+  uint32_t a_col[2][2];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Rows of C this lane accumulates (one per fragment row i) and the
-  // wave's scale-block column.
-  const int a_row0 = wm * CF::TM + (lane & 15);
-  const int b_row0 = wn * CF::TN + (lane & 15);
-  const int kq = lane >> 4;
-  const int wave_nblk = min((n0 + wn * CF::TN) / 128, nblocks_n - 1);
-
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < kblocks; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < kblocks) load_tile((kt + 1) * BK);
-    const float sb_k = sB[(size_t)kt * nblocks_n + wave_nblk];
-    float sa_k[FM];
+  for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int gm = m0 + a_row0 + i * 16;
-      sa_k[i] = (gm < M) ? sA[(size_t)gm * kblocks + kt] * sb_k : 0.f;
+    for (int h = 0; h < 2; ++h) a_col[ks][h] = a_row + 16 * ((4 * ks + a_c + h) ^ a_x);
+
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
+
+  // Block scales: sA row of this lane per m fragment, sB per wave.  The
+  // scales of tile kb+1 are loaded before its tile loads are issued, so
+  // the wait that lands the tile also lands them.
+  int sa_row[FM];
+#pragma unroll
+  for (int mf = 0; mf < FM; ++mf) sa_row[mf] = min(m0 + am + 32 * mf, M - 1) * kblocks;
+  const int wave_nb = min((n0 + wn * CF::TN) / 128, nblocks_n - 1);
+  float sa_c[FM], sb_c;
+  auto load_scales = [&](int kb) {
+    sb_c = sB[(size_t)kb * nblocks_n + wave_nb];
+#pragma unroll
+    for (int mf = 0; mf < FM; ++mf) sa_c[mf] = sA[sa_row[mf] + kb];
+  };
+
+  load_scales(0);
+  issue(0, 0);
+  for (int kb = 0; kb < kblocks; ++kb) {
+    const uint32_t so = (kb & 1) * CF::STAGE;
+    wait_vmcnt<0>();  // this wave's loads of tile kb and its scales landed
+    __syncthreads();  // tile kb visible to all waves; the other stage is free
+    float s_m[FM];
+#pragma unroll
+    for (int mf = 0; mf < FM; ++mf) s_m[mf] = sa_c[mf] * sb_c;
+    if (kb + 1 < kblocks) {
+      load_scales(kb + 1);
+      issue(kb + 1, (kb & 1) ^ 1);
     }
-    const unsigned char* sa = smem + cur * CF::LDS_STAGE;
-    const unsigned char* sb = sa + CF::LDS_A;
-    i32x8 bfr[FN];
+
+    i32x8 bf[2][FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int r = b_row0 + j * 16;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(sb + lds_off(r, 2 * kq));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(sb + lds_off(r, 2 * kq + 1));
-      bfr[j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-    }
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int r = a_row0 + i * 16;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(sa + lds_off(r, 2 * kq));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(sa + lds_off(r, 2 * kq + 1));
-      const i32x8 af{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      for (int nf = 0; nf < FN; ++nf) {
+        u32x2 v[4];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const f32x4 p = mfma16_fp8(bfr[j], af, f32x4{0.f, 0.f, 0.f, 0.f});
-        acc[i][j] += sa_k[i] * p;
+        for (int r = 0; r < 4; ++r) v[r] = lds_read_tr8_at(b_col[nf] + so + (64 * ks + 8 * r) * BN);
+        bf[ks][nf] = i32x8{(int)v[0][0], (int)v[0][1], (int)v[1][0], (int)v[1][1],
+                           (int)v[2][0], (int)v[2][1], (int)v[3][0], (int)v[3][1]};
+      }
+
+    // Two MFMAs per fragment into a fresh partial; the promotion of one
+    // fragment trails the MFMAs of the next.
+    f32x16 p[2];
+#pragma unroll
+    for (int mf = 0; mf < FM; ++mf) {
+      i32x8 af[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint32_t r = so + 32 * mf * BK;
+        const u32x4 lo = lds_ld128(a_col[ks][0] + r);
+        const u32x4 hi = lds_ld128(a_col[ks][1] + r);
+        af[ks] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int nf = 0; nf < FN; ++nf) {
+        const int f = mf * FN + nf;
+        const f32x16 x = mfma32_fp8(bf[0][nf], af[0], f32x16{});
+        p[f & 1] = mfma32_fp8(bf[1][nf], af[1], x);
+        if (f > 0) {
+          const int g = f - 1;
+          acc[g % FN][g / FN] += s_m[g / FN] * p[g & 1];
+        }
       }
     }
-    if (kt + 1 < kblocks) store_tile(cur ^ 1);
-    __syncthreads();
+    {
+      const int g = FM * FN - 1;
+      acc[g % FN][g / FN] += s_m[g / FN] * p[g & 1];
+    }
   }
 
+  // ---- store C: lane holds m = m0 + am + 32 mf, n = n0 + wn*TN + 32 nf + 8 i + 4 (l/32) + j ----
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int gm = m0 + wm * CF::TM + i * 16 + (lane & 15);
+  for (int mf = 0; mf < FM; ++mf) {
+    const int gm = m0 + am + 32 * mf;
     if (gm >= M) continue;
+    uint16_t* crow = C + (size_t)gm * N;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int gn = n0 + wn * CF::TN + j * 16 + 4 * (lane >> 4);
-      if (gn < N) {
-        st64(C + (size_t)gm * N + gn,
-             u32x2{pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])});
+    for (int nf = 0; nf < FN; ++nf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int gn = n0 + wn * CF::TN + 32 * nf + 8 * i + 4 * (lane >> 5);
+        if (gn < N) {
+          const f32x16& a = acc[nf][mf];
+          st64(crow + gn, u32x2{pack_bf16x2(a[4 * i], a[4 * i + 1]), pack_bf16x2(a[4 * i + 2], a[4 * i + 3])});
+        }
       }
-    }
   }
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN>
 static int launch(const void* A, const float* sA, const void* B, const float* sB, void* C, int M, int N, int K,
                   hipStream_t stream) {
-  using CF = Cfg<BM, BN, WM, WN>;
-  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const size_t smem = 2 * CF::LDS_STAGE;
-  auto kern = gemm_fp8_bs_kernel<BM, BN, WM, WN>;
+  using CF = Cfg<BM, BN>;
+  const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
+  const size_t smem = 2 * CF::STAGE;
+  auto kern = gemm_fp8_bs_kernel<BM, BN>;
   MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-  hipLaunchKernelGGL(kern, dim3(tiles), dim3(CF::NT), smem, stream, (const uint8_t*)A, sA, (const uint8_t*)B, sB,
-                     (uint16_t*)C, M, N, K);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NT), smem, stream, (const uint8_t*)A, sA, (const uint8_t*)B,
+                     sB, (uint16_t*)C, M, N, K);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
 }
@@ -224,8 +284,11 @@ extern "C" int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, con
   if (K % 128) return MX_ERR_SHAPE;
   if (N % 16) return MX_ERR_ALIGN;
   if ((long long)M * K > (1LL << 40) || (long long)K * N > (1LL << 40)) return MX_ERR_SHAPE;
+  if ((long long)N * 256 > 0xffffffffLL || (long long)K * 256 > 0xffffffffLL) return MX_ERR_SHAPE;
   if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15) return MX_ERR_ALIGN;
   if (((uintptr_t)sA | (uintptr_t)sB) & 3) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  return mx::gemm8::launch<128, 128, 2, 2>(A, sA, B, sB, C, M, N, K, s);
+  const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
+  if (tiles256 >= 256) return mx::gemm8::launch<256, 256>(A, sA, B, sB, C, M, N, K, s);
+  return mx::gemm8::launch<128, 128>(A, sA, B, sB, C, M, N, K, s);
 }
