@@ -244,6 +244,36 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
 }
 #pragma clang diagnostic pop
 
+// Workgroup barrier without the release/acquire fences of __syncthreads().
+// Those fences make the compiler drain every outstanding LDS access of the
+// wave (lgkmcnt(0)) before the barrier, which empties a read lookahead.  For
+// kernels that order their LDS traffic themselves: DMA'd tiles are waited
+// for with wait_vmcnt before the barrier, and a stage handed back to the DMA
+// after the barrier was consumed by instructions that already waited for
+// their reads.  The empty asm statements keep the compiler from moving
+// memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Scheduling of one region of NM MFMAs and R LDS reads (issued in that
+// region for a later use): alternate one MFMA with an even share of the
+// reads, so a read lookahead never needs more than a few LDS instructions in
+// flight (lgkmcnt counts at most 15) and the compiler can wait for exactly
+// the reads each MFMA needs.  Call right after the region's code, before a
+// sched_barrier that closes the region.
+template <int NM, int R, int I = 0>
+__device__ __forceinline__ void interleave_mfma_ds() {
+  if constexpr (I < NM) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    constexpr int r = (R * (I + 1)) / NM - (R * I) / NM;
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);  // r LDS reads
+    interleave_mfma_ds<NM, R, I + 1>();
+  }
+}
+
 // 32-bit LDS byte address of a pointer into __shared__ memory.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) unsigned char*)p);

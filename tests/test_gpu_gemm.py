@@ -85,6 +85,21 @@ def test_kat_pattern(ops):
     assert torch.equal(c, want)
 
 
+@pytest.mark.parametrize("mnk", [(4096, 4096, 32), (4096, 4096, 96), (4000, 4040, 4128), (4096, 4352, 2048)])
+def test_direct_load_path(ops, mnk):
+    """Shapes that take the large-problem kernel (>= 256 tiles of 256x256,
+    K % 32 == 0): a single K tile, fewer K tiles than ring stages, ragged M
+    and N with a K-tile count that is not a multiple of the ring depth."""
+    m, n, k = mnk
+    announce(f"gemm_bf16 direct-load {m}x{n}x{k}")
+    a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
+    c = run(ops, a, b)
+    ref = ogemm.gemm_ref(a, b)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+
+
 def test_target_size_sampled(ops):
     """8192^3 (the roofline target): 256 cells against fp64 dot products."""
     announce("gemm_bf16 8192^3 sampled")
