@@ -16,8 +16,10 @@
 //  * Each K tile is one 128-deep scale block: two MFMAs build a fresh fp32
 //    partial per 32x32 fragment, promoted with one FMA per element,
 //    acc += (sA[m,kb] * sB[kb,nb]) * partial (arbitrary fp32 scales, so the
-//    power-of-two E8M0 hardware scales cannot carry them).  The promotion
-//    of one fragment is issued behind the MFMAs of the next.
+//    power-of-two E8M0 hardware scales cannot carry them).  The fragments
+//    of one row block build their partials side by side, so no MFMA waits
+//    for the one just before it, and the promotion of one row block
+//    overlaps the MFMAs of the next.
 //  * 256x256 tiles, 8 waves (2 in m x 4 in n, two per SIMD), each wave
 //    128(m) x 64(n): the fp32 accumulators stay in architectural VGPRs,
 //    where the promotion FMAs can reach them.  Grids under 256 such tiles
@@ -32,6 +34,8 @@
 //    transposes.
 //  * 16-byte chunks are XOR-swizzled per row so every fragment read phase
 //    is bank-conflict free.
+#include <type_traits>
+
 #include "mx_common.h"
 
 namespace mx {
@@ -128,18 +132,19 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     if (!full_n) col = min(n0 + col, N - 16) - n0;
     b_off[n] = (uint32_t)row * N + col;
   }
+  // LDS layout [A0 | A1 | B0 | B1]: one base register per fragment reaches
+  // both stages of its operand with the 16-bit immediate offset of ds_read.
   auto issue = [&](int kb, int stage) {
-    const uint32_t st = lds0 + stage * CF::STAGE;
+    const uint32_t sa = lds0 + stage * CF::A_B, sb = lds0 + 2 * CF::A_B + stage * CF::B_B;
     const uint8_t* abase = A + (size_t)m0 * K + (size_t)kb * BK;
     const uint8_t* bbase = B + (size_t)kb * BK * N + n0;
 #pragma unroll
-    for (int n = 0; n < CF::A_LPW; ++n) dma16(abase, a_off[n], st + (wave * CF::A_LPW + n) * 1024);
+    for (int n = 0; n < CF::A_LPW; ++n) dma16(abase, a_off[n], sa + (wave * CF::A_LPW + n) * 1024);
 #pragma unroll
-    for (int n = 0; n < CF::B_LPW; ++n)
-      dma16(bbase, b_off[n], st + CF::A_B + (wave * CF::B_LPW + n) * 1024);
+    for (int n = 0; n < CF::B_LPW; ++n) dma16(bbase, b_off[n], sb + (wave * CF::B_LPW + n) * 1024);
   };
 
-  // ---- fragment lane addresses (stage 0) ----
+  // ---- fragment lane addresses (stage 0; stage 1 is an immediate away) ----
   // A^T (B operand): row m = wm*TM + 32 mf + l%32, chunks 4 ks + 2 (l/32) + {0,1}.
   const int am = wm * CF::TM + (lane & 31);
   const uint32_t a_row = lds0 + am * BK;
@@ -149,7 +154,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   const int q = lane >> 4, jj = (lane & 15) >> 1, hh = lane & 1;
   const int b_k0 = 32 * (q >> 1) + jj;                       // plus 64 ks + 8 r
   const int b_c0 = wn * CF::TN + 16 * (q & 1) + 8 * hh;      // plus 32 nf
-  const uint32_t b_row = lds0 + CF::A_B + b_k0 * BN;
+  const uint32_t b_row = lds0 + 2 * CF::A_B + b_k0 * BN;
   const int b_x = swz_b<BN>(b_k0);  // rows 8 apart share it
   uint32_t b_col[FN];
 #pragma unroll
@@ -177,67 +182,77 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
 #pragma unroll
   for (int mf = 0; mf < FM; ++mf) sa_row[mf] = min(m0 + am + 32 * mf, M - 1) * kblocks;
   const int wave_nb = min((n0 + wn * CF::TN) / 128, nblocks_n - 1);
+  // The weight scale is wave-uniform, but it is loaded with a vector load
+  // (an opaque per-lane zero offset): a scalar load would share lgkmcnt with
+  // the LDS reads and return out of order, turning every LDS wait of the
+  // tile into lgkmcnt(0).
+  int vzero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
   float sa_c[FM], sb_c;
   auto load_scales = [&](int kb) {
-    sb_c = sB[(size_t)kb * nblocks_n + wave_nb];
+    sb_c = sB[(size_t)kb * nblocks_n + wave_nb + vzero];
 #pragma unroll
     for (int mf = 0; mf < FM; ++mf) sa_c[mf] = sA[sa_row[mf] + kb];
   };
 
-  load_scales(0);
-  issue(0, 0);
-  for (int kb = 0; kb < kblocks; ++kb) {
-    const uint32_t so = (kb & 1) * CF::STAGE;
+  // One K tile (= one scale block) in stage STG.  Reads go out in the order
+  // the MFMAs consume them; the A^T fragment of each k half is re-read for
+  // the next row block right after its MFMAs are issued.  The fragments of
+  // one row block build their partials side by side, so no MFMA waits for
+  // the one just before it; each partial is promoted with one FMA per
+  // element.
+  auto tile = [&](int kb, auto stg_tag) {
+    constexpr int STG = decltype(stg_tag)::value;
+    constexpr uint32_t oa = STG * CF::A_B, ob = STG * CF::B_B;
     wait_vmcnt<0>();  // this wave's loads of tile kb and its scales landed
-    __syncthreads();  // tile kb visible to all waves; the other stage is free
+    lds_barrier();    // tile kb visible to all waves; the other stage is free
     float s_m[FM];
 #pragma unroll
     for (int mf = 0; mf < FM; ++mf) s_m[mf] = sa_c[mf] * sb_c;
     if (kb + 1 < kblocks) {
       load_scales(kb + 1);
-      issue(kb + 1, (kb & 1) ^ 1);
+      issue(kb + 1, STG ^ 1);
     }
-
-    i32x8 bf[2][FN];
+    auto read_b = [&](int ks, int nf) {
+      u32x2 v[4];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+      for (int r = 0; r < 4; ++r) v[r] = lds_read_tr8_at(b_col[nf] + ob + (64 * ks + 8 * r) * BN);
+      return i32x8{(int)v[0][0], (int)v[0][1], (int)v[1][0], (int)v[1][1],
+                   (int)v[2][0], (int)v[2][1], (int)v[3][0], (int)v[3][1]};
+    };
+    auto read_a = [&](int mf, int ks) {
+      const uint32_t r = oa + 32 * mf * BK;
+      const u32x4 lo = lds_ld128(a_col[ks][0] + r);
+      const u32x4 hi = lds_ld128(a_col[ks][1] + r);
+      return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    };
+    i32x8 bf[2][FN], a[2];
+    bf[0][0] = read_b(0, 0);
+    a[0] = read_a(0, 0);
 #pragma unroll
-      for (int nf = 0; nf < FN; ++nf) {
-        u32x2 v[4];
+    for (int nf = 1; nf < FN; ++nf) bf[0][nf] = read_b(0, nf);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = lds_read_tr8_at(b_col[nf] + so + (64 * ks + 8 * r) * BN);
-        bf[ks][nf] = i32x8{(int)v[0][0], (int)v[0][1], (int)v[1][0], (int)v[1][1],
-                           (int)v[2][0], (int)v[2][1], (int)v[3][0], (int)v[3][1]};
-      }
-
-    // Two MFMAs per fragment into a fresh partial; the promotion of one
-    // fragment trails the MFMAs of the next.
-    f32x16 p[2];
+    for (int nf = 0; nf < FN; ++nf) bf[1][nf] = read_b(1, nf);
+    a[1] = read_a(0, 1);
 #pragma unroll
     for (int mf = 0; mf < FM; ++mf) {
-      i32x8 af[2];
+      f32x16 p[FN];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const uint32_t r = so + 32 * mf * BK;
-        const u32x4 lo = lds_ld128(a_col[ks][0] + r);
-        const u32x4 hi = lds_ld128(a_col[ks][1] + r);
-        af[ks] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      }
+      for (int nf = 0; nf < FN; ++nf) p[nf] = mfma32_fp8(bf[0][nf], a[0], f32x16{});
+      if (mf + 1 < FM) a[0] = read_a(mf + 1, 0);
 #pragma unroll
-      for (int nf = 0; nf < FN; ++nf) {
-        const int f = mf * FN + nf;
-        const f32x16 x = mfma32_fp8(bf[0][nf], af[0], f32x16{});
-        p[f & 1] = mfma32_fp8(bf[1][nf], af[1], x);
-        if (f > 0) {
-          const int g = f - 1;
-          acc[g % FN][g / FN] += s_m[g / FN] * p[g & 1];
-        }
-      }
+      for (int nf = 0; nf < FN; ++nf) p[nf] = mfma32_fp8(bf[1][nf], a[1], p[nf]);
+      if (mf + 1 < FM) a[1] = read_a(mf + 1, 1);
+#pragma unroll
+      for (int nf = 0; nf < FN; ++nf) acc[nf][mf] += s_m[mf] * p[nf];
     }
-    {
-      const int g = FM * FN - 1;
-      acc[g % FN][g / FN] += s_m[g / FN] * p[g & 1];
-    }
+  };
+
+  load_scales(0);
+  issue(0, 0);
+  for (int kb = 0; kb < kblocks; kb += 2) {
+    tile(kb, std::integral_constant<int, 0>{});
+    if (kb + 1 < kblocks) tile(kb + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- store C: lane holds m = m0 + am + 32 mf, n = n0 + wn*TN + 32 nf + 8 i + 4 (l/32) + j ----
