@@ -259,9 +259,11 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 
   // ---- values of stage pi: O^T[128 wave + 32 dt .., heads] += V^T . P^T ----
   auto values = [&](int pi) {
+    // all four flags in one LDS read (one wait instead of four)
+    const u32x4 fl = *reinterpret_cast<const u32x4*>(smem + F_OFF + (pi & 1) * NWAVES * 4);
 #pragma unroll
     for (int g = 0; g < NWAVES; ++g) {
-      const int f = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int*>(smem + F_OFF)[(pi & 1) * NWAVES + g]);
+      const int f = __builtin_amdgcn_readfirstlane(fl[g]);
       if (f) {
         const float c = reinterpret_cast<const float*>(smem + C_OFF)[((pi & 1) * NWAVES + g) * 32 + l32];
 #pragma unroll
@@ -270,24 +272,27 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
     }
     const unsigned char* lat = smem + (pi & (NLAT - 1)) * LAT_B;
     const u32x4* pbuf = reinterpret_cast<const u32x4*>(smem + P_OFF + (pi & 1) * P_BUF);
+    // V^T fragments of both k halves are read up front (the second half's
+    // reads overlap the first half's MFMAs).
+    u32x4 vf[2][VTW];
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      const unsigned char* vb = lat + 16 * k2 * 1024;
-      u32x4 vf[VTW];
+    for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
       for (int dt = 0; dt < VTW; ++dt) {
-        const unsigned char* p = vb + ((dt & 1) ? v_off_o : v_off_e) + 128 * (dt >> 1);
+        const unsigned char* p = lat + 16 * k2 * 1024 + ((dt & 1) ? v_off_o : v_off_e) + 128 * (dt >> 1);
         const u32x2 lo = lds_read_tr16(p);
         const u32x2 hi = lds_read_tr16(p + 8 * 1024);
-        vf[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        vf[k2][dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
       u32x4 pb[2];
       pb[0] = pbuf[k2 * 64 + lane];
 #pragma unroll
       for (int g = 0; g < NWAVES; ++g) {
         if (g + 1 < NWAVES) pb[(g + 1) & 1] = pbuf[((g + 1) * 2 + k2) * 64 + lane];
 #pragma unroll
-        for (int dt = 0; dt < VTW; ++dt) acc[g][dt] = mfma32<BF16>(vf[dt], pb[g & 1], acc[g][dt]);
+        for (int dt = 0; dt < VTW; ++dt) acc[g][dt] = mfma32<BF16>(vf[k2][dt], pb[g & 1], acc[g][dt]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -374,11 +379,13 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 
 // Merge the per-split softmax states:  o = sum_s w_s o_s / sum_s w_s,
 // w_s = l_s 2^(m_s - max_s m_s), o_s the normalised split output.  One
-// thread per 4 latent columns of a (b, 32-head group) tile (4096 of them,
-// 16 workgroups of 256), so the merge spreads over the whole GPU; the
-// split loop is batched for memory parallelism.
+// thread per 16 bytes of a (b, 32-head group) partial tile: the adjacent
+// lanes 2p, 2p+1 of one slot, i.e. 4 latent columns of two heads (2048
+// threads, 8 workgroups of 256 per tile), so the merge spreads over the
+// whole GPU with 128-bit loads; the split loop is batched for memory
+// parallelism.
 constexpr int CMB_WG = 256;
-constexpr int CMB_PER = VT * 4 * 64 / CMB_WG;  // workgroups per (b, 32-head group) = 16
+constexpr int CMB_PER = VT * 4 * 32 / CMB_WG;  // workgroups per (b, 32-head group) = 8
 
 __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __restrict__ ws_o,
                                                             const float* __restrict__ ws_ml,
@@ -387,44 +394,55 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
   const int gi = blockIdx.x / CMB_PER;          // b * HW + hw
   const int part = blockIdx.x % CMB_PER;
   const int b = gi / HW, hw = gi % HW;
-  const int idx = part * CMB_WG + threadIdx.x;  // slot * 64 + lane
-  const int lane = idx & 63, slot = idx >> 6;
-  const int l32 = lane & 31, hsel = lane >> 5;
-  const int head = hw * HPW + l32;
+  const int idx = part * CMB_WG + threadIdx.x;  // slot * 32 + lane pair
+  const int lp = idx & 31, slot = idx >> 5;
+  const int lane0 = 2 * lp;                     // lanes lane0, lane0 + 1
+  const int l32 = lane0 & 31, hsel = lane0 >> 5;
   const size_t g0 = (size_t)b * nsplit * HW + hw;  // tile of split 0; split stride HW
-  const float* ml = ws_ml + g0 * 64 + 2 * l32;
-  float mmax = -1e30f;
-  for (int s = 0; s < nsplit; ++s) mmax = fmaxf(mmax, ml[(size_t)s * HW * 64]);
-  f32x4 o{0.f, 0.f, 0.f, 0.f};
-  float l = 0.f;
-  const uint32_t* po = ws_o + g0 * PT_U32 + (size_t)idx * 2;
+  const float* ml = ws_ml + g0 * 64 + 2 * l32;     // (m, l) of heads l32, l32 + 1
+  float2 mmax{-1e30f, -1e30f};
+  for (int s = 0; s < nsplit; ++s) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(ml + (size_t)s * HW * 64);
+    mmax.x = fmaxf(mmax.x, x[0]);
+    mmax.y = fmaxf(mmax.y, x[2]);
+  }
+  f32x4 o0{0.f, 0.f, 0.f, 0.f}, o1{0.f, 0.f, 0.f, 0.f};
+  float l0 = 0.f, l1 = 0.f;
+  const uint32_t* po = ws_o + g0 * PT_U32 + ((size_t)slot * 64 + lane0) * 2;
   const size_t sstride = (size_t)HW * PT_U32;
-  auto acc1 = [&](const u32x2 p, const float2 mlv) {
-    const float w = mlv.y * __builtin_amdgcn_exp2f(mlv.x - mmax);
-    l += w;
-    o += w * f32x4{bf16_bits_to_f32(p[0] & 0xffffu), bf16_bits_to_f32(p[0] >> 16), bf16_bits_to_f32(p[1] & 0xffffu),
-                   bf16_bits_to_f32(p[1] >> 16)};
+  auto acc1 = [&](const u32x4 p, const f32x4 mlv) {
+    const float w0 = mlv[1] * __builtin_amdgcn_exp2f(mlv[0] - mmax.x);
+    const float w1 = mlv[3] * __builtin_amdgcn_exp2f(mlv[2] - mmax.y);
+    l0 += w0;
+    l1 += w1;
+    o0 += w0 * f32x4{bf16_bits_to_f32(p[0] & 0xffffu), bf16_bits_to_f32(p[0] >> 16),
+                     bf16_bits_to_f32(p[1] & 0xffffu), bf16_bits_to_f32(p[1] >> 16)};
+    o1 += w1 * f32x4{bf16_bits_to_f32(p[2] & 0xffffu), bf16_bits_to_f32(p[2] >> 16),
+                     bf16_bits_to_f32(p[3] & 0xffffu), bf16_bits_to_f32(p[3] >> 16)};
   };
   // Eight splits per batch of loads: all independent, issued together.
   int s = 0;
   for (; s + 8 <= nsplit; s += 8) {
-    u32x2 p[8];
-    float2 mlv[8];
+    u32x4 p[8];
+    f32x4 mlv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      p[u] = ld64(po + (size_t)(s + u) * sstride);
-      mlv[u] = *reinterpret_cast<const float2*>(ml + (size_t)(s + u) * HW * 64);
+      p[u] = ld128(po + (size_t)(s + u) * sstride);
+      mlv[u] = *reinterpret_cast<const f32x4*>(ml + (size_t)(s + u) * HW * 64);
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc1(p[u], mlv[u]);
   }
   for (; s < nsplit; ++s)
-    acc1(ld64(po + (size_t)s * sstride), *reinterpret_cast<const float2*>(ml + (size_t)s * HW * 64));
-  if (head >= H) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+    acc1(ld128(po + (size_t)s * sstride), *reinterpret_cast<const f32x4*>(ml + (size_t)s * HW * 64));
   const int vt = slot >> 2, i = slot & 3;
-  st64(O + ((size_t)b * H + head) * DV + 32 * vt + 8 * i + 4 * hsel,
-       u32x2{pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)});
+  const int head0 = hw * HPW + l32;
+  const float inv0 = l0 > 0.f ? 1.f / l0 : 0.f, inv1 = l1 > 0.f ? 1.f / l1 : 0.f;
+  uint16_t* orow = O + ((size_t)b * H + head0) * DV + 32 * vt + 8 * i + 4 * hsel;
+  if (head0 < H)
+    st64(orow, u32x2{pack_bf16x2(o0[0] * inv0, o0[1] * inv0), pack_bf16x2(o0[2] * inv0, o0[3] * inv0)});
+  if (head0 + 1 < H)
+    st64(orow + DV, u32x2{pack_bf16x2(o1[0] * inv1, o1[1] * inv1), pack_bf16x2(o1[2] * inv1, o1[3] * inv1)});
 }
 
 inline size_t workspace_bytes(int B, int H, int T) {
