@@ -4,9 +4,10 @@ Headline (the `value` of the JSON line): the fused causal GQA forward at
 BASELINE configs[1] — B=1, Hq=32, Hkv=8, S=4096, D=128, bf16, N(0,1)
 inputs, scale 1/sqrt(128) — reported in algorithmic TFLOP/s (causal work
 2*B*Hq*D*S*(S+1)).  A "step" is one forward pass over that batch with
-inputs already resident in HBM.  The other four kernels (bf16 GEMM at
-1024^3 and 8192^3, fp8 block-scaled GEMM at 8192^3, MLA absorbed decode,
-GDN decode) are measured the same way and reported under "others".
+inputs already resident in HBM.  The other kernels (bf16 GEMM at 1024^3
+and 8192^3, fp8 block-scaled GEMM at 8192^3, MLA absorbed decode, GDN
+decode, KDA decode at the reference's "large" shape) are measured the same
+way and reported under "others".
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        [--only-headline]
@@ -191,6 +192,20 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
         "frac_hbm_peak_mean": F.gbps(nb, ms) / F.PEAK_HBM_GBPS,
     }
     log(f"gdn_decode: {res['gdn_decode']['gbps_mean']:.0f} GB/s mean")
+    del x, so, od
+
+    shape = S.KDA_LARGE
+    x = {n: t.cuda() for n, t in I.kda_inputs(shape).items()}
+    so = torch.empty_like(x["S_in"])
+    od = torch.empty((shape.batch, shape.n_heads, shape.d_v), dtype=torch.float16, device="cuda")
+    ms, _ = time_launches(lambda: ops.kda_decode(x["q"], x["k"], x["v"], x["g"], x["beta"], x["S_in"],
+                                                 S_out=so, o=od), steps, warmup)
+    nb = F.kda_decode_bytes(shape)
+    res["kda_decode"] = {
+        "unit": "GB/s", "shape": f"B{shape.batch} H{shape.n_heads} d{shape.d_k}", "mean_us": ms * 1e3,
+        "gbps_mean": F.gbps(nb, ms), "frac_hbm_peak_mean": F.gbps(nb, ms) / F.PEAK_HBM_GBPS,
+    }
+    log(f"kda_decode: {res['kda_decode']['gbps_mean']:.0f} GB/s mean")
     return res
 
 

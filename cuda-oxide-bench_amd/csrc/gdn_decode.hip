@@ -1,4 +1,5 @@
-// Gated-DeltaNet single-token decode for gfx950.
+// Gated-DeltaNet (GDN) and Kimi-Delta-Attention (KDA) single-token decode
+// for gfx950.
 //
 // Math (per batch b, value head hv, key head hk = hv / (Hv/Hk)), following
 // analysis/wave15-attention-architecture/reference/pytorch_reference_gdn.py:38-91
@@ -10,6 +11,13 @@
 // The output is formed without a second pass over S' through
 //     o = alpha (q^T S) + beta (q.k) r,
 // so both reductions (k^T S and q^T S) come out of the single read of S.
+//
+// KDA (cutile-attn-kda/main.py:190-272, oracle
+// analysis/wave15-attention-architecture/reference/pytorch_reference_kda.py:42-73)
+// replaces the scalar alpha by a per-row decay e = exp(g) (d_k values):
+//     u = (e*k)^T S,  r = v - u,  S' = diag(e) S + beta k r^T,
+//     o = (e*q)^T S + beta (q.k) r
+// — the same single-pass kernel with e folded into the row coefficients.
 //
 // Layout and schedule (bandwidth-bound: 2 x d_k x d_v x 4 bytes per head):
 //  * one workgroup per (b, hv, column block of BV values of d_v) — every
@@ -28,18 +36,27 @@
 namespace mx {
 namespace gdn {
 
-template <int DK, int BV, typename T>
+// Gate inputs of one launch.  GDN: scalar decay alpha and beta per (b, hv),
+// fp32.  KDA: per-channel log-gate g[b, h, 0..d_k) and beta[b, h] in the
+// 16-bit I/O type, decay exp(g).
+struct Gates {
+  const float* alpha;      // GDN
+  const float* beta;       // GDN
+  const uint16_t* g;       // KDA
+  const uint16_t* beta16;  // KDA
+};
+
+template <int DK, int BV, typename T, bool KDA>
 __global__ __launch_bounds__(DK * BV / 64) void gdn_decode_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const float* __restrict__ alpha, const float* __restrict__ beta, const float* S_in, float* S_out,
-    uint16_t* __restrict__ o, int Hk, int Hv, int DV) {
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, Gates gt,
+    const float* S_in, float* S_out, uint16_t* __restrict__ o, int Hk, int Hv, int DV) {
   constexpr int NT = DK * BV / 64;
   constexpr int TC = BV / 4;   // threads across a row segment
   constexpr int RG = NT / TC;  // row groups (= DK / 16)
   constexpr int RPT = DK / RG; // rows per thread (= 16)
   static_assert(RPT == 16, "16 rows per thread");
 
-  __shared__ float qs[DK], ks[DK];
+  __shared__ float qs[DK], ks[DK], es[KDA ? DK : 1];
   __shared__ __align__(16) float red_u[RG][BV];
   __shared__ __align__(16) float red_w[RG][BV];
   __shared__ float red_qk[RG];
@@ -74,23 +91,32 @@ __global__ __launch_bounds__(DK * BV / 64) void gdn_decode_kernel(
   for (int i = t; i < DK; i += NT) {
     qs[i] = T::to_f32(q[qkbase + i]);
     ks[i] = T::to_f32(k[qkbase + i]);
+    if constexpr (KDA) es[i] = expf(T::to_f32(gt.g[(size_t)bh * DK + i]));
   }
   const size_t vbase = (size_t)bh * DV + c0;
   const u32x2 vv = ld64(v + vbase);
   const float vf[4] = {T::to_f32(vv[0] & 0xffffu), T::to_f32(vv[0] >> 16), T::to_f32(vv[1] & 0xffffu),
                        T::to_f32(vv[1] >> 16)};
-  const float a = alpha[bh], be = beta[bh];
+  // GDN: the scalar decay multiplies the reductions once at the end (a);
+  // KDA: each row's decay e_i is folded into that row's coefficients.
+  const float a = KDA ? 1.f : gt.alpha[bh];
+  const float be = KDA ? T::to_f32(gt.beta16[bh]) : gt.beta[bh];
   __syncthreads();
 
   float u[4] = {0.f, 0.f, 0.f, 0.f}, w[4] = {0.f, 0.f, 0.f, 0.f};
   float qk = 0.f;
-  float kr[RPT];
+  float kr[RPT], er[KDA ? RPT : 1];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
     const int i = rg + RG * r;
-    const float ki = ks[i], qi = qs[i];
+    float ki = ks[i], qi = qs[i];
     kr[r] = ki;
     qk = fmaf(qi, ki, qk);
+    if constexpr (KDA) {
+      er[r] = es[i];
+      ki *= er[r];
+      qi *= er[r];
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       u[c] = fmaf(ki, s[r][c], u[c]);
@@ -122,9 +148,10 @@ __global__ __launch_bounds__(DK * BV / 64) void gdn_decode_kernel(
   for (int r = 0; r < RPT; ++r) {
     const int i = rg + RG * r;
     const float bk = be * kr[r];
+    const float ar = KDA ? er[r] : a;
     f32x4 nv;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) nv[c] = fmaf(bk, res[c], a * s[r][c]);
+    for (int c = 0; c < 4; ++c) nv[c] = fmaf(bk, res[c], ar * s[r][c]);
     st128_nt(Sout + (size_t)i * DV + c0, __builtin_bit_cast(u32x4, nv));
   }
   if (rg == 0) {
@@ -132,37 +159,43 @@ __global__ __launch_bounds__(DK * BV / 64) void gdn_decode_kernel(
   }
 }
 
-template <int DK, int BV, typename T>
-static int launch(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
-                  const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dv, hipStream_t s) {
+template <int DK, int BV, typename T, bool KDA>
+static int launch(const void* q, const void* k, const void* v, const Gates& gt, const float* S_in, float* S_out,
+                  void* o, int B, int Hk, int Hv, int dv, hipStream_t s) {
   const long long grid = (long long)B * Hv * (dv / BV);
   if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
-  hipLaunchKernelGGL((gdn_decode_kernel<DK, BV, T>), dim3((unsigned)grid), dim3(DK * BV / 64), 0, s,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, alpha, beta, S_in, S_out,
-                     (uint16_t*)o, Hk, Hv, dv);
+  hipLaunchKernelGGL((gdn_decode_kernel<DK, BV, T, KDA>), dim3((unsigned)grid), dim3(DK * BV / 64), 0, s,
+                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, gt, S_in, S_out, (uint16_t*)o, Hk,
+                     Hv, dv);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
 }
 
-// Column-block width: the widest of {d_v, d_v/2, ...} (>= 16 and >= 4096/d_k,
-// i.e. at least one wave per workgroup) that still gives >= 4096 workgroups
-// (16 per CU: small workgroups keep the last wave of the grid short); the
-// narrowest allowed one otherwise.  At B=64, Hv=32, d=128 this is 64
-// (4096 workgroups of 2 waves), measured ~7% faster than 128.
+// Column-block width.  Start from d_v and halve while the grid has fewer
+// than 4096 workgroups (16 per CU: small workgroups keep the last wave of
+// the grid short) but not below 64 columns (256-byte row segments stream
+// well; 64-byte ones do not: 4.0 vs 6.5 TB/s at B4 H64 d256).  Only when
+// that still leaves fewer than 1024 workgroups, keep halving down to the
+// narrowest allowed width (>= 16 and >= 4096/d_k, i.e. one wave per
+// workgroup) for parallelism.  Measured choices: B64 Hv32 d128 -> 64
+// (4096 workgroups, ~7% faster than 128), B4 H64 d256 -> 64, B1 H16 d256
+// -> 16.
 static int pick_bv(int B, int Hv, int dk, int dv) {
   const int min_bv = (4096 / dk > 16) ? 4096 / dk : 16;
+  auto groups = [&](int bv) { return (long long)B * Hv * (dv / bv); };
   int bv = dv;
-  while (bv / 2 >= min_bv && (long long)B * Hv * (dv / bv) < 4096) bv /= 2;
+  while (bv / 2 >= 64 && bv / 2 >= min_bv && groups(bv) < 4096) bv /= 2;
+  while (bv / 2 >= min_bv && groups(bv) < 1024) bv /= 2;
   return bv;
 }
 
-template <int DK, typename T>
-static int dispatch_dk(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
-                       const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dv, hipStream_t s) {
+template <int DK, typename T, bool KDA>
+static int dispatch_dk(const void* q, const void* k, const void* v, const Gates& gt, const float* S_in, float* S_out,
+                       void* o, int B, int Hk, int Hv, int dv, hipStream_t s) {
   const int bv = pick_bv(B, Hv, DK, dv);
-#define MX_GDN_BV(BV_)                                                                             \
-  if (bv == BV_) {                                                                                 \
-    if constexpr (DK * BV_ >= 4096) return launch<DK, BV_, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dv, s); \
+#define MX_GDN_BV(BV_)                                                                                     \
+  if (bv == BV_) {                                                                                         \
+    if constexpr (DK * BV_ >= 4096) return launch<DK, BV_, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s); \
   }
   MX_GDN_BV(16)
   MX_GDN_BV(32)
@@ -173,14 +206,27 @@ static int dispatch_dk(const void* q, const void* k, const void* v, const float*
   return MX_ERR_UNSUPPORTED;
 }
 
-template <typename T>
-static int dispatch(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
-                    const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dk, int dv,
-                    hipStream_t s) {
-  if (dk == 64) return dispatch_dk<64, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dv, s);
-  if (dk == 128) return dispatch_dk<128, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dv, s);
-  if (dk == 256) return dispatch_dk<256, T>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dv, s);
+template <typename T, bool KDA>
+static int dispatch(const void* q, const void* k, const void* v, const Gates& gt, const float* S_in, float* S_out,
+                    void* o, int B, int Hk, int Hv, int dk, int dv, hipStream_t s) {
+  if (dk == 64) return dispatch_dk<64, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s);
+  if (dk == 128) return dispatch_dk<128, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s);
+  if (dk == 256) return dispatch_dk<256, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s);
   return MX_ERR_UNSUPPORTED;
+}
+
+// Argument checks shared by both entry points.
+static int check_state(const float* S_in, const float* S_out, const void* v, const void* o, int B, int Hv, int dk,
+                       int dv) {
+  if (((uintptr_t)S_in | (uintptr_t)S_out) & 15) return MX_ERR_ALIGN;
+  if (((uintptr_t)v | (uintptr_t)o) & 7) return MX_ERR_ALIGN;
+  // The state may be updated in place; any other overlap would let one
+  // workgroup overwrite rows another has not read yet.
+  const size_t sbytes = (size_t)B * Hv * dk * dv * sizeof(float);
+  const char* si = (const char*)S_in;
+  const char* so = (const char*)S_out;
+  if (si != so && si < so + sbytes && so < si + sbytes) return MX_ERR_ALIAS;
+  return MX_OK;
 }
 
 }  // namespace gdn
@@ -196,16 +242,26 @@ extern "C" int mx_gdn_decode(const void* q, const void* k, const void* v, const 
   if (!mx_is_dim(dk) || !mx_is_dim(dv)) return MX_ERR_SHAPE;
   if ((long long)B * Hv > 0x7fffffffLL / 16) return MX_ERR_SHAPE;
   if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
-  if (((uintptr_t)S_in | (uintptr_t)S_out) & 15) return MX_ERR_ALIGN;
-  if (((uintptr_t)v | (uintptr_t)o) & 7) return MX_ERR_ALIGN;
-  // The state may be updated in place; any other overlap would let one
-  // workgroup overwrite rows another has not read yet.
-  const size_t sbytes = (size_t)B * Hv * dk * dv * sizeof(float);
-  const char* si = (const char*)S_in;
-  const char* so = (const char*)S_out;
-  if (si != so && si < so + sbytes && so < si + sbytes) return MX_ERR_ALIAS;
+  if (const int e = mx::gdn::check_state(S_in, S_out, v, o, B, Hv, dk, dv)) return e;
   hipStream_t s = (hipStream_t)stream;
+  const mx::gdn::Gates gt{alpha, beta, nullptr, nullptr};
   if (dtype == MX_DTYPE_BF16)
-    return mx::gdn::dispatch<mx::BF16>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dk, dv, s);
-  return mx::gdn::dispatch<mx::F16>(q, k, v, alpha, beta, S_in, S_out, o, B, Hk, Hv, dk, dv, s);
+    return mx::gdn::dispatch<mx::BF16, false>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dk, dv, s);
+  return mx::gdn::dispatch<mx::F16, false>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dk, dv, s);
+}
+
+extern "C" int mx_kda_decode(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                             const float* S_in, float* S_out, void* o, int B, int H, int dk, int dv, int dtype,
+                             void* stream) {
+  if (!q || !k || !v || !g || !beta || !S_in || !S_out || !o) return MX_ERR_NULL;
+  if (B <= 0 || H <= 0) return MX_ERR_SHAPE;
+  if (!mx_is_dim(dk) || !mx_is_dim(dv)) return MX_ERR_SHAPE;
+  if ((long long)B * H > 0x7fffffffLL / 16) return MX_ERR_SHAPE;
+  if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
+  if (const int e = mx::gdn::check_state(S_in, S_out, v, o, B, H, dk, dv)) return e;
+  hipStream_t s = (hipStream_t)stream;
+  const mx::gdn::Gates gt{nullptr, nullptr, (const uint16_t*)g, (const uint16_t*)beta};
+  if (dtype == MX_DTYPE_BF16)
+    return mx::gdn::dispatch<mx::BF16, true>(q, k, v, gt, S_in, S_out, o, B, H, H, dk, dv, s);
+  return mx::gdn::dispatch<mx::F16, true>(q, k, v, gt, S_in, S_out, o, B, H, H, dk, dv, s);
 }

@@ -81,6 +81,18 @@ def gdn_decode_bytes(s: GDNShape, io_bytes: int = 2, gate_bytes: int = 4) -> int
     return state + qk + vo + gates
 
 
+def kda_decode_flops(s) -> int:
+    """6*B*H*d_k*d_v (cutile-attn-kda/main.py:111-113)."""
+    return 6 * s.batch * s.n_heads * s.d_k * s.d_v
+
+
+def kda_decode_bytes(s, io_bytes: int = 2) -> int:
+    """fp32 state read + written, plus q, k, g (d_k each), v, o (d_v each)
+    and beta in the 16-bit I/O type per (b, h) (cutile-attn-kda/main.py:116-126)."""
+    bh = s.batch * s.n_heads
+    return bh * (2 * s.d_k * s.d_v * 4 + (3 * s.d_k + 2 * s.d_v + 1) * io_bytes)
+
+
 def tflops(flops: int, ms: float) -> float:
     return flops / (ms * 1e-3) / 1e12
 

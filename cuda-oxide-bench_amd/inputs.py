@@ -19,7 +19,7 @@ import numpy as np
 import torch
 
 from .quant import quantize_fp8_blockwise
-from .shapes import FP8GemmShape, GDNShape, GemmShape, GQAShape, MLADecodeShape
+from .shapes import FP8GemmShape, GDNShape, GemmShape, GQAShape, KDAShape, MLADecodeShape
 
 SEED = 0xC0FFEE
 SAMPLE_SEED = 0xBEEF
@@ -110,3 +110,26 @@ def gdn_inputs(s: GDNShape, dtype: torch.dtype = torch.bfloat16, seed: int = SEE
         "q": q.to(dtype), "k": k.to(dtype), "v": v.to(dtype),
         "alpha": alpha.contiguous(), "beta": beta.contiguous(), "S_in": S.contiguous(),
     }
+
+
+KDA_SEED = 17
+
+
+def kda_inputs(s: KDAShape, dtype: torch.dtype = torch.float16, seed: int = KDA_SEED):
+    """The reference's KDA recipe (cutile-attn-kda/main.py:286-310), restated
+    draw for draw on numpy's default_rng: q, k ~ N(0,1)/sqrt(d_k), v ~ N(0,1),
+    g = -|N(0,1)|/2 (decay exp(g) in (~0.6, 1]), beta ~ U(0.1, 0.9),
+    S_in ~ 0.1 N(0,1) fp32; the 16-bit inputs are rounded from float32 the
+    way the reference's astype(np.float16) does (round to nearest even).
+    Returns dict q, k, g [B,H,dk]; v [B,H,dv]; beta [B,H] in `dtype`; S_in fp32."""
+    rng = np.random.default_rng(seed)
+    B, Hh, dk, dv = s.batch, s.n_heads, s.d_k, s.d_v
+    scale_k = 1.0 / np.sqrt(dk)
+    q = (rng.standard_normal((B, Hh, dk)) * scale_k).astype(np.float32)
+    k = (rng.standard_normal((B, Hh, dk)) * scale_k).astype(np.float32)
+    v = rng.standard_normal((B, Hh, dv)).astype(np.float32)
+    gg = (-np.abs(rng.standard_normal((B, Hh, dk))) * 0.5).astype(np.float32)
+    beta = rng.uniform(0.1, 0.9, size=(B, Hh)).astype(np.float32)
+    S = (rng.standard_normal((B, Hh, dk, dv)) * 0.1).astype(np.float32)
+    t = lambda x: torch.from_numpy(x).to(dtype)  # noqa: E731
+    return {"q": t(q), "k": t(k), "v": t(v), "g": t(gg), "beta": t(beta), "S_in": torch.from_numpy(S).contiguous()}

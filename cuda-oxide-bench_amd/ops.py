@@ -198,3 +198,37 @@ def gdn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, alpha: torch.T
               S_in.data_ptr(), S_out.data_ptr(), o.data_ptr(), B, Hk, Hv, dk, dv, _IO_DTYPES[q.dtype],
               _stream())
     return o, S_out
+
+
+def kda_decode(q, k, v, g, beta, S_in, S_out=None, o=None):
+    """One KDA decode step (cutile-attn-kda/main.py:190-272): GDN with the
+    per-channel decay exp(g) on the rows of the state.  q, k, g [B,H,dk];
+    v [B,H,dv]; beta [B,H] (all bf16 or f16); S_in [B,H,dk,dv] fp32.
+    Returns (o [B,H,dv], S_out).  S_out may be S_in (in-place update)."""
+    _require(q, "q", _IO_DTYPES, 3)
+    for t, n in ((k, "k"), (v, "v"), (g, "g")):
+        _require(t, n, (q.dtype,), 3)
+    _require(beta, "beta", (q.dtype,), 2)
+    _require(S_in, "S_in", (torch.float32,), 4)
+    B, Hh, dk = q.shape
+    dv = v.shape[2]
+    if tuple(k.shape) != (B, Hh, dk) or tuple(g.shape) != (B, Hh, dk) or tuple(v.shape[:2]) != (B, Hh):
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} g {tuple(g.shape)} v {tuple(v.shape)}")
+    if tuple(beta.shape) != (B, Hh):
+        raise ValueError(f"beta must be {(B, Hh)}")
+    if tuple(S_in.shape) != (B, Hh, dk, dv):
+        raise ValueError(f"S_in must be {(B, Hh, dk, dv)}, got {tuple(S_in.shape)}")
+    if S_out is None:
+        S_out = torch.empty_like(S_in)
+    _require(S_out, "S_out", (torch.float32,), 4)
+    if S_out.shape != S_in.shape:
+        raise ValueError("S_out must match S_in")
+    if o is None:
+        o = torch.empty((B, Hh, dv), dtype=q.dtype, device=q.device)
+    _require(o, "o", (q.dtype,), 3)
+    if tuple(o.shape) != (B, Hh, dv):
+        raise ValueError(f"o must be {(B, Hh, dv)}")
+    _same_device(q, k, v, g, beta, S_in, S_out, o)
+    _lib.call("mx_kda_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+              S_in.data_ptr(), S_out.data_ptr(), o.data_ptr(), B, Hh, dk, dv, _IO_DTYPES[q.dtype], _stream())
+    return o, S_out

@@ -108,6 +108,24 @@ class GDNShape:
 
 
 @dataclass(frozen=True)
+class KDAShape:
+    """KDA decode (cutile-attn-kda/main.py:60-70): one key head per value head."""
+
+    name: str
+    batch: int
+    n_heads: int
+    d_k: int
+    d_v: int
+
+    @property
+    def state_elems(self) -> int:
+        return self.batch * self.n_heads * self.d_k * self.d_v
+
+    def assert_valid(self) -> None:
+        assert self.d_k > 0 and self.d_v > 0 and self.batch > 0 and self.n_heads > 0
+
+
+@dataclass(frozen=True)
 class FP8GemmShape:
     name: str
     m: int
@@ -154,3 +172,11 @@ GDN_REGISTRY = {s.name: s for s in (
     GDNShape("small", batch=1, n_heads=8, d_k=128, d_v=128),
     GDNShape("large", batch=4, n_heads=64, d_k=256, d_v=256),
 )}
+
+# KDA: reference registry (cutile-attn-kda/main.py:75-101).  "large" is the
+# configuration this path is measured on (it fills the GPU).
+KDA_CORRECTNESS = KDAShape("correctness", batch=1, n_heads=2, d_k=64, d_v=64)
+KDA_KIMI_LINEAR = KDAShape("kimi_linear_decode", batch=1, n_heads=32, d_k=128, d_v=128)
+KDA_QWEN3_PARITY = KDAShape("qwen3_next_gdn_parity", batch=1, n_heads=16, d_k=256, d_v=256)
+KDA_LARGE = KDAShape("large", batch=4, n_heads=64, d_k=256, d_v=256)
+KDA_REGISTRY = {s.name: s for s in (KDA_CORRECTNESS, KDA_KIMI_LINEAR, KDA_QWEN3_PARITY, KDA_LARGE)}

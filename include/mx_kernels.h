@@ -126,6 +126,25 @@ int mx_gdn_decode(const void* q, const void* k, const void* v, const float* alph
                   const float* beta, const float* S_in, float* S_out, void* o, int B, int Hk,
                   int Hv, int dk, int dv, int dtype, void* stream);
 
+/*
+ * Kimi-Delta-Attention (KDA) single-token recurrent decode: GDN with a
+ * per-channel gate.  Per (b, head h), with e = exp(g[b,h,:]) (d_k values):
+ *   S_dec = Diag(e) S
+ *   u     = k^T S_dec                        (d_v)
+ *   S_out = S_dec + beta * k (v - u)^T       (d_k x d_v, fp32)
+ *   o     = S_out^T q                        (d_v)
+ * q, k, g: [B, H, dk]; v, o: [B, H, dv]; beta: [B, H] — all in the 16-bit
+ * type `dtype` (the reference's f16 gate and beta); S_in, S_out:
+ * [B, H, dk, dv] fp32 with dv contiguous.  q is used as given (no 1/sqrt(dk)
+ * inside).  S_out may equal S_in; partial overlap is rejected.  dk and dv
+ * must be 64, 128 or 256.
+ * Replaces: cutile-attn-kda/main.py:318-321 (ct.launch of `kda_decode`,
+ * kernel at :190-272).
+ */
+int mx_kda_decode(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                  const float* S_in, float* S_out, void* o, int B, int H, int dk, int dv,
+                  int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

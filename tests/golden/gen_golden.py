@@ -26,6 +26,7 @@ from oracle import fp8 as ofp8  # noqa: E402
 from oracle import gdn as ogdn  # noqa: E402
 from oracle import gemm as ogemm  # noqa: E402
 from oracle import gqa as ogqa  # noqa: E402
+from oracle import kda as okda  # noqa: E402
 from oracle import mla as omla  # noqa: E402
 
 OUT = Path(__file__).resolve().parent
@@ -88,6 +89,12 @@ def main() -> int:
     save("gdn_grouped_bf16", q=bits16(x["q"]), k=bits16(x["k"]), v=bits16(x["v"]),
          alpha=x["alpha"].numpy(), beta=x["beta"].numpy(), S_in=x["S_in"].numpy(),
          o=o.numpy(), S_out=so.numpy())
+
+    # KDA: the reference's correctness shape and recipe (f16, seed 17).
+    x = inputs.kda_inputs(S.KDA_CORRECTNESS)
+    o, so = okda.kda_decode_ref(**x)
+    save("kda_correctness_f16", q=bits16(x["q"]), k=bits16(x["k"]), v=bits16(x["v"]), g=bits16(x["g"]),
+         beta=bits16(x["beta"]), S_in=x["S_in"].numpy(), o=o, S_out=so)
     return 0
 
 

@@ -24,7 +24,7 @@ def declared_functions() -> list[str]:
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("mx_gemm_bf16", "mx_gemm_fp8_bs", "mx_gqa_fwd", "mx_mla_decode", "mx_mla_decode_workspace",
-              "mx_gdn_decode", "mx_strerror", "mx_version"):
+              "mx_gdn_decode", "mx_kda_decode", "mx_strerror", "mx_version"):
         assert n in names
 
 
@@ -97,3 +97,15 @@ def test_gdn_validation():
     assert f(*args, 2, 2, 4, 64, 64, 3, None) == _lib.MX_ERR_DTYPE
     s_in, s_out = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x100000 + 256)
     assert f(P, P, P, P, P, s_in, s_out, P, 2, 2, 4, 64, 64, 0, None) == _lib.MX_ERR_ALIAS
+
+
+def test_kda_validation():
+    f = _lib.load().mx_kda_decode
+    args = [P] * 8
+    assert f(None, *args[1:], 2, 4, 64, 64, 0, None) == _lib.MX_ERR_NULL
+    assert f(*args[:3], None, *args[4:], 2, 4, 64, 64, 0, None) == _lib.MX_ERR_NULL   # g
+    assert f(*args, 0, 4, 64, 64, 0, None) == _lib.MX_ERR_SHAPE
+    assert f(*args, 2, 4, 96, 64, 0, None) == _lib.MX_ERR_SHAPE      # dk
+    assert f(*args, 2, 4, 64, 64, 3, None) == _lib.MX_ERR_DTYPE
+    s_in, s_out = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x100000 + 256)
+    assert f(P, P, P, P, P, s_in, s_out, P, 2, 4, 64, 64, 0, None) == _lib.MX_ERR_ALIAS

@@ -16,6 +16,7 @@ CELLS = {
                      "--iters"],
     "hip-attn-mla": ["--smoke", "--bench", "--export-cubin", "--csv-out", "--cubin-out"],
     "hip-attn-gdn": ["--smoke", "--bench", "--export-cubin", "--csv-out", "--cubin-out", "--shape"],
+    "hip-attn-kda": ["--smoke", "--bench", "--export-cubin", "--csv-out", "--cubin-out", "--shape"],
 }
 
 

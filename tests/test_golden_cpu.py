@@ -10,6 +10,7 @@ from oracle import fp8 as ofp8
 from oracle import gdn as ogdn
 from oracle import gemm as ogemm
 from oracle import gqa as ogqa
+from oracle import kda as okda
 from oracle import mla as omla
 
 shapes = import_submodule("shapes")
@@ -50,3 +51,13 @@ def test_gdn_fixtures():
              "S_in": torch.from_numpy(g["S_in"])}
         o, s = ogdn.gdn_decode_ref(**x)
         assert np.allclose(o.numpy(), g["o"], atol=1e-6) and np.allclose(s.numpy(), g["S_out"], atol=1e-7)
+
+
+def test_kda_fixture():
+    g = load_golden("kda_correctness_f16")
+    x = inputs.kda_inputs(shapes.KDA_CORRECTNESS)
+    for n in ("q", "k", "v", "g", "beta"):
+        assert torch.equal(from_bits(g[n], torch.float16), x[n])
+    assert np.array_equal(g["S_in"], x["S_in"].numpy())
+    o, s = okda.kda_decode_ref(**x)
+    assert np.array_equal(o, g["o"]) and np.array_equal(s, g["S_out"])
