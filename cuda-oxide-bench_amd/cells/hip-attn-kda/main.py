@@ -6,7 +6,7 @@ kimi_linear_decode, as bench.py), --export-cubin / --cubin-out (accepted).
 --smoke runs the reference's SHAPE_CORRECTNESS (B1 H2 d64, f16, the
 reference's seed-17 recipe) against the committed golden oracle output with
 the reference's gate (max_abs <= 1e-3 or rel <= 1e-3 on o and S,
-main.py:370-382) and this path's normwise bounds (o 2e-2, S 1e-3).  --bench
+main.py:374-380) and this path's normwise bounds (o 2e-2, S 1e-3).  --bench
 uses 2 warm-up + 50 timed launches and writes results.csv with the
 reference columns (impl,kernel,batch,n_heads,d_k,d_v,block_v,iter,gpu_us,
 gbps,tflops) plus dtype,frac_hbm at the end, and a roofline.json sidecar.

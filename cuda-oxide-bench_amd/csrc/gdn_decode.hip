@@ -12,7 +12,7 @@
 //     o = alpha (q^T S) + beta (q.k) r,
 // so both reductions (k^T S and q^T S) come out of the single read of S.
 //
-// KDA (cutile-attn-kda/main.py:190-272, oracle
+// KDA (cutile-attn-kda/main.py:187-271, oracle
 // analysis/wave15-attention-architecture/reference/pytorch_reference_kda.py:42-73)
 // replaces the scalar alpha by a per-row decay e = exp(g) (d_k values):
 //     u = (e*k)^T S,  r = v - u,  S' = diag(e) S + beta k r^T,

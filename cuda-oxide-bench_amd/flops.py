@@ -82,13 +82,13 @@ def gdn_decode_bytes(s: GDNShape, io_bytes: int = 2, gate_bytes: int = 4) -> int
 
 
 def kda_decode_flops(s) -> int:
-    """6*B*H*d_k*d_v (cutile-attn-kda/main.py:111-113)."""
+    """6*B*H*d_k*d_v (cutile-attn-kda/main.py:112-114)."""
     return 6 * s.batch * s.n_heads * s.d_k * s.d_v
 
 
 def kda_decode_bytes(s, io_bytes: int = 2) -> int:
     """fp32 state read + written, plus q, k, g (d_k each), v, o (d_v each)
-    and beta in the 16-bit I/O type per (b, h) (cutile-attn-kda/main.py:116-126)."""
+    and beta in the 16-bit I/O type per (b, h) (cutile-attn-kda/main.py:117-128)."""
     bh = s.batch * s.n_heads
     return bh * (2 * s.d_k * s.d_v * 4 + (3 * s.d_k + 2 * s.d_v + 1) * io_bytes)
 

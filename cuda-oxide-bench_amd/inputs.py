@@ -116,7 +116,7 @@ KDA_SEED = 17
 
 
 def kda_inputs(s: KDAShape, dtype: torch.dtype = torch.float16, seed: int = KDA_SEED):
-    """The reference's KDA recipe (cutile-attn-kda/main.py:286-310), restated
+    """The reference's KDA recipe (cutile-attn-kda/main.py:282-305), restated
     draw for draw on numpy's default_rng: q, k ~ N(0,1)/sqrt(d_k), v ~ N(0,1),
     g = -|N(0,1)|/2 (decay exp(g) in (~0.6, 1]), beta ~ U(0.1, 0.9),
     S_in ~ 0.1 N(0,1) fp32; the 16-bit inputs are rounded from float32 the

@@ -201,7 +201,7 @@ def gdn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, alpha: torch.T
 
 
 def kda_decode(q, k, v, g, beta, S_in, S_out=None, o=None):
-    """One KDA decode step (cutile-attn-kda/main.py:190-272): GDN with the
+    """One KDA decode step (cutile-attn-kda/main.py:187-271): GDN with the
     per-channel decay exp(g) on the rows of the state.  q, k, g [B,H,dk];
     v [B,H,dv]; beta [B,H] (all bf16 or f16); S_in [B,H,dk,dv] fp32.
     Returns (o [B,H,dv], S_out).  S_out may be S_in (in-place update)."""

@@ -109,7 +109,7 @@ class GDNShape:
 
 @dataclass(frozen=True)
 class KDAShape:
-    """KDA decode (cutile-attn-kda/main.py:60-70): one key head per value head."""
+    """KDA decode (cutile-attn-kda/main.py:64-74): one key head per value head."""
 
     name: str
     batch: int
@@ -173,7 +173,7 @@ GDN_REGISTRY = {s.name: s for s in (
     GDNShape("large", batch=4, n_heads=64, d_k=256, d_v=256),
 )}
 
-# KDA: reference registry (cutile-attn-kda/main.py:75-101).  "large" is the
+# KDA: reference registry (cutile-attn-kda/main.py:77-104).  "large" is the
 # configuration this path is measured on (it fills the GPU).
 KDA_CORRECTNESS = KDAShape("correctness", batch=1, n_heads=2, d_k=64, d_v=64)
 KDA_KIMI_LINEAR = KDAShape("kimi_linear_decode", batch=1, n_heads=32, d_k=128, d_v=128)

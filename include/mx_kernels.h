@@ -138,8 +138,8 @@ int mx_gdn_decode(const void* q, const void* k, const void* v, const float* alph
  * [B, H, dk, dv] fp32 with dv contiguous.  q is used as given (no 1/sqrt(dk)
  * inside).  S_out may equal S_in; partial overlap is rejected.  dk and dv
  * must be 64, 128 or 256.
- * Replaces: cutile-attn-kda/main.py:318-321 (ct.launch of `kda_decode`,
- * kernel at :190-272).
+ * Replaces: cutile-attn-kda/main.py:357-360 (ct.launch of `kda_decode`,
+ * kernel at :187-271; bench launches at :428, :438).
  */
 int mx_kda_decode(const void* q, const void* k, const void* v, const void* g, const void* beta,
                   const float* S_in, float* S_out, void* o, int B, int H, int dk, int dv,

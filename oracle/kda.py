@@ -5,7 +5,7 @@ instead of a scalar alpha (docs/adrs/0006-kda-as-gdn-extension.md:5-16).
 
 kda_decode_ref restates naive_recurrent_kda_step of
 analysis/wave15-attention-architecture/reference/pytorch_reference_kda.py:42-73
-(also cutile-attn-kda/main.py:145-176): float64 numpy, q used as given
+(also cutile-attn-kda/main.py:147-179): float64 numpy, q used as given
 (scale 1.0, the harness convention), order decay -> residual -> rank-1
 update -> read-out.
 

@@ -1,6 +1,6 @@
 """KDA decode parity on the GPU vs the CPU oracle (pytorch_reference_kda.py:42-73,
 fp64).  Bounds: the reference's own acceptance gate, max_abs <= 1e-3 or
-rel <= 1e-3 on o and on S (cutile-attn-kda/main.py:370-382), plus this
+rel <= 1e-3 on o and on S (cutile-attn-kda/main.py:374-380), plus this
 path's normwise bounds (o <= 2e-2 for the 16-bit output, S <= 1e-3)."""
 from __future__ import annotations
 

@@ -72,7 +72,7 @@ def test_fp64_loops():
 
 
 def test_reference_recipe():
-    """The restated generator follows cutile-attn-kda/main.py:286-310: seed 17,
+    """The restated generator follows cutile-attn-kda/main.py:282-305: seed 17,
     decay exp(g) in (0, 1], beta in [0.1, 0.9], deterministic."""
     s = shapes.KDA_KIMI_LINEAR
     x = inputs.kda_inputs(s)
