@@ -6,8 +6,9 @@ inputs, scale 1/sqrt(128) — reported in algorithmic TFLOP/s (causal work
 2*B*Hq*D*S*(S+1)).  A "step" is one forward pass over that batch with
 inputs already resident in HBM.  The other kernels (bf16 GEMM at 1024^3
 and 8192^3, fp8 block-scaled GEMM at 8192^3, MLA absorbed decode, GDN
-decode, KDA decode at the reference's "large" shape) are measured the same
-way and reported under "others".
+decode, KDA decode at the reference's "large" shape, the fp8 activation
+quantiser at 8192x8192) are measured the same way and reported under
+"others".
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        [--only-headline]
@@ -206,6 +207,19 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
         "gbps_mean": F.gbps(nb, ms), "frac_hbm_peak_mean": F.gbps(nb, ms) / F.PEAK_HBM_GBPS,
     }
     log(f"kda_decode: {res['kda_decode']['gbps_mean']:.0f} GB/s mean")
+    del x, so, od
+
+    m = k = 8192
+    xa = torch.randn((m, k), generator=torch.Generator().manual_seed(I.SEED)).to(torch.bfloat16).cuda()
+    qa = torch.empty((m, k), dtype=torch.float8_e4m3fn, device="cuda")
+    sa_ = torch.empty((m, k // 128), dtype=torch.float32, device="cuda")
+    ms, _ = time_launches(lambda: ops.quant_fp8_act(xa, q=qa, scales=sa_), steps, warmup)
+    nb = F.quant_fp8_act_bytes(m, k)
+    res["quant_fp8_act"] = {
+        "unit": "GB/s", "shape": f"{m}x{k} bf16 -> e4m3 + 1x128 scales", "mean_us": ms * 1e3,
+        "gbps_mean": F.gbps(nb, ms), "frac_hbm_peak_mean": F.gbps(nb, ms) / F.PEAK_HBM_GBPS,
+    }
+    log(f"quant_fp8_act: {res['quant_fp8_act']['gbps_mean']:.0f} GB/s mean")
     return res
 
 

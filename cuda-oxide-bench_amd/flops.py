@@ -93,6 +93,11 @@ def kda_decode_bytes(s, io_bytes: int = 2) -> int:
     return bh * (2 * s.d_k * s.d_v * 4 + (3 * s.d_k + 2 * s.d_v + 1) * io_bytes)
 
 
+def quant_fp8_act_bytes(m: int, k: int, io_bytes: int = 2) -> int:
+    """16-bit activations read, e4m3 codes and 1x128 fp32 scales written."""
+    return m * k * io_bytes + m * k + (m * k // 128) * 4
+
+
 def tflops(flops: int, ms: float) -> float:
     return flops / (ms * 1e-3) / 1e12
 

@@ -232,3 +232,25 @@ def kda_decode(q, k, v, g, beta, S_in, S_out=None, o=None):
     _lib.call("mx_kda_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
               S_in.data_ptr(), S_out.data_ptr(), o.data_ptr(), B, Hh, dk, dv, _IO_DTYPES[q.dtype], _stream())
     return o, S_out
+
+
+def quant_fp8_act(x, q=None, scales=None):
+    """fp8 activation quantisation with 1x128 block scales (the producer of
+    gemm_fp8_bs's A operand): x [M,K] bf16/f16 (K % 128 == 0) ->
+    (q [M,K] float8_e4m3fn, scales [M,K/128] fp32) with x ~= q * scale."""
+    _require(x, "x", _IO_DTYPES, 2)
+    M, K = x.shape
+    if K % 128:
+        raise ValueError(f"K ({K}) must be a multiple of 128")
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
+    _require(q, "q", (torch.float8_e4m3fn,), 2)
+    if scales is None:
+        scales = torch.empty((M, K // 128), dtype=torch.float32, device=x.device)
+    _require(scales, "scales", (torch.float32,), 2)
+    if tuple(q.shape) != (M, K) or tuple(scales.shape) != (M, K // 128):
+        raise ValueError(f"q must be {(M, K)} and scales {(M, K // 128)}")
+    _same_device(x, q, scales)
+    _lib.call("mx_quant_fp8_act", x.data_ptr(), q.data_ptr(), scales.data_ptr(), M, K, K, _IO_DTYPES[x.dtype],
+              _stream())
+    return q, scales

@@ -75,6 +75,21 @@ int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, const float* s
                    int N, int K, void* stream);
 
 /*
+ * fp8 activation quantisation (the producer of mx_gemm_fp8_bs's A operand):
+ * for every row m and 128-wide column block kb of X[M,K] (bf16 or f16,
+ * leading dimension ldx >= K, in elements):
+ *   scales[m,kb] = max_{k in kb} |X[m,k]| / 448   (1.0 for an all-zero block)
+ *   Q[m,k]       = e4m3fn(RNE(clamp(X[m,k] / scales[m,kb], -448, 448)))
+ * Q is [M,K] row-major bytes, scales [M, K/128] fp32.  Requires K % 128 == 0,
+ * ldx % 8 == 0, 16-byte aligned X and Q.
+ * Replaces: the host-side generation of the fp8 GEMM operands
+ * (mojo-matmul-fp8/matmul_fp8.mojo:262-270 fills them on the CPU), extended
+ * with the 1x128 block scaling this path specifies.
+ */
+int mx_quant_fp8_act(const void* X, void* Q, float* scales, int M, int K, int ldx, int dtype,
+                     void* stream);
+
+/*
  * Fused grouped-query attention forward (flash-attention style, one pass):
  *   O[b,h,s,:] = softmax_t( scale * Q[b,h,s,:]·K[b,h/G,t,:] + mask ) · V[b,h/G,t,:]
  * with G = Hq / Hkv and mask = -inf for t > s when causal != 0.

@@ -51,8 +51,9 @@ def e4m3_encode(x: np.ndarray) -> np.ndarray:
     pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (hi % 2 == 0))
     pick_hi |= (lo == hi)
     code = np.where(pick_hi, hi, lo).astype(np.uint8)
-    neg = (x < 0) & (code != 0)
-    return np.where(neg, code | 0x80, code).astype(np.uint8)
+    # The sign bit is kept even when the magnitude rounds to zero (-0 is
+    # 0x80), as torch.float8_e4m3fn and IEEE-style conversions do.
+    return np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)
 
 
 def e4m3_decode(codes: np.ndarray) -> np.ndarray:

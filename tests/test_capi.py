@@ -24,7 +24,7 @@ def declared_functions() -> list[str]:
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("mx_gemm_bf16", "mx_gemm_fp8_bs", "mx_gqa_fwd", "mx_mla_decode", "mx_mla_decode_workspace",
-              "mx_gdn_decode", "mx_kda_decode", "mx_strerror", "mx_version"):
+              "mx_gdn_decode", "mx_kda_decode", "mx_quant_fp8_act", "mx_strerror", "mx_version"):
         assert n in names
 
 
@@ -109,3 +109,12 @@ def test_kda_validation():
     assert f(*args, 2, 4, 64, 64, 3, None) == _lib.MX_ERR_DTYPE
     s_in, s_out = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x100000 + 256)
     assert f(P, P, P, P, P, s_in, s_out, P, 2, 4, 64, 64, 0, None) == _lib.MX_ERR_ALIAS
+
+
+def test_quant_fp8_validation():
+    f = _lib.load().mx_quant_fp8_act
+    assert f(None, P, P, 4, 128, 128, 0, None) == _lib.MX_ERR_NULL
+    assert f(P, P, P, 4, 96, 96, 0, None) == _lib.MX_ERR_SHAPE       # K % 128
+    assert f(P, P, P, 4, 128, 64, 0, None) == _lib.MX_ERR_SHAPE      # ldx < K
+    assert f(P, P, P, 4, 128, 132, 0, None) == _lib.MX_ERR_ALIGN     # ldx % 8
+    assert f(P, P, P, 4, 128, 128, 2, None) == _lib.MX_ERR_DTYPE

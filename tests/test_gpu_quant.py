@@ -1,0 +1,90 @@
+"""fp8 activation quantisation on the GPU vs the CPU oracle's recipe
+(oracle/fp8.py quantize_blockwise: amax/448 scale, RNE to e4m3fn, whose
+codec is pinned against torch.float8_e4m3fn).  Bar: bit-exact codes and
+scales (integer / byte output)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, import_submodule
+from oracle import fp8 as ofp8
+from oracle.metrics import normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+
+inputs = import_submodule("inputs")
+shapes = import_submodule("shapes")
+
+
+def quant(ops, x):
+    q, s = ops.quant_fp8_act(x.cuda())
+    torch.cuda.synchronize()
+    return q.view(torch.uint8).cpu().numpy(), s.cpu().numpy()
+
+
+def expect(x):
+    return ofp8.quantize_blockwise(x.float().numpy(), (1, 128))
+
+
+@pytest.mark.parametrize("mk,dt", [((1, 128), torch.bfloat16), ((3, 384), torch.bfloat16), ((77, 1024), torch.float16),
+                                   ((256, 2048), torch.bfloat16), ((1000, 640), torch.float16)])
+def test_bit_exact_random(ops, mk, dt):
+    m, k = mk
+    announce(f"quant_fp8 {m}x{k} {dt}")
+    g = torch.Generator().manual_seed(m * 7919 + k)
+    x = (torch.randn((m, k), generator=g) * torch.exp(torch.randn((m, 1), generator=g) * 3)).to(dt)
+    q, s = quant(ops, x)
+    qe, se = expect(x)
+    assert np.array_equal(s, se)
+    assert np.array_equal(q, qe)
+
+
+def test_edge_cases(ops):
+    """Zero blocks (scale 1, code 0), a lone nonzero (-> +-448), exact e4m3
+    midpoints after scaling (ties to even), values in the e4m3 subnormal
+    range, and mixed signs."""
+    announce("quant_fp8 edge cases")
+    x = torch.zeros((6, 256), dtype=torch.float32)
+    x[1, 5] = -3.0                                     # lone value: scale 3/448, code -448
+    x[2, :128] = torch.linspace(-448, 448, 128)        # scale exactly 1
+    # midpoints between adjacent e4m3 values with scale 1 (amax 448 at the end)
+    pos = ofp8.e4m3_decode(np.arange(0, 0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = (pos[1:] + pos[:-1]) / 2
+    x[3, :126] = torch.from_numpy(mids.astype(np.float32))
+    x[3, 127] = 448.0
+    x[4, 128:] = torch.from_numpy((np.arange(128) - 64) * 2.0 ** -12)  # tiny: subnormal e4m3 codes
+    x[4, 200] = 448.0
+    x[5] = torch.randn(256) * 1e-3
+    for dt in (torch.bfloat16, torch.float16):
+        xb = x.to(dt)
+        q, s = quant(ops, xb)
+        qe, se = expect(xb)
+        assert np.array_equal(s, se) and np.array_equal(q, qe)
+        assert s[0, 0] == 1.0 and s[0, 1] == 1.0 and not q[0].any()
+        assert ofp8.e4m3_decode(q[1:2, 5])[0] == -448.0
+
+
+def test_feeds_fp8_gemm(ops):
+    """Device-quantised activations into the block-scaled fp8 GEMM equal the
+    oracle GEMM of the same dequantised operands."""
+    announce("quant_fp8 -> gemm_fp8_bs")
+    m, n, k = 384, 512, 1024
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn((m, k), generator=g).to(torch.bfloat16)
+    _, _, b8, sb = inputs.fp8_gemm_inputs(shapes.FP8GemmShape("t", m, n, k))
+    q, s = ops.quant_fp8_act(a.cuda())
+    c = ops.gemm_fp8_bs(q, s, b8.cuda(), sb.cuda())
+    torch.cuda.synchronize()
+    ref = ofp8.gemm_fp8_bs_ref(q.view(torch.uint8).cpu().numpy(), s.cpu().numpy(),
+                               ofp8.fp8_tensor_codes(b8), sb.numpy())
+    assert normwise_rel_err(c.float().cpu(), torch.from_numpy(ref)) <= 2e-2
+    # and the dequantised A is close to the bf16 A it came from
+    deq = ofp8.dequantize_blockwise(q.view(torch.uint8).cpu().numpy(), s.cpu().numpy(), (1, 128))
+    assert np.abs(deq - a.float().numpy()).max() <= 0.07 * np.abs(a.float().numpy()).max()
+
+
+def test_rejects_bad_k(ops):
+    with pytest.raises(Exception):
+        ops.quant_fp8_act(torch.zeros((4, 96), dtype=torch.bfloat16, device="cuda"))
