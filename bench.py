@@ -178,8 +178,21 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
         "unit": "GB/s", "mean_us": ms * 1e3, "gbps_mean": F.gbps(nb, ms),
         "frac_hbm_peak_mean": F.gbps(nb, ms) / F.PEAK_HBM_GBPS, "tflops_mean": F.tflops(fl, ms),
     }
-    del qd, kvd, o, ws
     log(f"mla_decode: {res['mla_decode']['gbps_mean']:.0f} GB/s mean")
+    # the whole absorbed step: q_nope W_UK -> latent decode -> o_lat W_UV
+    x = {n: t.cuda() for n, t in I.mla_projection_inputs(shape).items()}
+    qb = torch.empty((shape.batch, shape.n_h, shape.d_qk), dtype=torch.bfloat16, device="cuda")
+    od = torch.empty((shape.batch, shape.n_h, 128), dtype=torch.bfloat16, device="cuda")
+    ms, _ = time_launches(lambda: ops.mla_decode_absorbed(x["q_nope"], x["q_rope"], kvd, x["w_uk"], x["w_uv"],
+                                                          shape.scale, q_buf=qb, o_lat=o, out=od, workspace=ws),
+                          steps, warmup)
+    nb2 = nb + sum(x[n].numel() * 2 for n in ("w_uk", "w_uv", "q_nope", "q_rope")) + od.numel() * 2
+    res["mla_decode_absorbed_step"] = {
+        "unit": "GB/s", "mean_us": ms * 1e3, "gbps_mean": F.gbps(nb2, ms),
+        "note": "absorb (batched GEMM) + rope copy + latent decode + combine + up-projection",
+    }
+    del qd, kvd, o, ws, x, qb, od
+    log(f"mla_decode_absorbed_step: {res['mla_decode_absorbed_step']['mean_us']:.1f} us mean")
 
     shape = S.GDN_BASELINE
     x = {n: t.cuda() for n, t in I.gdn_inputs(shape).items()}

@@ -30,6 +30,7 @@ _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
+_ll = ctypes.c_longlong
 
 # name -> (restype, argtypes); mirrors include/mx_kernels.h one to one.
 SIGNATURES: dict[str, tuple] = {
@@ -43,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "mx_gdn_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "mx_kda_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "mx_quant_fp8_act": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "mx_gemm_bf16_batched": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _ll, _ll, _ll, _vp]),
 }
 
 

@@ -71,13 +71,18 @@ struct Cfg {
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
 };
 
+// gridDim.y indexes a batch of independent products whose operands sit
+// sA / sB / sC elements apart (0 and gridDim.y = 1 for a single GEMM).
 template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C, int M,
-    int N, int K, int lda, int ldb, int ldc) {
+    int N, int K, int lda, int ldb, int ldc, long long sA, long long sB, long long sC) {
   using CF = Cfg<BM, BN, WM, WN>;
   constexpr int NT = CF::NT, FM = CF::FM, FN = CF::FN;
   extern __shared__ __align__(16) unsigned char smem[];
+  A += (size_t)blockIdx.y * sA;
+  B += (size_t)blockIdx.y * sB;
+  C += (size_t)blockIdx.y * sC;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -464,15 +469,15 @@ static int launch_dma(const void* A, const void* B, void* C, int M, int N, int K
 
 template <int BM, int BN, int WM, int WN>
 static int launch(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
-                  hipStream_t stream) {
+                  hipStream_t stream, int batch = 1, long long sA = 0, long long sB = 0, long long sC = 0) {
   using CF = Cfg<BM, BN, WM, WN>;
   const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
+  if (tiles > 0x7fffffffLL || batch > 65535) return MX_ERR_SHAPE;
   const size_t smem = 2 * CF::LDS_STAGE;
   auto kern = gemm_bf16_kernel<BM, BN, WM, WN>;
   MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CF::NT), smem, stream, (const uint16_t*)A,
-                     (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)batch), dim3(CF::NT), smem, stream, (const uint16_t*)A,
+                     (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
 }
@@ -499,4 +504,24 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   if (tiles256 >= 512) return mx::gemm::launch<256, 256, 2, 4>(A, B, C, M, N, K, lda, ldb, ldc, s);
   if (tiles128 >= 256) return mx::gemm::launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
   return mx::gemm::launch<64, 64, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
+}
+
+extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda,
+                                    int ldb, int ldc, long long strideA, long long strideB, long long strideC,
+                                    void* stream) {
+  if (!A || !B || !C) return MX_ERR_NULL;
+  if (batch <= 0 || M <= 0 || N <= 0 || K <= 0) return MX_ERR_SHAPE;
+  if (batch > 65535 || strideA < 0 || strideB < 0 || strideC < 0) return MX_ERR_SHAPE;
+  if (lda < K || ldb < N || ldc < N) return MX_ERR_SHAPE;
+  if ((K % 8) || (N % 8) || (lda % 8) || (ldb % 8) || (ldc % 8)) return MX_ERR_ALIGN;
+  if ((strideA % 8) || (strideB % 8) || (strideC % 8)) return MX_ERR_ALIGN;
+  if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15) return MX_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  // The batched products of this path are small per item (e.g. the MLA
+  // weight absorption: M = decode batch, one head's weight per item), so
+  // the register-staged kernel with tiles sized to the item.
+  const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * batch;
+  if (M >= 128 && t128 >= 256)
+    return mx::gemm::launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
+  return mx::gemm::launch<64, 64, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
 }

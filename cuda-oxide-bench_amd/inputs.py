@@ -133,3 +133,17 @@ def kda_inputs(s: KDAShape, dtype: torch.dtype = torch.float16, seed: int = KDA_
     S = (rng.standard_normal((B, Hh, dk, dv)) * 0.1).astype(np.float32)
     t = lambda x: torch.from_numpy(x).to(dtype)  # noqa: E731
     return {"q": t(q), "k": t(k), "v": t(v), "g": t(gg), "beta": t(beta), "S_in": torch.from_numpy(S).contiguous()}
+
+
+def mla_projection_inputs(s: MLADecodeShape, d_nope: int = 128, d_v: int = 128, seed: int = SEED + 1):
+    """The tensors around the absorbed decode (DeepSeek-V3: d_nope = d_v = 128):
+    q_nope [B,H,d_nope], q_rope [B,H,d_rope] ~ N(0,1); W_UK [H,d_nope,d_c],
+    W_UV [H,d_c,d_v] ~ N(0,1)/sqrt(fan-in); all bf16."""
+    g = _gen(seed)
+    B, Hh, dc, dr = s.batch, s.n_h, s.d_latent, s.d_qk - s.d_latent
+    q_nope = torch.randn((B, Hh, d_nope), generator=g, dtype=torch.float32)
+    q_rope = torch.randn((B, Hh, dr), generator=g, dtype=torch.float32)
+    w_uk = torch.randn((Hh, d_nope, dc), generator=g, dtype=torch.float32) / math.sqrt(d_nope)
+    w_uv = torch.randn((Hh, dc, d_v), generator=g, dtype=torch.float32) / math.sqrt(dc)
+    return {n: t.to(torch.bfloat16) for n, t in
+            (("q_nope", q_nope), ("q_rope", q_rope), ("w_uk", w_uk), ("w_uv", w_uv))}

@@ -254,3 +254,96 @@ def quant_fp8_act(x, q=None, scales=None):
     _lib.call("mx_quant_fp8_act", x.data_ptr(), q.data_ptr(), scales.data_ptr(), M, K, K, _IO_DTYPES[x.dtype],
               _stream())
     return q, scales
+
+
+def gemm_bf16_batched(a, b, out=None):
+    """C[i] = A[i] @ B[i] for contiguous bf16 A [batch,M,K], B [batch,K,N]."""
+    _require(a, "a", (torch.bfloat16,), 3)
+    _require(b, "b", (torch.bfloat16,), 3)
+    nb, M, K = a.shape
+    if b.shape[0] != nb or b.shape[1] != K:
+        raise ValueError(f"shape mismatch: a {tuple(a.shape)} vs b {tuple(b.shape)}")
+    N = b.shape[2]
+    if out is None:
+        out = torch.empty((nb, M, N), dtype=torch.bfloat16, device=a.device)
+    _require(out, "out", (torch.bfloat16,), 3)
+    if tuple(out.shape) != (nb, M, N):
+        raise ValueError(f"out must be {(nb, M, N)}")
+    _same_device(a, b, out)
+    _lib.call("mx_gemm_bf16_batched", a.data_ptr(), b.data_ptr(), out.data_ptr(), nb, M, N, K, K, N, N,
+              M * K, K * N, M * N, _stream())
+    return out
+
+
+def _head_gemm(x, w, out, out_ld):
+    """out[:, h, :] = x[:, h, :] @ w[h] for every head, x [B,H,K] and w
+    [H,K,N] contiguous; out rows are out_ld elements apart per head slot."""
+    B, Hh, K = x.shape
+    N = w.shape[2]
+    _lib.call("mx_gemm_bf16_batched", x.data_ptr(), w.data_ptr(), out.data_ptr(), Hh, B, N, K, Hh * K, N,
+              Hh * out_ld, K, K * N, out_ld, _stream())
+
+
+def mla_absorb_q(q_nope, w_uk, out=None):
+    """Weight absorption of the MLA query: q_lat[b,h,:] = q_nope[b,h,:] @ W_UK[h]
+    (MECHANISMS.md:91-94: q^T (W_UK c) = (W_UK^T q)^T c).  q_nope [B,H,dn],
+    w_uk [H,dn,d_c] bf16 -> q_lat [B,H,d_c] bf16 (fp32 accumulate)."""
+    _require(q_nope, "q_nope", (torch.bfloat16,), 3)
+    _require(w_uk, "w_uk", (torch.bfloat16,), 3)
+    B, Hh, dn = q_nope.shape
+    if w_uk.shape[0] != Hh or w_uk.shape[1] != dn:
+        raise ValueError(f"w_uk must be [{Hh}, {dn}, d_c], got {tuple(w_uk.shape)}")
+    dc = w_uk.shape[2]
+    if out is None:
+        out = torch.empty((B, Hh, dc), dtype=torch.bfloat16, device=q_nope.device)
+    _require(out, "out", (torch.bfloat16,), 3)
+    if tuple(out.shape) != (B, Hh, dc):
+        raise ValueError(f"out must be {(B, Hh, dc)}")
+    _same_device(q_nope, w_uk, out)
+    _head_gemm(q_nope, w_uk, out, dc)
+    return out
+
+
+def mla_up_project(o_lat, w_uv, out=None):
+    """Output up-projection of the absorbed MLA decode: o[b,h,:] =
+    o_lat[b,h,:] @ W_UV[h] (MECHANISMS.md:115-120).  o_lat [B,H,d_c],
+    w_uv [H,d_c,dv] bf16 -> o [B,H,dv] bf16."""
+    _require(o_lat, "o_lat", (torch.bfloat16,), 3)
+    _require(w_uv, "w_uv", (torch.bfloat16,), 3)
+    B, Hh, dc = o_lat.shape
+    if w_uv.shape[0] != Hh or w_uv.shape[1] != dc:
+        raise ValueError(f"w_uv must be [{Hh}, {dc}, dv], got {tuple(w_uv.shape)}")
+    dv = w_uv.shape[2]
+    if out is None:
+        out = torch.empty((B, Hh, dv), dtype=torch.bfloat16, device=o_lat.device)
+    _require(out, "out", (torch.bfloat16,), 3)
+    if tuple(out.shape) != (B, Hh, dv):
+        raise ValueError(f"out must be {(B, Hh, dv)}")
+    _same_device(o_lat, w_uv, out)
+    _head_gemm(o_lat, w_uv, out, dv)
+    return out
+
+
+def mla_decode_absorbed(q_nope, q_rope, kv, w_uk, w_uv, scale, q_buf=None, o_lat=None, out=None, workspace=None):
+    """Full weight-absorbed MLA decode step (MECHANISMS.md:77-94, 115-120):
+    q_lat = q_nope @ W_UK[h] written into Q[..., :512] next to q_rope,
+    latent attention over the KV cache (mla_decode), then o = o_lat @ W_UV[h].
+    q_nope [B,H,128], q_rope [B,H,64], kv [B,T,576], w_uk [H,128,512],
+    w_uv [H,512,dv], all bf16 -> o [B,H,dv]."""
+    _require(q_rope, "q_rope", (torch.bfloat16,), 3)
+    B, Hh, _ = q_nope.shape
+    dc = w_uk.shape[2]
+    if q_buf is None:
+        q_buf = torch.empty((B, Hh, dc + q_rope.shape[2]), dtype=torch.bfloat16, device=q_nope.device)
+    _require(q_buf, "q_buf", (torch.bfloat16,), 3)
+    if tuple(q_buf.shape) != (B, Hh, dc + q_rope.shape[2]) or tuple(q_rope.shape[:2]) != (B, Hh):
+        raise ValueError("q_buf must be [B, H, d_c + d_rope] and q_rope [B, H, d_rope]")
+    _require(q_nope, "q_nope", (torch.bfloat16,), 3)
+    _require(w_uk, "w_uk", (torch.bfloat16,), 3)
+    if w_uk.shape[0] != Hh or w_uk.shape[1] != q_nope.shape[2]:
+        raise ValueError(f"w_uk must be [{Hh}, {q_nope.shape[2]}, d_c], got {tuple(w_uk.shape)}")
+    _same_device(q_nope, q_rope, w_uk, q_buf)
+    _head_gemm(q_nope, w_uk, q_buf, q_buf.shape[2])   # q_lat into q_buf[..., :d_c]
+    q_buf[..., dc:].copy_(q_rope)
+    o_lat = mla_decode(q_buf, kv, scale, out=o_lat, workspace=workspace)
+    return mla_up_project(o_lat, w_uv, out=out)

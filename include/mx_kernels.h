@@ -60,6 +60,22 @@ int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N, int K, int
                  int ldc, void* stream);
 
 /*
+ * Strided-batched bf16 GEMM:  for i < batch,
+ *   C_i[M,N] = A_i[M,K] · B_i[K,N],  X_i = X + i * strideX (elements)
+ * with the layout and requirements of mx_gemm_bf16 per item, batch <= 65535,
+ * strides >= 0 and multiples of 8.  Items may be interleaved views, e.g.
+ * head h of a [B, H, d] activation (A + h*d, lda = H*d).  This path uses it
+ * for the per-head MLA weight products either side of the latent decode:
+ * q_lat = q_nope · W_UK[h] and o = o_lat · W_UV[h].
+ * Replaces: the per-head up-projections of the absorbed MLA decode that
+ * analysis/wave15-attention-research/MECHANISMS.md:91-94, 115-120 describes
+ * (the reference has no kernel for them).
+ */
+int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int batch, int M, int N, int K,
+                         int lda, int ldb, int ldc, long long strideA, long long strideB,
+                         long long strideC, void* stream);
+
+/*
  * fp8 block-scaled GEMM:
  *   C[m,n] = sum_kb sA[m,kb] * sB[kb,n/128] * sum_{k in block kb} A[m,k] * B[k,n]
  * A[M,K], B[K,N] row-major OCP e4m3 ("e4m3fn", torch.float8_e4m3fn) bytes;

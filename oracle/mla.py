@@ -46,3 +46,34 @@ def mla_merge(parts) -> torch.Tensor:
     l = sum(w * p[1] for w, p in zip(ws, parts))
     o = sum(w[..., None] * p[2] for w, p in zip(ws, parts))
     return o / l[..., None]
+
+
+def mla_absorbed_ref(q_nope, q_rope, kv, w_uk, w_uv, scale: float) -> torch.Tensor:
+    """The absorbed decode step with the device path's roundings
+    (MECHANISMS.md:91-94, 115-120): q_lat = bf16(q_nope @ W_UK[h]) (fp32
+    accumulate), Q = [q_lat, q_rope], o_lat = bf16(mla_decode_ref(Q, kv)),
+    o = o_lat @ W_UV[h] in fp32.  Shapes: q_nope [B,H,dn], q_rope
+    [B,H,dr], kv [B,T,dc+dr], w_uk [H,dn,dc], w_uv [H,dc,dv]."""
+    qn, qr = q_nope.detach().cpu().float(), q_rope.detach().cpu().float()
+    wk, wv = w_uk.detach().cpu().float(), w_uv.detach().cpu().float()
+    q_lat = torch.einsum("bhn,hnc->bhc", qn, wk).to(torch.bfloat16).float()
+    Q = torch.cat([q_lat, qr], dim=-1)
+    o_lat = mla_decode_ref(Q, kv, scale, d_latent=wk.shape[2]).to(torch.bfloat16).float()
+    return torch.einsum("bhc,hcv->bhv", o_lat, wv)
+
+
+def mla_unabsorbed_ref(q_nope, q_rope, kv, w_uk, w_uv, scale: float, d_latent: int = 512) -> torch.Tensor:
+    """The same step without absorption, float64: per-head keys
+    k = [W_UK[h]^T c_t, k_rope_t] and values v = W_UV[h]^T c_t are
+    materialised from the latent rows c_t = kv[b,t,:d_latent] and
+    o = softmax(scale q.k) v with q = [q_nope, q_rope] (MECHANISMS.md:77-88).
+    Equal to mla_absorbed_ref up to the bf16 roundings that one applies."""
+    qn, qr = q_nope.detach().cpu().double(), q_rope.detach().cpu().double()
+    wk, wv = w_uk.detach().cpu().double(), w_uv.detach().cpu().double()
+    kvd = kv.detach().cpu().double()
+    c, kr = kvd[..., :d_latent], kvd[..., d_latent:]
+    k_nope = torch.einsum("btc,hnc->bhtn", c, wk)              # [B,H,T,dn]
+    v = torch.einsum("btc,hcv->bhtv", c, wv)                   # [B,H,T,dv]
+    s = (torch.einsum("bhn,bhtn->bht", qn, k_nope) + torch.einsum("bhr,btr->bht", qr, kr)) * scale
+    p = torch.softmax(s, dim=-1)
+    return torch.einsum("bht,bhtv->bhv", p, v)

@@ -24,7 +24,8 @@ def declared_functions() -> list[str]:
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("mx_gemm_bf16", "mx_gemm_fp8_bs", "mx_gqa_fwd", "mx_mla_decode", "mx_mla_decode_workspace",
-              "mx_gdn_decode", "mx_kda_decode", "mx_quant_fp8_act", "mx_strerror", "mx_version"):
+              "mx_gdn_decode", "mx_kda_decode", "mx_quant_fp8_act", "mx_gemm_bf16_batched", "mx_strerror",
+              "mx_version"):
         assert n in names
 
 
@@ -118,3 +119,12 @@ def test_quant_fp8_validation():
     assert f(P, P, P, 4, 128, 64, 0, None) == _lib.MX_ERR_SHAPE      # ldx < K
     assert f(P, P, P, 4, 128, 132, 0, None) == _lib.MX_ERR_ALIGN     # ldx % 8
     assert f(P, P, P, 4, 128, 128, 2, None) == _lib.MX_ERR_DTYPE
+
+
+def test_gemm_batched_validation():
+    f = _lib.load().mx_gemm_bf16_batched
+    assert f(None, P, P, 2, 64, 64, 64, 64, 64, 64, 4096, 4096, 4096, None) == _lib.MX_ERR_NULL
+    assert f(P, P, P, 0, 64, 64, 64, 64, 64, 64, 4096, 4096, 4096, None) == _lib.MX_ERR_SHAPE
+    assert f(P, P, P, 70000, 64, 64, 64, 64, 64, 64, 0, 0, 0, None) == _lib.MX_ERR_SHAPE
+    assert f(P, P, P, 2, 64, 64, 64, 64, 64, 64, -8, 0, 0, None) == _lib.MX_ERR_SHAPE
+    assert f(P, P, P, 2, 64, 64, 64, 64, 64, 64, 4, 0, 0, None) == _lib.MX_ERR_ALIGN

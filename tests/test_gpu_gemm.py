@@ -122,3 +122,21 @@ def test_rejects_bad_arguments(ops):
     b = torch.zeros((60, 64), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(Exception):
         ops.gemm_bf16(a, b)
+
+
+@pytest.mark.parametrize("bmnk", [(1, 64, 64, 64), (7, 100, 136, 72), (128, 32, 512, 128), (128, 32, 128, 512),
+                                  (3, 300, 264, 520)])
+def test_batched_vs_oracle(ops, bmnk):
+    """Strided-batched GEMM: every item against the fp32 oracle."""
+    nb, m, n, k = bmnk
+    announce(f"gemm_bf16_batched {nb}x{m}x{n}x{k}")
+    g = torch.Generator().manual_seed(nb * 131 + m)
+    a = (torch.rand((nb, m, k), generator=g) * 2 - 1).to(torch.bfloat16)
+    b = (torch.rand((nb, k, n), generator=g) * 2 - 1).to(torch.bfloat16)
+    c = ops.gemm_bf16_batched(a.cuda(), b.cuda())
+    torch.cuda.synchronize()
+    c = c.cpu()
+    for i in range(nb):
+        ref = ogemm.gemm_ref(a[i], b[i])
+        assert normwise_rel_err(c[i], ref) <= TOL
+        assert torch.all((c[i].float() - ref).abs() <= 0.2 + 0.05 * ref.abs())

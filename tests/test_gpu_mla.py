@@ -89,3 +89,34 @@ def test_running_max_jumps(ops):
     err = normwise_rel_err(o[bs], ref[bs])
     assert err <= TOL, f"normwise rel err {err:.3e}"
     assert torch.isfinite(o.float()).all()
+
+
+def test_absorb_and_up_project(ops):
+    """The per-head weight products around the decode (head-strided batched
+    GEMM) against fp32 per-head matmuls, at the DeepSeek-V3 head shapes."""
+    announce("mla absorb q / up-project B32 H128")
+    s = shapes.MLA_BASELINE
+    x = inputs.mla_projection_inputs(s)
+    d = {k: v.cuda() for k, v in x.items()}
+    q_lat = ops.mla_absorb_q(d["q_nope"], d["w_uk"])
+    o_lat = torch.randn((s.batch, s.n_h, 512), generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    o = ops.mla_up_project(o_lat.cuda(), d["w_uv"])
+    torch.cuda.synchronize()
+    ref_q = torch.einsum("bhn,hnc->bhc", x["q_nope"].float(), x["w_uk"].float())
+    ref_o = torch.einsum("bhc,hcv->bhv", o_lat.float(), x["w_uv"].float())
+    assert normwise_rel_err(q_lat.cpu(), ref_q) <= 2e-2
+    assert normwise_rel_err(o.cpu(), ref_o) <= 2e-2
+
+
+def test_absorbed_pipeline(ops):
+    """q_nope, q_rope, latent cache, W_UK, W_UV -> o: the whole absorbed
+    decode step (absorb, latent attention, up-projection) against the oracle."""
+    announce("mla absorbed pipeline B4 H128 T1024")
+    s = shapes.MLADecodeShape("t", batch=4, n_h=128, ctx=1024)
+    _, kv = inputs.mla_inputs(s)
+    x = inputs.mla_projection_inputs(s)
+    d = {k: v.cuda() for k, v in x.items()}
+    o = ops.mla_decode_absorbed(d["q_nope"], d["q_rope"], kv.cuda(), d["w_uk"], d["w_uv"], s.scale)
+    torch.cuda.synchronize()
+    ref = omla.mla_absorbed_ref(x["q_nope"], x["q_rope"], kv, x["w_uk"], x["w_uv"], s.scale)
+    assert normwise_rel_err(o.cpu(), ref) <= 2e-2

@@ -43,3 +43,23 @@ def test_split_merge_equals_unsplit():
     full = omla.mla_decode_ref(q, kv, s.scale)
     parts = [omla.mla_partial(q, kv[:, a:b], s.scale) for a, b in ((0, 31), (31, 64), (64, 100))]
     assert torch.allclose(omla.mla_merge(parts), full, atol=1e-5, rtol=1e-5)
+
+
+def test_absorption_identity():
+    """Weight absorption changes nothing but roundings: the absorbed form
+    (q_nope W_UK against the latent rows, then W_UV) equals attention over
+    the materialised per-head keys and values (MECHANISMS.md:77-94)."""
+    s = shapes.MLADecodeShape("t", 2, 4, 33)
+    _, kv = inputs.mla_inputs(s)
+    x = inputs.mla_projection_inputs(s)
+    full = omla.mla_unabsorbed_ref(x["q_nope"], x["q_rope"], kv, x["w_uk"], x["w_uv"], s.scale)
+    # absorbed, in float64 without the bf16 roundings
+    qn, wk, wv = x["q_nope"].double(), x["w_uk"].double(), x["w_uv"].double()
+    Q = torch.cat([torch.einsum("bhn,hnc->bhc", qn, wk), x["q_rope"].double()], dim=-1)
+    sc = torch.einsum("bhd,btd->bht", Q, kv.double()) * s.scale
+    o_lat = torch.einsum("bht,btc->bhc", torch.softmax(sc, -1), kv.double()[..., :512])
+    absorbed = torch.einsum("bhc,hcv->bhv", o_lat, wv)
+    assert torch.allclose(absorbed, full, rtol=1e-10, atol=1e-12)
+    # and the rounded oracle stays within bf16 distance of it
+    r = omla.mla_absorbed_ref(x["q_nope"], x["q_rope"], kv, x["w_uk"], x["w_uv"], s.scale).double()
+    assert (r - full).abs().max() / full.abs().max() < 2e-2
