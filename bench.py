@@ -181,17 +181,17 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
     log(f"mla_decode: {res['mla_decode']['gbps_mean']:.0f} GB/s mean")
     # the whole absorbed step: q_nope W_UK -> latent decode -> o_lat W_UV
     x = {n: t.cuda() for n, t in I.mla_projection_inputs(shape).items()}
-    qb = torch.empty((shape.batch, shape.n_h, shape.d_qk), dtype=torch.bfloat16, device="cuda")
     od = torch.empty((shape.batch, shape.n_h, 128), dtype=torch.bfloat16, device="cuda")
+    wsa = torch.empty(ops.mla_decode_absorbed_workspace_bytes(shape.batch, shape.n_h, shape.ctx) + 256,
+                      dtype=torch.uint8, device="cuda")
     ms, _ = time_launches(lambda: ops.mla_decode_absorbed(x["q_nope"], x["q_rope"], kvd, x["w_uk"], x["w_uv"],
-                                                          shape.scale, q_buf=qb, o_lat=o, out=od, workspace=ws),
-                          steps, warmup)
+                                                          shape.scale, out=od, workspace=wsa), steps, warmup)
     nb2 = nb + sum(x[n].numel() * 2 for n in ("w_uk", "w_uv", "q_nope", "q_rope")) + od.numel() * 2
     res["mla_decode_absorbed_step"] = {
         "unit": "GB/s", "mean_us": ms * 1e3, "gbps_mean": F.gbps(nb2, ms),
-        "note": "absorb (batched GEMM) + rope copy + latent decode + combine + up-projection",
+        "note": "one mx_mla_decode_absorbed call: absorb + latent decode + combine + up-projection",
     }
-    del qd, kvd, o, ws, x, qb, od
+    del qd, kvd, o, ws, x, od, wsa
     log(f"mla_decode_absorbed_step: {res['mla_decode_absorbed_step']['mean_us']:.1f} us mean")
 
     shape = S.GDN_BASELINE

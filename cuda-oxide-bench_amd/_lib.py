@@ -45,6 +45,8 @@ SIGNATURES: dict[str, tuple] = {
     "mx_kda_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "mx_quant_fp8_act": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "mx_gemm_bf16_batched": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _ll, _ll, _ll, _vp]),
+    "mx_mla_decode_absorbed": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
+    "mx_mla_decode_absorbed_workspace": (_sz, [_i, _i, _i]),
 }
 
 

@@ -482,6 +482,170 @@ static int launch(const void* A, const void* B, void* C, int M, int N, int K, in
   return MX_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Small-M batched kernel (M <= 32, e.g. one decode batch against one head's
+// weight): weight-streaming, so it needs enough bytes in flight per CU and
+// few rounds of workgroups rather than big tiles.  A workgroup is one wave
+// computing a 32 x (32 NF) tile of C over the whole K; 64-deep chunks of A
+// [32][64] and B [64][32 NF] go HBM -> LDS by direct loads into an
+// NS-stage ring, NS-1 chunks ahead (6 stages for narrow tiles, 4 at NF = 4:
+// 48-80 KB of LDS, two workgroups per CU).  A single wave needs no barrier: the ring stage
+// it overwrites was consumed by its own MFMAs, which waited for those
+// reads.  A rows (128 B) use the 16-row chunk swizzle of the large kernel;
+// B rows (64 NF bytes) put chunk c of k-row k at c ^ (((k & 3) << 2) mod
+// (4 NF)) so the 4 consecutive k-rows of a transposing read phase occupy
+// distinct 64-byte quarters of the bank sweep (no swizzle needed at NF = 1,
+// where those 4 rows are 256 contiguous bytes).
+// ---------------------------------------------------------------------------
+constexpr int SM_BK = 64;
+constexpr int SM_A_B = 32 * SM_BK * 2;  // 4 KB
+
+template <int NF>
+__device__ __forceinline__ int sm_swz(int k) {
+  return NF == 1 ? 0 : (((k & 3) << 2) & (4 * NF - 1));
+}
+
+// s_waitcnt for "at most min(MAXC, after) chunks of LPC loads in flight".
+template <int LPC, int MAXC>
+__device__ __forceinline__ void wait_chunks(int after) {
+  if constexpr (MAXC >= 4) {
+    if (after >= 4) { wait_vmcnt<4 * LPC>(); return; }
+  }
+  if constexpr (MAXC >= 3) {
+    if (after == 3) { wait_vmcnt<3 * LPC>(); return; }
+  }
+  if constexpr (MAXC >= 2) {
+    if (after == 2) { wait_vmcnt<2 * LPC>(); return; }
+  }
+  if (after >= 1) { wait_vmcnt<LPC>(); return; }
+  wait_vmcnt<0>();
+}
+
+template <int NF>
+__global__ __launch_bounds__(64) void gemm_bf16_smallm_kernel(const uint16_t* __restrict__ A,
+                                                              const uint16_t* __restrict__ B,
+                                                              uint16_t* __restrict__ C, int M, int N, int K, int lda,
+                                                              int ldb, int ldc, long long sA, long long sB,
+                                                              long long sC) {
+  constexpr int TN = 32 * NF;                 // columns per workgroup
+  constexpr int RB = TN * 2;                  // B row bytes in LDS
+  constexpr int B_B = SM_BK * RB;             // B chunk bytes
+  constexpr int STAGE = SM_A_B + B_B;
+  constexpr int BL = B_B / 1024;              // B direct loads per chunk
+  constexpr int LPC = 4 + BL;                 // direct loads per chunk
+  constexpr int BCH = RB / 16;                // 16-byte chunks per B row
+  constexpr int BRPL = 1024 / RB;             // B rows per direct load
+  constexpr int SM_NS = NF == 4 ? 4 : 6;      // ring stages
+  __shared__ __align__(1024) unsigned char smem[SM_NS * STAGE];
+  const int lane = threadIdx.x;
+  const int g = lane >> 5;
+  const int tiles_n = (N + TN - 1) / TN;
+  const int n0 = (int)(blockIdx.x % tiles_n) * TN;
+  const size_t item = blockIdx.x / tiles_n;
+  A += item * sA;
+  B += item * sB;
+  C += item * sC;
+  const int nk = K / SM_BK;
+  const uint32_t lds0 = lds_addr(smem);
+
+  // Direct-load lane offsets.  A load n (0..3): rows 8n + lane/8, chunk
+  // (lane%8) ^ swz_a<64>(row); rows past M re-read row M-1.  B load n:
+  // k-rows BRPL n + lane/BCH, chunk (lane%BCH) ^ sm_swz(k-row); columns
+  // past N re-read the last valid 8.
+  uint32_t a_off[4], b_off[BL];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int row = 8 * n + (lane >> 3);
+    a_off[n] = (uint32_t)min(row, M - 1) * (uint32_t)lda * 2u + 16u * ((lane & 7) ^ swz_a<64>(row));
+  }
+#pragma unroll
+  for (int n = 0; n < BL; ++n) {
+    const int kr = BRPL * n + lane / BCH;
+    const int col = min(n0 + 8 * ((lane % BCH) ^ sm_swz<NF>(kr)), N - 8);
+    b_off[n] = (uint32_t)kr * (uint32_t)ldb * 2u + 2u * col;
+  }
+  auto issue = [&](int kt) {
+    const uint32_t st = lds0 + (kt % SM_NS) * STAGE;
+    const uint16_t* ab = A + (size_t)kt * SM_BK;
+    const uint16_t* bb = B + (size_t)kt * SM_BK * ldb;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) dma16(ab, a_off[n], st + n * 1024);
+#pragma unroll
+    for (int n = 0; n < BL; ++n) dma16(bb, b_off[n], st + SM_A_B + n * 1024);
+  };
+
+  // Fragments (C^T = B^T . A^T): A^T (B operand) row m = lane%32, chunk
+  // 2 ks + g; B^T (A operand) of column tile nf by transposing reads, lane
+  // (g, sg, 4j+a) at k-row 16 ks + 8 g + 4 r + j, columns 32 nf + 16 sg + 4 a.
+  const int am = lane & 31;
+  const int b_sg = (lane >> 4) & 1, b_j = (lane >> 2) & 3, b_a = lane & 3;
+  const uint32_t a_base = lds0 + am * 128;
+  const int ax = swz_a<64>(am);
+  uint32_t b_base[NF];
+#pragma unroll
+  for (int nf = 0; nf < NF; ++nf) {
+    const int chunk = (32 * nf + 16 * b_sg + 4 * b_a) >> 3;  // k-row 8g + b_j: swizzle sm_swz(b_j)
+    b_base[nf] = lds0 + SM_A_B + (8 * g + b_j) * RB + 16 * (chunk ^ sm_swz<NF>(b_j)) + 8 * (b_a & 1);
+  }
+
+  f32x16 acc[NF];
+#pragma unroll
+  for (int nf = 0; nf < NF; ++nf) acc[nf] = f32x16{};
+#pragma unroll
+  for (int p = 0; p < SM_NS - 1; ++p)
+    if (p < nk) issue(p);
+  for (int kt = 0; kt < nk; ++kt) {
+    // chunk kt landed once at most min(NS-2, nk-1-kt) later chunks are in flight
+    wait_chunks<LPC, SM_NS - 2>(nk - 1 - kt);
+    if (kt + SM_NS - 1 < nk) issue(kt + SM_NS - 1);
+    const uint32_t so = (kt % SM_NS) * STAGE;
+#pragma unroll
+    for (int ks = 0; ks < SM_BK / 16; ++ks) {
+      const u32x4 af = lds_ld128(a_base + so + 16 * ((2 * ks + g) ^ ax));
+#pragma unroll
+      for (int nf = 0; nf < NF; ++nf) {
+        const uint32_t bp = b_base[nf] + so + 16 * ks * RB;
+        const u32x2 lo = lds_read_tr16_at(bp);
+        const u32x2 hi = lds_read_tr16_at(bp + 4 * RB);
+        acc[nf] = mfma32<BF16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, af, acc[nf]);
+      }
+    }
+  }
+
+  // lane holds m = lane%32, n = n0 + 32 nf + 8 i + 4 g + {0..3}
+  if (am < M) {
+    uint16_t* crow = C + (size_t)am * ldc;
+#pragma unroll
+    for (int nf = 0; nf < NF; ++nf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int gn = n0 + 32 * nf + 8 * i + 4 * g;
+        const f32x16& a = acc[nf];
+        if (gn < N) st64(crow + gn, u32x2{pack_bf16x2(a[4 * i], a[4 * i + 1]), pack_bf16x2(a[4 * i + 2], a[4 * i + 3])});
+      }
+  }
+}
+
+static int launch_smallm(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda, int ldb,
+                         int ldc, long long sA, long long sB, long long sC, hipStream_t stream) {
+  // Widest column tile that still leaves >= 512 workgroups (two per CU).
+  auto groups = [&](int tn) { return (long long)batch * ((N + tn - 1) / tn); };
+  const int nf = groups(128) >= 512 ? 4 : (groups(64) >= 512 ? 2 : 1);
+  const long long grid = groups(32 * nf);
+  if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
+  if (nf == 4)
+    hipLaunchKernelGGL(gemm_bf16_smallm_kernel<4>, dim3((unsigned)grid), dim3(64), 0, stream, (const uint16_t*)A,
+                       (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
+  else if (nf == 2)
+    hipLaunchKernelGGL(gemm_bf16_smallm_kernel<2>, dim3((unsigned)grid), dim3(64), 0, stream, (const uint16_t*)A,
+                       (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
+  else
+    hipLaunchKernelGGL(gemm_bf16_smallm_kernel<1>, dim3((unsigned)grid), dim3(64), 0, stream, (const uint16_t*)A,
+                       (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
 }  // namespace gemm
 }  // namespace mx
 
@@ -517,9 +681,11 @@ extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int b
   if ((strideA % 8) || (strideB % 8) || (strideC % 8)) return MX_ERR_ALIGN;
   if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  // The batched products of this path are small per item (e.g. the MLA
-  // weight absorption: M = decode batch, one head's weight per item), so
-  // the register-staged kernel with tiles sized to the item.
+  // Decode-sized items (M <= 32, whole 64-deep K chunks): the
+  // weight-streaming small-M kernel.  Its lane offsets are 32-bit.
+  if (M <= 32 && K % 64 == 0 && (long long)lda * 2 * 32 <= 0xffffffffLL && (long long)ldb * 2 * 64 <= 0xffffffffLL)
+    return mx::gemm::launch_smallm(A, B, C, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, s);
+  // Otherwise the register-staged kernel with tiles sized to the item.
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * batch;
   if (M >= 128 && t128 >= 256)
     return mx::gemm::launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);

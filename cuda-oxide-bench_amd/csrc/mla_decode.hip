@@ -124,11 +124,15 @@ __device__ __forceinline__ void issue_stage(const unsigned char* kvb, int tok0, 
 // row sum; (m, l) per head in ws_ml.
 constexpr int PT_U32 = VT * 4 * 64 * 2;  // uint32 words per partial tile
 
+// Q is read as its latent part (512 values, rows q_ld elements apart) and
+// its rope part (64 values at Qr, rows qr_ld apart): Qr = Q + 512 with
+// q_ld = qr_ld = 576 for a packed [B,H,576] query.
 __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __restrict__ Q,
+                                                          const uint16_t* __restrict__ Qr,
                                                           const uint16_t* __restrict__ KV,
                                                           uint16_t* __restrict__ O, uint32_t* __restrict__ ws_o,
                                                           float* __restrict__ ws_ml, int B, int H, int T,
-                                                          float sl2, int nsplit, int tps) {
+                                                          float sl2, int nsplit, int tps, int q_ld, int qr_ld) {
   extern __shared__ __align__(1024) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -150,9 +154,11 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
   const int head_s = hgb * HPG + wave * HPW + l32;
   u32x4 qf[KS];
   {
-    const uint16_t* qrow = Q + ((size_t)b * H + min(head_s, H - 1)) * DQK + 8 * hsel;
+    const size_t hrow = (size_t)b * H + min(head_s, H - 1);
+    const uint16_t* qrow = Q + hrow * q_ld + 8 * hsel;
+    const uint16_t* rrow = Qr + hrow * qr_ld + 8 * hsel;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = ld128(qrow + 16 * ks);
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = ks < DV / 16 ? ld128(qrow + 16 * ks) : ld128(rrow + 16 * (ks - DV / 16));
   }
 
   const unsigned char* kvb = reinterpret_cast<const unsigned char*>(KV + (size_t)b * T * DQK);
@@ -452,8 +458,51 @@ inline size_t workspace_bytes(int B, int H, int T) {
   return (size_t)B * sp.nsplit * HW * (PT_U32 * sizeof(uint32_t) + 2 * HPW * sizeof(float));
 }
 
+// The decode (+ combine) launches of one call; arguments already checked.
+static int launch_decode(const void* Q, const void* Qr, int q_ld, int qr_ld, const void* KV, void* O, int B, int H,
+                         int T, float scale, void* workspace, hipStream_t s) {
+  const Split sp = pick_split(B, H, T);
+  const long long HGB = (H + HPG - 1) / HPG;
+  const long long HW = (H + HPW - 1) / HPW;
+  const long long grid = (long long)B * HGB * sp.nsplit;
+  if (grid > 0x7fffffffLL || (long long)B * HW * CMB_PER > 0x7fffffffLL) return MX_ERR_SHAPE;
+  uint32_t* ws_o = (uint32_t*)workspace;
+  float* ws_ml = sp.nsplit > 1 ? reinterpret_cast<float*>(ws_o + (size_t)B * sp.nsplit * HW * PT_U32) : nullptr;
+  MX_RETURN_IF_HIP(
+      hipFuncSetAttribute((const void*)mla_decode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
+  hipLaunchKernelGGL(mla_decode_kernel, dim3((unsigned)grid), dim3(NT), LDS_BYTES, s, (const uint16_t*)Q,
+                     (const uint16_t*)Qr, (const uint16_t*)KV, (uint16_t*)O, ws_o, ws_ml, B, H, T, scale * kLog2e,
+                     sp.nsplit, sp.tps, q_ld, qr_ld);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  if (sp.nsplit > 1) {
+    hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)(B * HW * CMB_PER)), dim3(CMB_WG), 0, s, ws_o, ws_ml,
+                       (uint16_t*)O, H, sp.nsplit);
+    MX_RETURN_IF_HIP(hipGetLastError());
+  }
+  return MX_OK;
+}
+
+static int check_decode(const void* KV, int B, int H, int T, float scale) {
+  if (B <= 0 || H <= 0 || T <= 0) return MX_ERR_SHAPE;
+  if (!(scale > 0.f) || !__builtin_isfinite(scale)) return MX_ERR_SHAPE;
+  if ((long long)B * T * DQK > (1LL << 40) || (long long)B * H > (1LL << 30)) return MX_ERR_SHAPE;
+  if ((uintptr_t)KV & 15) return MX_ERR_ALIGN;
+  return MX_OK;
+}
+
+// Workspace of the absorbed step: q_lat [B,H,512] and o_lat [B,H,512] bf16,
+// each rounded up to 256 bytes, then the decode's split partials.
+inline size_t absorbed_workspace_bytes(int B, int H, int T) {
+  const size_t lat = ((size_t)B * H * DV * 2 + 255) / 256 * 256;
+  return 2 * lat + workspace_bytes(B, H, T);
+}
+
 }  // namespace mla
 }  // namespace mx
+
+extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda,
+                                    int ldb, int ldc, long long strideA, long long strideB, long long strideC,
+                                    void* stream);
 
 extern "C" size_t mx_mla_decode_workspace(int B, int H, int T, int d_latent) {
   if (B <= 0 || H <= 0 || T <= 0 || d_latent != mx::mla::DV) return 0;
@@ -466,29 +515,46 @@ extern "C" int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int 
   if (!Q || !KV || !O) return MX_ERR_NULL;
   if (B <= 0 || H <= 0 || T <= 0) return MX_ERR_SHAPE;
   if (d_latent != DV || d_rope != DQK - DV) return MX_ERR_UNSUPPORTED;
-  if (!(scale > 0.f) || !__builtin_isfinite(scale)) return MX_ERR_SHAPE;
-  if ((long long)B * T * DQK > (1LL << 40) || (long long)B * H > (1LL << 30)) return MX_ERR_SHAPE;
-  if (((uintptr_t)Q | (uintptr_t)KV | (uintptr_t)O) & 15) return MX_ERR_ALIGN;
+  if (const int e = check_decode(KV, B, H, T, scale)) return e;
+  if (((uintptr_t)Q | (uintptr_t)O) & 15) return MX_ERR_ALIGN;
   const size_t need = workspace_bytes(B, H, T);
   if (need > 0 && (!workspace || ws_bytes < need)) return MX_ERR_WORKSPACE;
   if (need > 0 && ((uintptr_t)workspace & 15)) return MX_ERR_ALIGN;
+  return launch_decode(Q, (const uint16_t*)Q + DV, DQK, DQK, KV, O, B, H, T, scale, workspace, (hipStream_t)stream);
+}
+
+extern "C" size_t mx_mla_decode_absorbed_workspace(int B, int H, int T) {
+  if (B <= 0 || H <= 0 || T <= 0) return 0;
+  return mx::mla::absorbed_workspace_bytes(B, H, T);
+}
+
+extern "C" int mx_mla_decode_absorbed(const void* q_nope, const void* q_rope, const void* KV, const void* w_uk,
+                                      const void* w_uv, void* O, int B, int H, int T, int d_nope, int d_v,
+                                      float scale, void* workspace, size_t ws_bytes, void* stream) {
+  using namespace mx::mla;
+  if (!q_nope || !q_rope || !KV || !w_uk || !w_uv || !O) return MX_ERR_NULL;
+  if (const int e = check_decode(KV, B, H, T, scale)) return e;
+  if (d_nope <= 0 || d_v <= 0 || (d_nope % 8) || (d_v % 8) || d_nope > 4096 || d_v > 4096) return MX_ERR_SHAPE;
+  if (B > 65535 || H > 65535) return MX_ERR_SHAPE;
+  if (((uintptr_t)q_nope | (uintptr_t)q_rope | (uintptr_t)w_uk | (uintptr_t)w_uv | (uintptr_t)O) & 15)
+    return MX_ERR_ALIGN;
+  const size_t need = absorbed_workspace_bytes(B, H, T);
+  if (!workspace || ws_bytes < need) return MX_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  const Split sp = pick_split(B, H, T);
-  const long long HGB = (H + HPG - 1) / HPG;
-  const long long HW = (H + HPW - 1) / HPW;
-  const long long grid = (long long)B * HGB * sp.nsplit;
-  if (grid > 0x7fffffffLL || (long long)B * HW * CMB_PER > 0x7fffffffLL) return MX_ERR_SHAPE;
-  uint32_t* ws_o = (uint32_t*)workspace;
-  float* ws_ml = sp.nsplit > 1 ? reinterpret_cast<float*>(ws_o + (size_t)B * sp.nsplit * HW * PT_U32) : nullptr;
-  MX_RETURN_IF_HIP(
-      hipFuncSetAttribute((const void*)mla_decode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
-  hipLaunchKernelGGL(mla_decode_kernel, dim3((unsigned)grid), dim3(NT), LDS_BYTES, s, (const uint16_t*)Q,
-                     (const uint16_t*)KV, (uint16_t*)O, ws_o, ws_ml, B, H, T, scale * kLog2e, sp.nsplit, sp.tps);
-  MX_RETURN_IF_HIP(hipGetLastError());
-  if (sp.nsplit > 1) {
-    hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)(B * HW * CMB_PER)), dim3(CMB_WG), 0, s, ws_o, ws_ml,
-                       (uint16_t*)O, H, sp.nsplit);
-    MX_RETURN_IF_HIP(hipGetLastError());
-  }
-  return MX_OK;
+  const size_t lat = ((size_t)B * H * DV * 2 + 255) / 256 * 256;
+  unsigned char* ws = (unsigned char*)workspace;
+  void* q_lat = ws;
+  void* o_lat = ws + lat;
+  void* dws = workspace_bytes(B, H, T) ? (void*)(ws + 2 * lat) : nullptr;
+  // q_lat[b,h,:] = q_nope[b,h,:] . W_UK[h]   (one product per head)
+  int rc = mx_gemm_bf16_batched(q_nope, w_uk, q_lat, H, B, DV, d_nope, H * d_nope, DV, H * DV, d_nope,
+                                (long long)d_nope * DV, DV, stream);
+  if (rc) return rc;
+  // latent attention with Q = [q_lat, q_rope]
+  rc = launch_decode(q_lat, q_rope, DV, DQK - DV, KV, o_lat, B, H, T, scale, dws, s);
+  if (rc) return rc;
+  // o[b,h,:] = o_lat[b,h,:] . W_UV[h]
+  return mx_gemm_bf16_batched(o_lat, w_uv, O, H, B, d_v, DV, H * DV, d_v, H * d_v, DV, (long long)DV * d_v, d_v,
+                              stream);
 }

@@ -324,26 +324,37 @@ def mla_up_project(o_lat, w_uv, out=None):
     return out
 
 
-def mla_decode_absorbed(q_nope, q_rope, kv, w_uk, w_uv, scale, q_buf=None, o_lat=None, out=None, workspace=None):
+def mla_decode_absorbed_workspace_bytes(B: int, H: int, T: int) -> int:
+    return int(_lib.load().mx_mla_decode_absorbed_workspace(B, H, T))
+
+
+def mla_decode_absorbed(q_nope, q_rope, kv, w_uk, w_uv, scale, out=None, workspace=None):
     """Full weight-absorbed MLA decode step (MECHANISMS.md:77-94, 115-120):
-    q_lat = q_nope @ W_UK[h] written into Q[..., :512] next to q_rope,
-    latent attention over the KV cache (mla_decode), then o = o_lat @ W_UV[h].
-    q_nope [B,H,128], q_rope [B,H,64], kv [B,T,576], w_uk [H,128,512],
-    w_uv [H,512,dv], all bf16 -> o [B,H,dv]."""
-    _require(q_rope, "q_rope", (torch.bfloat16,), 3)
-    B, Hh, _ = q_nope.shape
-    dc = w_uk.shape[2]
-    if q_buf is None:
-        q_buf = torch.empty((B, Hh, dc + q_rope.shape[2]), dtype=torch.bfloat16, device=q_nope.device)
-    _require(q_buf, "q_buf", (torch.bfloat16,), 3)
-    if tuple(q_buf.shape) != (B, Hh, dc + q_rope.shape[2]) or tuple(q_rope.shape[:2]) != (B, Hh):
-        raise ValueError("q_buf must be [B, H, d_c + d_rope] and q_rope [B, H, d_rope]")
-    _require(q_nope, "q_nope", (torch.bfloat16,), 3)
-    _require(w_uk, "w_uk", (torch.bfloat16,), 3)
-    if w_uk.shape[0] != Hh or w_uk.shape[1] != q_nope.shape[2]:
-        raise ValueError(f"w_uk must be [{Hh}, {q_nope.shape[2]}, d_c], got {tuple(w_uk.shape)}")
-    _same_device(q_nope, q_rope, w_uk, q_buf)
-    _head_gemm(q_nope, w_uk, q_buf, q_buf.shape[2])   # q_lat into q_buf[..., :d_c]
-    q_buf[..., dc:].copy_(q_rope)
-    o_lat = mla_decode(q_buf, kv, scale, out=o_lat, workspace=workspace)
-    return mla_up_project(o_lat, w_uv, out=out)
+    q_lat = q_nope @ W_UK[h], latent attention of [q_lat, q_rope] over the
+    KV cache, o = o_lat @ W_UV[h] — one C-ABI call (mx_mla_decode_absorbed).
+    q_nope [B,H,dn], q_rope [B,H,64], kv [B,T,576], w_uk [H,dn,512],
+    w_uv [H,512,dv], all bf16 -> o [B,H,dv].  Pass `workspace` (uint8, at
+    least mla_decode_absorbed_workspace_bytes) to allocate nothing."""
+    for t, n in ((q_nope, "q_nope"), (q_rope, "q_rope"), (kv, "kv"), (w_uk, "w_uk"), (w_uv, "w_uv")):
+        _require(t, n, (torch.bfloat16,), 3)
+    B, Hh, dn = q_nope.shape
+    T = kv.shape[1]
+    if tuple(q_rope.shape) != (B, Hh, 64) or kv.shape[0] != B or kv.shape[2] != 576:
+        raise ValueError(f"q_rope must be {(B, Hh, 64)} and kv [B, T, 576]")
+    if tuple(w_uk.shape) != (Hh, dn, 512) or w_uv.shape[0] != Hh or w_uv.shape[1] != 512:
+        raise ValueError(f"w_uk must be {(Hh, dn, 512)} and w_uv [{Hh}, 512, dv]")
+    dv = w_uv.shape[2]
+    if out is None:
+        out = torch.empty((B, Hh, dv), dtype=torch.bfloat16, device=q_nope.device)
+    _require(out, "out", (torch.bfloat16,), 3)
+    if tuple(out.shape) != (B, Hh, dv):
+        raise ValueError(f"out must be {(B, Hh, dv)}")
+    need = mla_decode_absorbed_workspace_bytes(B, Hh, T)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need + 256, dtype=torch.uint8, device=q_nope.device)
+    ws_ptr = (workspace.data_ptr() + 255) // 256 * 256
+    ws_bytes = workspace.numel() * workspace.element_size() - (ws_ptr - workspace.data_ptr())
+    _same_device(q_nope, q_rope, kv, w_uk, w_uv, out, workspace)
+    _lib.call("mx_mla_decode_absorbed", q_nope.data_ptr(), q_rope.data_ptr(), kv.data_ptr(), w_uk.data_ptr(),
+              w_uv.data_ptr(), out.data_ptr(), B, Hh, T, dn, dv, float(scale), ws_ptr, ws_bytes, _stream())
+    return out

@@ -141,6 +141,26 @@ int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int H, int T, i
 size_t mx_mla_decode_workspace(int B, int H, int T, int d_latent);
 
 /*
+ * The whole weight-absorbed MLA decode step (DeepSeek-V3 form):
+ *   q_lat[b,h,:] = q_nope[b,h,:] · W_UK[h]              (d_nope -> 512)
+ *   o_lat[b,h,:] = mx_mla_decode with Q = [q_lat, q_rope] over KV[b]
+ *   O[b,h,:]     = o_lat[b,h,:] · W_UV[h]                (512 -> d_v)
+ * q_nope [B,H,d_nope], q_rope [B,H,64], KV [B,T,576], W_UK [H,d_nope,512],
+ * W_UV [H,512,d_v], O [B,H,d_v], all bf16 row-major; fp32 accumulation,
+ * q_lat and o_lat rounded to bf16.  The workspace (q_lat, o_lat and the
+ * decode's split partials) is sized by mx_mla_decode_absorbed_workspace and
+ * must be 256-byte aligned.  d_nope, d_v multiples of 8 (<= 4096).
+ * Replaces: the per-head up-projections either side of the absorbed decode
+ * that analysis/wave15-attention-research/MECHANISMS.md:77-94, 115-120
+ * describes (the reference ships only the pre-projected prefill cell,
+ * cutile-attn-mla/main.py:81-163).
+ */
+int mx_mla_decode_absorbed(const void* q_nope, const void* q_rope, const void* KV, const void* w_uk,
+                           const void* w_uv, void* O, int B, int H, int T, int d_nope, int d_v,
+                           float scale, void* workspace, size_t ws_bytes, void* stream);
+size_t mx_mla_decode_absorbed_workspace(int B, int H, int T);
+
+/*
  * Gated-DeltaNet single-token recurrent decode, per (b, value head hv),
  * with key head hk = hv / (Hv / Hk):
  *   u     = alpha * (k^T S)                  (d_v)

@@ -24,7 +24,8 @@ def declared_functions() -> list[str]:
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("mx_gemm_bf16", "mx_gemm_fp8_bs", "mx_gqa_fwd", "mx_mla_decode", "mx_mla_decode_workspace",
-              "mx_gdn_decode", "mx_kda_decode", "mx_quant_fp8_act", "mx_gemm_bf16_batched", "mx_strerror",
+              "mx_gdn_decode", "mx_kda_decode", "mx_quant_fp8_act", "mx_gemm_bf16_batched", "mx_mla_decode_absorbed",
+              "mx_mla_decode_absorbed_workspace", "mx_strerror",
               "mx_version"):
         assert n in names
 
@@ -128,3 +129,15 @@ def test_gemm_batched_validation():
     assert f(P, P, P, 70000, 64, 64, 64, 64, 64, 64, 0, 0, 0, None) == _lib.MX_ERR_SHAPE
     assert f(P, P, P, 2, 64, 64, 64, 64, 64, 64, -8, 0, 0, None) == _lib.MX_ERR_SHAPE
     assert f(P, P, P, 2, 64, 64, 64, 64, 64, 64, 4, 0, 0, None) == _lib.MX_ERR_ALIGN
+
+
+def test_mla_absorbed_validation():
+    lib = _lib.load()
+    f = lib.mx_mla_decode_absorbed
+    need = lib.mx_mla_decode_absorbed_workspace(32, 128, 4096)
+    assert need >= 2 * 32 * 128 * 512 * 2
+    assert f(None, P, P, P, P, P, 32, 128, 4096, 128, 128, 0.07, P, need, None) == _lib.MX_ERR_NULL
+    assert f(P, P, P, P, P, P, 32, 128, 4096, 128, 128, 0.07, None, 0, None) == _lib.MX_ERR_WORKSPACE
+    assert f(P, P, P, P, P, P, 32, 128, 4096, 128, 128, 0.07, P, need - 1, None) == _lib.MX_ERR_WORKSPACE
+    assert f(P, P, P, P, P, P, 32, 128, 4096, 100, 128, 0.07, P, need, None) == _lib.MX_ERR_SHAPE
+    assert f(P, P, P, P, P, P, 32, 128, 4096, 128, 128, -1.0, P, need, None) == _lib.MX_ERR_SHAPE

@@ -124,7 +124,7 @@ def test_rejects_bad_arguments(ops):
         ops.gemm_bf16(a, b)
 
 
-@pytest.mark.parametrize("bmnk", [(1, 64, 64, 64), (7, 100, 136, 72), (128, 32, 512, 128), (128, 32, 128, 512),
+@pytest.mark.parametrize("bmnk", [(1, 64, 64, 64), (7, 100, 136, 72), (128, 32, 512, 128), (128, 32, 128, 512), (16, 5, 40, 192),
                                   (3, 300, 264, 520)])
 def test_batched_vs_oracle(ops, bmnk):
     """Strided-batched GEMM: every item against the fp32 oracle."""

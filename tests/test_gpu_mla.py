@@ -120,3 +120,20 @@ def test_absorbed_pipeline(ops):
     torch.cuda.synchronize()
     ref = omla.mla_absorbed_ref(x["q_nope"], x["q_rope"], kv, x["w_uk"], x["w_uv"], s.scale)
     assert normwise_rel_err(o.cpu(), ref) <= 2e-2
+
+
+@pytest.mark.parametrize("b,h,t,dv", [(32, 128, 4096, 128), (40, 16, 300, 64), (1, 128, 64, 128)])
+def test_absorbed_step_shapes(ops, b, h, t, dv):
+    """The one-call absorbed step at the BASELINE shape (split decode,
+    small-M projections), a batch above 32 (register-staged projections)
+    and a single sequence (unsplit decode)."""
+    announce(f"mla absorbed step B{b} H{h} T{t} dv{dv}")
+    s = shapes.MLADecodeShape("t", batch=b, n_h=h, ctx=t)
+    _, kv = inputs.mla_inputs(s)
+    x = inputs.mla_projection_inputs(s, d_v=dv)
+    d = {k: v.cuda() for k, v in x.items()}
+    o = ops.mla_decode_absorbed(d["q_nope"], d["q_rope"], kv.cuda(), d["w_uk"], d["w_uv"], s.scale)
+    torch.cuda.synchronize()
+    bs = list(range(min(b, 4)))
+    ref = omla.mla_absorbed_ref(x["q_nope"][bs], x["q_rope"][bs], kv[bs], x["w_uk"], x["w_uv"], s.scale)
+    assert normwise_rel_err(o.cpu()[bs], ref) <= 2e-2
