@@ -342,10 +342,10 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 #pragma unroll
           for (int e = 0; e < 16; ++e) neg_m[qt][e] = -m_run[qt];
         }
+        // exp2 of key chunk 0 now; chunk c+1 is exponentiated inside the
+        // P.V step of chunk c, in the shadow of its MFMAs.
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) s[qt][t][e] = __builtin_amdgcn_exp2f(s[qt][t][e]);
+        for (int e = 0; e < 8; ++e) s[qt][0][e] = __builtin_amdgcn_exp2f(s[qt][0][e]);
       }
 
       __builtin_amdgcn_s_setprio(1);
@@ -370,11 +370,28 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
         if (c + 1 < 4) {
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) vb[(c + 1) & 1][dt] = vread(c + 1, dt);
+          const int t1 = (c + 1) >> 1, j1 = 8 * ((c + 1) & 1);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[qt][t1][j1 + e] = __builtin_amdgcn_exp2f(s[qt][t1][j1 + e]);
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) acc_o[qt][dt] = mfma32<T>(vb[c & 1][dt], pf[qt], acc_o[qt][dt]);
+        if (c + 1 < 4) {
+          // packs and row sums of chunk c first, then each MFMA followed by
+          // its share of chunk c+1's exp2 and the next chunk's V reads
+          __builtin_amdgcn_sched_group_barrier(0x002, 4 * QT, 0);
+#pragma unroll
+          for (int m = 0; m < DT * QT; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x400, 8 * QT / (DT * QT), 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT / (DT * QT), 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4 * QT / (DT * QT), 0);
+          }
+        }
         __builtin_amdgcn_sched_barrier(0);  // keep the one-chunk read lookahead
       }
 #pragma unroll
