@@ -37,6 +37,8 @@
 //    its normalised partial output (bf16, coalesced 512 B stores) and
 //    (m, l) to the workspace, and a second kernel merges the splits with
 //    the log-sum-exp rule.  With one split, O is written directly.
+#include <type_traits>
+
 #include "mx_common.h"
 
 namespace mx {
@@ -101,22 +103,22 @@ __host__ __device__ inline Split pick_split(int B, int H, int T) {
 // j <- chunk j ^ swz(t), from a wave-uniform row address) or eight rope
 // rows.  Rows past the end of the split re-read the last valid row (finite
 // data whose scores are masked).
-__device__ __forceinline__ void issue_stage(const unsigned char* kvb, int tok0, int t1, uint32_t lat, uint32_t rope,
-                                            int wave, int lane) {
+__device__ __forceinline__ void issue_part(const unsigned char* kvb, int tok0, int t1, uint32_t lat, uint32_t rope,
+                                           int wave, int lane, int n) {
   constexpr int LR = BT / NWAVES;  // latent rows per wave
-  uint32_t l16 = lane * 16;
-  asm volatile("" : "+v"(l16));  // keep the per-row XORs here instead of 8 hoisted VGPRs
-#pragma unroll
-  for (int n = 0; n < LR; ++n) {
+  if (n < LR) {
+    uint32_t l16 = lane * 16;
+    asm volatile("" : "+v"(l16));  // keep the per-row XOR here instead of a hoisted VGPR per row
     const int r = wave * LR + n;
     const int tok = min(tok0 + r, t1 - 1);
     dma16(kvb + (size_t)tok * ROW_B, l16 ^ (uint32_t)(16 * swz(r)), lat + r * 1024);
+  } else {
+    const int r0 = wave * 8;
+    const int tb = min(tok0 + r0, t1 - 1);
+    const int tok = min(tok0 + r0 + (lane >> 3), t1 - 1);
+    const uint32_t off = (uint32_t)(tok - tb) * ROW_B + 16 * (64 + ((lane & 7) ^ swz(lane >> 3)));
+    dma16(kvb + (size_t)tb * ROW_B, off, rope + r0 * 128);
   }
-  const int r0 = wave * 8;
-  const int tb = min(tok0 + r0, t1 - 1);
-  const int tok = min(tok0 + r0 + (lane >> 3), t1 - 1);
-  const uint32_t off = (uint32_t)(tok - tb) * ROW_B + 16 * (64 + ((lane & 7) ^ swz(lane >> 3)));
-  dma16(kvb + (size_t)tb * ROW_B, off, rope + r0 * 128);
 }
 
 // Partial tile of one (sequence, split, 32-head group): 64 slots (latent
@@ -163,9 +165,14 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 
   const unsigned char* kvb = reinterpret_cast<const unsigned char*>(KV + (size_t)b * T * DQK);
   const uint32_t lds0 = lds_addr(smem);
+  // part n (0..LPW-1) of this wave's direct loads of stage i
+  auto issue_p = [&](int i, int n) {
+    issue_part(kvb, t0 + i * BT, t1, lds0 + (i & (NLAT - 1)) * LAT_B, lds0 + ROPE_OFF + (i % NROPE) * ROPE_B, wave,
+               lane, n);
+  };
   auto issue = [&](int i) {
-    issue_stage(kvb, t0 + i * BT, t1, lds0 + (i & (NLAT - 1)) * LAT_B, lds0 + ROPE_OFF + (i % NROPE) * ROPE_B, wave,
-                lane);
+#pragma unroll
+    for (int n = 0; n < LPW; ++n) issue_p(i, n);
   };
   // Ring prologue.  The Q loads complete together with stage 0, so no
   // compiler-visible load is outstanding once the cache loads stream.
@@ -199,16 +206,16 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
     for (int dt = 0; dt < VTW; ++dt) acc[g][dt] = f32x16{};
   float m_run = -1e30f, l_run = 0.f;
 
-  // ---- scores of stage si for head group `wave`, then the online softmax;
-  // P^T (bf16, B-operand layout, k order: tokens 4 hsel + j then
-  // 8 + 4 hsel + j), the rescale flag and factors go to buffer si&1 ----
-  auto scores = [&](int si) {
+  // ---- S^T of stage si for head group `wave` (36 k-steps, two chains).
+  // With dma >= 0, this wave's direct loads of stage dma are issued one
+  // per 4 k-steps, so they queue behind MFMAs instead of stalling the wave
+  // at the address unit all at once. ----
+  auto score_mfma = [&](int si, int dma) {
     const unsigned char* lat = smem + (si & (NLAT - 1)) * LAT_B;
     const unsigned char* rope = smem + ROPE_OFF + (si % NROPE) * ROPE_B - l32 * (1024 - 128);
     auto kread = [&](int ks) {
       return ks < 32 ? ld128(lat + koff[ks & 3] + 128 * (ks >> 2)) : ld128(rope + koff[ks & 3]);
     };
-    // K reads run KLA k-steps ahead of the MFMAs; two accumulation chains.
     constexpr int KLA = 6;
     f32x16 sa = f32x16{}, sb = f32x16{};
     u32x4 kf[8];
@@ -221,21 +228,28 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
         sb = mfma32<BF16>(kf[ks & 7], qf[ks], sb);
       else
         sa = mfma32<BF16>(kf[ks & 7], qf[ks], sa);
+      if ((ks & 3) == 2 && ks / 4 < LPW && dma >= 0) issue_p(dma, ks / 4);
       __builtin_amdgcn_sched_barrier(0);
     }
-    f32x16 sc = sa + sb;
+    return sa + sb;
+  };
 
-    // lane holds head l32, tokens tb + 8 i + 4 hsel + j for sc[4 i + j]
+  // Softmax pieces of stage si on its scores sc (lane holds head l32,
+  // tokens tb + 8 i + 4 hsel + j for sc[4 i + j]).
+  auto scale_mask = [&](f32x16& sc, int si, int r0, int r1, float& mx) {
     const int tb = t0 + si * BT;
     const bool need_mask = tb + BT > t1;
-    float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int r = r0; r < r1; ++r) {
       float x = sc[r] * sl2;
       if (need_mask && tb + 8 * (r >> 2) + 4 * hsel + (r & 3) >= t1) x = -INFINITY;
       sc[r] = x;
       mx = fmaxf(mx, x);
     }
+  };
+  // Lazy running-max update; the rescale flag and factors of stage si go
+  // to buffer si&1 for the value waves.
+  auto update_max = [&](float mx, int si) {
     mx = max_xor32(mx);
     int* flags = reinterpret_cast<int*>(smem + F_OFF) + (si & 1) * NWAVES;
     float* corrs = reinterpret_cast<float*>(smem + C_OFF) + ((si & 1) * NWAVES + wave) * 32;
@@ -249,22 +263,35 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
       flag = si > 0;  // at stage 0 the value accumulators are still zero
     }
     if (lane == 0) flags[wave] = flag;
+  };
+  // P^T chunk k2 (bf16, B-operand layout, k order: tokens 4 hsel + j then
+  // 8 + 4 hsel + j) of stage si to LDS, and its row sum.
+  auto p_chunk = [&](const f32x16& sc, int si, int k2) {
     u32x4* pbuf = reinterpret_cast<u32x4*>(smem + P_OFF + (si & 1) * P_BUF);
+    float p[8];
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      float p[8];
+    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(sc[8 * k2 + e] - m_run);
+    const u32x4 pf{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                   pack_bf16x2(p[6], p[7])};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(sc[8 * k2 + e] - m_run);
-      const u32x4 pf{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                     pack_bf16x2(p[6], p[7])};
-#pragma unroll
-      for (int w = 0; w < 4; ++w) l_run = dot2_ones<BF16>(pf[w], l_run);
-      pbuf[(wave * 2 + k2) * 64 + lane] = pf;
-    }
+    for (int w = 0; w < 4; ++w) l_run = dot2_ones<BF16>(pf[w], l_run);
+    pbuf[(wave * 2 + k2) * 64 + lane] = pf;
+  };
+  auto scores_alone = [&](int si, int dma) {
+    f32x16 sc = score_mfma(si, dma);
+    float mx = -INFINITY;
+    scale_mask(sc, si, 0, 16, mx);
+    update_max(mx, si);
+    p_chunk(sc, si, 0);
+    p_chunk(sc, si, 1);
   };
 
-  // ---- values of stage pi: O^T[128 wave + 32 dt .., heads] += V^T . P^T ----
-  auto values = [&](int pi) {
+  // ---- values of stage pi: O^T[128 wave + 32 dt .., heads] += V^T . P^T.
+  // With SOFT, the softmax of stage pi+1 (scores sc) runs beside the MFMAs:
+  // scale, mask and max beside the first k half, exp2 / P^T beside the
+  // second. ----
+  auto values = [&](int pi, auto with_soft, f32x16& sc) {
+    constexpr bool SOFT = decltype(with_soft)::value;
     // all four flags in one LDS read (one wait instead of four)
     const u32x4 fl = *reinterpret_cast<const u32x4*>(smem + F_OFF + (pi & 1) * NWAVES * 4);
 #pragma unroll
@@ -290,6 +317,7 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
         const u32x2 hi = lds_read_tr16(p + 8 * 1024);
         vf[k2][dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
+    float mx = -INFINITY;
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
       u32x4 pb[2];
@@ -299,43 +327,45 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
         if (g + 1 < NWAVES) pb[(g + 1) & 1] = pbuf[((g + 1) * 2 + k2) * 64 + lane];
 #pragma unroll
         for (int dt = 0; dt < VTW; ++dt) acc[g][dt] = mfma32<BF16>(vf[k2][dt], pb[g & 1], acc[g][dt]);
+        if constexpr (SOFT) {
+          if (k2 == 0)
+            scale_mask(sc, pi + 1, 4 * g, 4 * g + 4, mx);
+          else if (g & 1)
+            p_chunk(sc, pi + 1, g >> 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (SOFT) {
+        if (k2 == 0) update_max(mx, pi + 1);
       }
     }
   };
 
-  // Iteration i: scores of stage i and values of stage i-1 (either order
-  // per wave).  Slot reuse: stage i+2 overwrites latent slot (i+2)%4
-  // (stage i-2, whose values finished before this iteration's barrier) and
-  // rope slot (i+2)%3 (stage i-1, whose scores did); the P^T/flag buffers
-  // alternate by stage.
+  // Iteration i: scores of stage i (S^T MFMAs, with the direct loads of
+  // stage i+2 spread among them), then the values of stage i-1 with the
+  // softmax of stage i beside them.  Slot reuse: stage i+2 overwrites
+  // latent slot (i+2)%4 (stage i-2, whose values finished before this
+  // iteration's barrier) and rope slot (i+2)%3 (stage i-1, whose scores
+  // did); the P^T/flag buffers alternate by stage.
   auto sync = [&](int i) {
     if (i + 1 < nblk)
       wait_vmcnt<LPW>();
     else
       wait_vmcnt<0>();
     __syncthreads();  // stage i landed for all waves; P^T of stage i-1 visible
-    if (i + 2 < nblk) issue(i + 2);
   };
-  if (wave & 1) {
-    sync(0);
-    scores(0);
-    for (int i = 1; i < nblk; ++i) {
-      sync(i);
-      values(i - 1);
-      scores(i);
-    }
-  } else {
-    sync(0);
-    scores(0);
-    for (int i = 1; i < nblk; ++i) {
-      sync(i);
-      scores(i);
-      values(i - 1);
-    }
+  sync(0);
+  scores_alone(0, nblk > 2 ? 2 : -1);
+  for (int i = 1; i < nblk; ++i) {
+    sync(i);
+    f32x16 sc = score_mfma(i, i + 2 < nblk ? i + 2 : -1);
+    values(i - 1, std::true_type{}, sc);
   }
   sync(nblk);
-  values(nblk - 1);
+  {
+    f32x16 none{};
+    values(nblk - 1, std::false_type{}, none);
+  }
 
   // Row sums to the value waves; (m, l) of each split to the workspace.
   const float l_tot = sum_xor32(l_run);
