@@ -67,10 +67,13 @@ constexpr int C_OFF = P_OFF + 2 * P_BUF;               // rescale factors: [2 bu
 constexpr int F_OFF = C_OFF + 2 * NWAVES * 32 * 4;     // rescale flags: [2 buf][4 group] int
 constexpr int L_OFF = F_OFF + 2 * NWAVES * 4;          // final row sums: [4 group][32] fp32
 constexpr int LDS_BYTES = L_OFF + NWAVES * 32 * 4;
+constexpr int Q_WAVE_B = HPW * (1024 + 128);            // Q staging per wave (prologue only)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 16.0f;          // log2 headroom before a rescale
 static_assert(BT * DQK / 8 == 64 * NWAVES * LPW, "a stage splits into whole wave loads");
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+static_assert(NWAVES * Q_WAVE_B <= LDS_BYTES, "Q staging fits the LDS allocation");
+static_assert(DV / 16 == 32 && (DQK - DV) / 16 == 4, "Q fragment split: 32 latent + 4 rope k-steps");
 
 // Chunk c of row t sits at chunk position c ^ swz(t) of its row.  swz maps
 // t%8 to 0,2,4,6,1,3,5,7: distinct over 8 rows (K reads: 8 consecutive
@@ -153,18 +156,45 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 
   // Score role: heads hgb*128 + 32*wave + l32.  Padding heads (>= H) reuse
   // the last real head's row; their results are never stored.
-  const int head_s = hgb * HPG + wave * HPW + l32;
-  u32x4 qf[KS];
-  {
-    const size_t hrow = (size_t)b * H + min(head_s, H - 1);
-    const uint16_t* qrow = Q + hrow * q_ld + 8 * hsel;
-    const uint16_t* rrow = Qr + hrow * qr_ld + 8 * hsel;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = ks < DV / 16 ? ld128(qrow + 16 * ks) : ld128(rrow + 16 * (ks - DV / 16));
-  }
-
   const unsigned char* kvb = reinterpret_cast<const unsigned char*>(KV + (size_t)b * T * DQK);
   const uint32_t lds0 = lds_addr(smem);
+
+  // Q^T fragments of the wave's 32 heads.  The rows go HBM -> LDS with
+  // direct loads, one 1 KB head row (latent part) or eight 128 B rope rows
+  // per instruction, so every load is a contiguous run of the row; chunk c
+  // of head h sits at position c ^ (h & 15) within its 256 B group (latent)
+  // or c ^ ((h >> 1) & 7) (rope), which makes the fragment reads below
+  // bank-conflict free.  Each wave stages into its own 36 KB, before the
+  // cache ring starts.  Padding heads (>= H) read the last real head.
+  u32x4 qf[KS];
+  {
+    const int h0 = hgb * HPG + wave * HPW;
+    const int hb = min(h0, H - 1);
+    const unsigned char* qb = reinterpret_cast<const unsigned char*>(Q + ((size_t)b * H + hb) * q_ld);
+    const unsigned char* rb = reinterpret_cast<const unsigned char*>(Qr + ((size_t)b * H + hb) * qr_ld);
+    const uint32_t qs = lds0 + wave * Q_WAVE_B;
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+      const int row = min(h0 + j, H - 1) - hb;
+      const int c = (lane & ~15) | ((lane ^ j) & 15);
+      dma16(qb, (uint32_t)row * q_ld * 2 + 16 * c, qs + j * 1024);
+    }
+#pragma unroll
+    for (int j = 0; j < HPW / 8; ++j) {
+      const int hl = 8 * j + (lane >> 3);
+      const int row = min(h0 + hl, H - 1) - hb;
+      const int c = (lane & 7) ^ ((hl >> 1) & 7);
+      dma16(rb, (uint32_t)row * qr_ld * 2 + 16 * c, qs + HPW * 1024 + j * 1024);
+    }
+    wait_vmcnt<0>();  // this wave's rows landed; only this wave reads them
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int c = 2 * (ks & 31) + hsel;
+      qf[ks] = ks < DV / 16 ? lds_ld128(qs + l32 * 1024 + 16 * ((c & ~15) | ((c ^ l32) & 15)))
+                            : lds_ld128(qs + HPW * 1024 + l32 * 128 + 16 * ((c & 7) ^ ((l32 >> 1) & 7)));
+    }
+    __syncthreads();  // every wave holds its fragments before the ring overwrites the staging area
+  }
   // part n (0..LPW-1) of this wave's direct loads of stage i
   auto issue_p = [&](int i, int n) {
     issue_part(kvb, t0 + i * BT, t1, lds0 + (i & (NLAT - 1)) * LAT_B, lds0 + ROPE_OFF + (i % NROPE) * ROPE_B, wave,
@@ -174,10 +204,8 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 #pragma unroll
     for (int n = 0; n < LPW; ++n) issue_p(i, n);
   };
-  // Ring prologue.  The Q loads complete together with stage 0, so no
-  // compiler-visible load is outstanding once the cache loads stream.
+  // Ring prologue.
   issue(0);
-  wait_vmcnt<0>();
   if (nblk > 1) issue(1);
 
   // K fragment (A operand): row l32, chunk c = 2 ks + hsel at position
