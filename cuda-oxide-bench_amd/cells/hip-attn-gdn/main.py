@@ -2,7 +2,8 @@
 
 Drop-in for cutile-attn-gdn/main.py: flags --smoke (default), --bench,
 --csv-out, --shape {registry} (default qwen3_next_decode), --export-cubin /
---cubin-out (accepted).  --smoke runs the reference's SHAPE_CORRECTNESS
+--cubin-out (accepted), --inputs-dir / --fixture (replay a
+gdn_<fixture>_*.npy set written in the reference's inputs/ layout).  --smoke runs the reference's SHAPE_CORRECTNESS
 (B2 H4 d64, f16, reference inputs) against the committed golden oracle
 output with the reference's gates (o: f16 allclose 5e-3; S: max_abs < 5e-3
 or rel < 5e-3, :283-298) and this path's normwise bounds (o 2e-2, S 1e-3).
@@ -27,18 +28,32 @@ WARMUP = 2
 ITERS = 50
 
 
-def run_smoke() -> bool:
+def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness") -> bool:
+    """The correctness check: the committed golden set, or with inputs_dir a
+    fixture set in the reference's inputs/ layout (gdn_<fixture>_*.npy:
+    f16 q/k/v/alpha/beta, f32 S_in, f16 o and f32 S_out expected;
+    cutile-attn-gdn/main.py:193-204)."""
     import numpy as np
     import torch
 
     pkg = H.package()
     ops = pkg.load_ops()
-    s = pkg.shapes.GDN_CORRECTNESS
-    print(f"[smoke] shape={s.name} B={s.batch} H={s.n_heads} d_k={s.d_k} d_v={s.d_v}")
-    g = H.load_golden("gdn_correctness_f16")
-    dt = torch.float16
-    args = [H.from_bits(g[n], dt).cuda() for n in ("q", "k", "v")]
-    args += [torch.from_numpy(g[n]).cuda() for n in ("alpha", "beta", "S_in")]
+    if inputs_dir:
+        fx = H.reference_fixtures(inputs_dir, "gdn", fixture)
+        args = [torch.from_numpy(fx[n]).cuda() for n in ("q", "k", "v")]
+        # gates are f16 on disk; the kernel takes them as fp32 (exact widening)
+        args += [torch.from_numpy(fx[n].astype(np.float32)).cuda() for n in ("alpha", "beta")]
+        args += [torch.from_numpy(fx["S_in"]).cuda()]
+        g = {"o": fx["o_expected"].astype(np.float32), "S_out": fx["S_out_expected"]}
+        print(f"[smoke] fixture={fixture} B={args[0].shape[0]} H={args[0].shape[1]} d_k={args[0].shape[2]} "
+              f"d_v={args[2].shape[2]}")
+    else:
+        s = pkg.shapes.GDN_CORRECTNESS
+        print(f"[smoke] shape={s.name} B={s.batch} H={s.n_heads} d_k={s.d_k} d_v={s.d_v}")
+        g = H.load_golden("gdn_correctness_f16")
+        dt = torch.float16
+        args = [H.from_bits(g[n], dt).cuda() for n in ("q", "k", "v")]
+        args += [torch.from_numpy(g[n]).cuda() for n in ("alpha", "beta", "S_in")]
     o, so = ops.gdn_decode(*args)
     torch.cuda.synchronize()
     o32, s32 = o.float().cpu().numpy(), so.cpu().numpy()
@@ -101,6 +116,9 @@ def main() -> int:
     ap.add_argument("--csv-out", default="results.csv")
     ap.add_argument("--cubin-out", default="gdn_decode_fused.cubin")
     ap.add_argument("--shape", default="qwen3_next_decode", choices=sorted(reg.keys()))
+    ap.add_argument("--inputs-dir", default=None,
+                    help="replay a fixture set written in the reference's inputs/ layout")
+    ap.add_argument("--fixture", default="correctness", help="fixture shape name (gdn_<fixture>_*.npy)")
     args = ap.parse_args()
     if not (args.smoke or args.bench or args.export_cubin):
         args.smoke = True
@@ -108,7 +126,7 @@ def main() -> int:
     print()
     rc = H.EXIT_OK
     if args.smoke:
-        if not run_smoke():
+        if not run_smoke(args.inputs_dir, args.fixture):
             rc = H.EXIT_SMOKE_FAIL
         print()
     if args.bench:

@@ -32,20 +32,30 @@ ITERS = 10
 BLOCK_M, BLOCK_N = 32, 64   # queries per wave tile, keys per LDS tile (fixed in the kernel)
 
 
-def run_smoke() -> bool:
+def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness") -> bool:
+    """The correctness check: the committed golden set, or with inputs_dir a
+    fixture set in the reference's inputs/ layout (gqa_<fixture>_*.npy,
+    f16 inputs, f32 expected output; cutile-attn-gqa/main.py:177-183)."""
     import numpy as np
     import torch
 
     pkg = H.package()
     ops = pkg.load_ops()
-    s = pkg.shapes.GQA_CORRECTNESS
-    print(f"[smoke] shape={s.name} B={s.batch} S={s.seq} n_q={s.n_q} n_kv={s.n_kv} d={s.d_head}")
-    g = H.load_golden("gqa_correctness_f16")
-    q, k, v = (H.from_bits(g[x], torch.float16).cuda() for x in "qkv")
+    if inputs_dir:
+        fx = H.reference_fixtures(inputs_dir, "gqa", fixture)
+        q, k, v = (torch.from_numpy(fx[x]).cuda() for x in "qkv")
+        expected = fx["expected"]
+        print(f"[smoke] fixture={fixture} B={q.shape[0]} S={q.shape[2]} n_q={q.shape[1]} n_kv={k.shape[1]} "
+              f"d={q.shape[3]}")
+    else:
+        s = pkg.shapes.GQA_CORRECTNESS
+        print(f"[smoke] shape={s.name} B={s.batch} S={s.seq} n_q={s.n_q} n_kv={s.n_kv} d={s.d_head}")
+        g = H.load_golden("gqa_correctness_f16")
+        q, k, v = (H.from_bits(g[x], torch.float16).cuda() for x in "qkv")
+        expected = g["o"]
     o = ops.gqa_fwd(q, k, v, causal=False)
     torch.cuda.synchronize()
     o32 = o.float().cpu().numpy()
-    expected = g["o"]
     tol = pkg.tolerances.get("f16")
     abs_err = np.abs(o32 - expected)
     max_abs = float(abs_err.max())
@@ -104,6 +114,9 @@ def main() -> int:
     ap.add_argument("--shape", choices=["llama3_8b", "baseline"], default="llama3_8b")
     ap.add_argument("--causal", action="store_true", default=None)
     ap.add_argument("--dtype", choices=["f16", "bf16"], default=None)
+    ap.add_argument("--inputs-dir", default=None,
+                    help="replay a fixture set written in the reference's inputs/ layout")
+    ap.add_argument("--fixture", default="correctness", help="fixture shape name (gqa_<fixture>_*.npy)")
     args = ap.parse_args()
     if not (args.smoke or args.bench or args.export_cubin):
         args.smoke = True
@@ -119,7 +132,7 @@ def main() -> int:
     print()
     rc = H.EXIT_OK
     if args.smoke:
-        if not run_smoke():
+        if not run_smoke(args.inputs_dir, args.fixture):
             rc = H.EXIT_SMOKE_FAIL
         print()
     if args.bench:

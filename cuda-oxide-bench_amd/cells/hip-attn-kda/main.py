@@ -2,7 +2,9 @@
 
 Drop-in for cutile-attn-kda/main.py (+ its bench.py --shape): flags --smoke
 (default), --bench, --csv-out, --shape {registry} (default
-kimi_linear_decode, as bench.py), --export-cubin / --cubin-out (accepted).
+kimi_linear_decode, as bench.py), --export-cubin / --cubin-out (accepted),
+--inputs-dir / --fixture (replay a kda_<fixture>_*.npy set written in the
+reference's inputs/ layout instead of the committed golden set).
 --smoke runs the reference's SHAPE_CORRECTNESS (B1 H2 d64, f16, the
 reference's seed-17 recipe) against the committed golden oracle output with
 the reference's gate (max_abs <= 1e-3 or rel <= 1e-3 on o and S,
@@ -26,17 +28,29 @@ WARMUP = 2
 ITERS = 50
 
 
-def run_smoke() -> bool:
+def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness") -> bool:
+    """The correctness check: the committed golden set, or with inputs_dir a
+    fixture set in the reference's inputs/ layout (kda_<fixture>_*.npy:
+    f16 q/k/v/g/beta, f32 S_in, f16 o and f32 S_out expected;
+    gen_kda_inputs.py:40-60)."""
     import numpy as np
     import torch
 
     pkg = H.package()
     ops = pkg.load_ops()
-    s = pkg.shapes.KDA_CORRECTNESS
-    print(f"[smoke] shape={s.name} B={s.batch} H={s.n_heads} d_k={s.d_k} d_v={s.d_v}")
-    g = H.load_golden("kda_correctness_f16")
-    x = [H.from_bits(g[n], torch.float16).cuda() for n in ("q", "k", "v", "g", "beta")]
-    o, so = ops.kda_decode(*x, torch.from_numpy(g["S_in"]).cuda())
+    if inputs_dir:
+        fx = H.reference_fixtures(inputs_dir, "kda", fixture)
+        x = [torch.from_numpy(fx[n]).cuda() for n in ("q", "k", "v", "g", "beta")]
+        s_in = torch.from_numpy(fx["S_in"]).cuda()
+        g = {"o": fx["o_expected"].astype(np.float32), "S_out": fx["S_out_expected"]}
+        print(f"[smoke] fixture={fixture} B={x[0].shape[0]} H={x[0].shape[1]} d_k={x[0].shape[2]} d_v={x[2].shape[2]}")
+    else:
+        s = pkg.shapes.KDA_CORRECTNESS
+        print(f"[smoke] shape={s.name} B={s.batch} H={s.n_heads} d_k={s.d_k} d_v={s.d_v}")
+        g = H.load_golden("kda_correctness_f16")
+        x = [H.from_bits(g[n], torch.float16).cuda() for n in ("q", "k", "v", "g", "beta")]
+        s_in = torch.from_numpy(g["S_in"]).cuda()
+    o, so = ops.kda_decode(*x, s_in)
     torch.cuda.synchronize()
     ok = True
     for name, got, want, bound in (("o", o.float().cpu().numpy(), g["o"], pkg.tolerances.NORMWISE_OUTPUT),
@@ -91,6 +105,9 @@ def main() -> int:
     ap.add_argument("--csv-out", default="results.csv")
     ap.add_argument("--cubin-out", default="kda_decode_fused.cubin")
     ap.add_argument("--shape", default="kimi_linear_decode", choices=sorted(reg.keys()))
+    ap.add_argument("--inputs-dir", default=None,
+                    help="replay a fixture set written in the reference's inputs/ layout")
+    ap.add_argument("--fixture", default="correctness", help="fixture shape name (kda_<fixture>_*.npy)")
     args = ap.parse_args()
     if not (args.smoke or args.bench or args.export_cubin):
         args.smoke = True
@@ -98,7 +115,7 @@ def main() -> int:
     print()
     rc = H.EXIT_OK
     if args.smoke:
-        if not run_smoke():
+        if not run_smoke(args.inputs_dir, args.fixture):
             rc = H.EXIT_SMOKE_FAIL
         print()
     if args.bench:

@@ -131,6 +131,14 @@ def load_golden(name: str) -> dict:
         return {k: z[k] for k in z.files}
 
 
+def reference_fixtures(inputs_dir: str, kind: str, name: str) -> dict:
+    """A fixture set written under the reference's inputs/ names (see npy.py)."""
+    npy = importlib.import_module(f"{PKG_DIR.name}.npy")
+    fx = npy.load_fixture_set(inputs_dir, kind, name)
+    print(f"[fixtures] {kind}_{name}_* from {inputs_dir}: " + ", ".join(f"{k}{tuple(v.shape)}" for k, v in fx.items()))
+    return fx
+
+
 def from_bits(arr, dtype):
     """uint16 bit patterns (as stored in the fixtures) -> torch bf16/f16 tensor."""
     import numpy as np
