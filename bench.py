@@ -7,8 +7,8 @@ inputs, scale 1/sqrt(128) — reported in algorithmic TFLOP/s (causal work
 inputs already resident in HBM.  The other kernels (bf16 GEMM at 1024^3
 and 8192^3, fp8 block-scaled GEMM at 8192^3, MLA absorbed decode, GDN
 decode, KDA decode at the reference's "large" shape, the fp8 activation
-quantiser at 8192x8192) are measured the same way and reported under
-"others".
+quantiser at 8192x8192, the pre-projected MLA prefill at the reference
+cell's bench shape) are measured the same way and reported under "others".
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        [--only-headline]
@@ -233,6 +233,19 @@ def bench_others(pkg, ops, steps, warmup) -> dict:
         "gbps_mean": F.gbps(nb, ms), "frac_hbm_peak_mean": F.gbps(nb, ms) / F.PEAK_HBM_GBPS,
     }
     log(f"quant_fp8_act: {res['quant_fp8_act']['gbps_mean']:.0f} GB/s mean")
+    del xa, qa, sa_
+
+    # pre-projected MLA prefill at the reference cell's bench shape (qk 192, v 128, native)
+    shape = S.MLA_PREFILL_BENCH
+    q, k, v = (t.cuda() for t in I.mla_prefill_inputs(shape, dtype=torch.bfloat16))
+    o = torch.empty((shape.batch, shape.n_h, shape.seq, shape.d_v), dtype=torch.bfloat16, device="cuda")
+    ms, _ = time_launches(lambda: ops.mla_prefill_fwd(q, k, v, out=o), steps, warmup)
+    fl = F.mla_attention_flops(shape)
+    res["mla_prefill"] = {
+        "unit": "TFLOPS", "shape": f"B{shape.batch} S{shape.seq} H{shape.n_h} qk{shape.qk_head_dim} v{shape.d_v} bf16",
+        "mean_ms": ms, "tflops_mean": F.tflops(fl, ms), "frac_mfma_peak_mean": F.tflops(fl, ms) / F.PEAK_BF16_TFLOPS,
+    }
+    log(f"mla_prefill: {res['mla_prefill']['tflops_mean']:.1f} TFLOPS mean")
     return res
 
 

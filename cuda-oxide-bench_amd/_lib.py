@@ -40,6 +40,7 @@ SIGNATURES: dict[str, tuple] = {
     "mx_gemm_fp8_bs": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mx_gqa_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _i, _vp]),
     "mx_mla_decode": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
+    "mx_mla_prefill_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _i, _vp]),
     "mx_mla_decode_workspace": (_sz, [_i, _i, _i, _i]),
     "mx_gdn_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "mx_kda_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),

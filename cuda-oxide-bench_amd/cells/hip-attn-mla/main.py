@@ -12,6 +12,18 @@ product (no padding) and `d_v` is 512.  --smoke checks the committed
 golden oracle output (H16, T40) with the bf16 normwise bound 2e-2;
 --bench times B32 H128 T4096 (DeepSeek-V3 shape) with 2 warm-up + 10
 timed launches.  GB/s counts the latent cache read once plus Q and O.
+
+--mode prefill runs the reference cell's own kernel instead: pre-projected
+multi-head attention over q/k of qk_head_dim and v of d_v
+(mx_mla_prefill_fwd, cutile-attn-mla/main.py:81-163) with qk_head_dim used
+natively, so qk_pad = qk_head_dim in the CSV.  --smoke checks the
+reference's SHAPE_CORRECTNESS_MLA (1,128,4, qk 96, v 64, f16) against the
+committed golden output with the reference's f16 allclose gate
+(:259-266), or with --inputs-dir / --fixture a mla_<fixture>_*.npy set in
+the reference's inputs/ layout; --bench times SHAPE_BENCH_MLA
+(deepseek_v3: B1 S2048 H128, qk 192, v 128) with 2 warm-up + 10 timed
+launches, TFLOPS by the reference's formula 2*B*H*S^2*(qk+d_v)
+(flops_mla.py:32-45); causal and dtype columns are appended.
 """
 from __future__ import annotations
 
@@ -80,6 +92,67 @@ def run_bench(csv_path: str, iters: int) -> None:
                                "tflops_median": F.tflops(fl, st["median_ms"]), "n_split": n_split})
 
 
+def run_prefill_smoke(inputs_dir: str | None, fixture: str) -> bool:
+    import numpy as np
+    import torch
+
+    pkg = H.package()
+    ops = pkg.load_ops()
+    if inputs_dir:
+        fx = H.reference_fixtures(inputs_dir, "mla", fixture)
+        q, k, v = (torch.from_numpy(fx[x]).cuda() for x in "qkv")
+        expected = fx["expected"]
+    else:
+        g = H.load_golden("mla_prefill_correctness_f16")
+        q, k, v = (H.from_bits(g[x], torch.float16).cuda() for x in "qkv")
+        expected = g["o"]
+    print(f"[smoke] prefill B={q.shape[0]} S={q.shape[2]} n_h={q.shape[1]} qk_head_dim={q.shape[3]} d_v={v.shape[3]}")
+    o = ops.mla_prefill_fwd(q, k, v)
+    torch.cuda.synchronize()
+    o32 = o.float().cpu().numpy()
+    tol = pkg.tolerances.get("f16")
+    err = np.abs(o32 - expected)
+    rel = float(err.max() / (np.abs(expected).max() + 1e-30))
+    ok = bool(np.allclose(o32, expected, atol=tol.atol, rtol=tol.rtol))
+    print(f"[smoke] max_abs={float(err.max()):.3e} rel={rel:.3e}  atol={tol.atol} rtol={tol.rtol}  "
+          f"{'OK' if ok else 'FAIL'}")
+    return ok
+
+
+def run_prefill_bench(csv_path: str, iters: int, causal: bool, dtype_name: str) -> None:
+    import dataclasses
+
+    import torch
+
+    pkg = H.package()
+    ops = pkg.load_ops()
+    F = pkg.flops
+    s = dataclasses.replace(pkg.shapes.MLA_PREFILL_BENCH, causal=causal)
+    dt = torch.bfloat16 if dtype_name == "bf16" else torch.float16
+    print(f"[bench] prefill shape={s.name} B={s.batch} S={s.seq} n_h={s.n_h} qk={s.qk_head_dim} d_v={s.d_v} "
+          f"causal={causal} dtype={dtype_name}")
+    q, k, v = (t.cuda() for t in pkg.inputs.mla_prefill_inputs(s, dtype=dt))
+    out = torch.empty((s.batch, s.n_h, s.seq, s.d_v), dtype=dt, device="cuda")
+    ms = H.time_iters(lambda: ops.mla_prefill_fwd(q, k, v, causal=causal, out=out), WARMUP, iters)
+    conv, alg = F.mla_attention_flops(s), F.mla_algorithmic_flops(s)
+    rows = []
+    for i, m in enumerate(ms):
+        print(f"[bench] iter={i} gpu_ms={m:.3f} tflops={F.tflops(conv, m):.3f}")
+        rows.append(["hip", "mla_fwd_fused", s.batch, s.seq, s.n_h, s.qk_head_dim, s.qk_head_dim, s.d_v, 32, 64, i,
+                     f"{m:.6f}", f"{F.tflops(conv, m):.6f}", int(causal), dtype_name, f"{F.tflops(alg, m):.6f}"])
+    H.write_csv(csv_path, ["impl", "kernel", "batch", "seq", "n_h", "qk_head_dim", "qk_pad", "d_v", "block_m",
+                           "block_n", "iter", "gpu_ms", "tflops", "causal", "dtype", "tflops_algorithmic"], rows)
+    st = H.summarize_ms(ms)
+    H.print_summary(f"{s.name} prefill (algorithmic FLOPs)", st, F.tflops(alg, st["best_ms"]),
+                    F.tflops(alg, st["median_ms"]), "TFLOPS", F.PEAK_BF16_TFLOPS)
+    H.write_sidecar(csv_path, {"kernel": "mla_fwd_fused", "shape": s.name, "causal": causal, "dtype": dtype_name,
+                               **st, "flops_algorithmic": alg, "flops_reference_convention": conv,
+                               "tflops_algorithmic_median": F.tflops(alg, st["median_ms"]),
+                               "peak_tflops": F.PEAK_BF16_TFLOPS,
+                               "frac_mfma_peak_median": F.tflops(alg, st["median_ms"]) / F.PEAK_BF16_TFLOPS,
+                               "bytes": F.mla_attention_bytes(s)})
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--smoke", action="store_true", default=False)
@@ -88,18 +161,31 @@ def main() -> int:
     ap.add_argument("--csv-out", default="results.csv")
     ap.add_argument("--cubin-out", default="mla_fwd_fused.cubin")
     ap.add_argument("--iters", type=int, default=None)
+    ap.add_argument("--mode", choices=["decode", "prefill"], default="decode",
+                    help="decode: absorbed latent-cache decode (the measured path); prefill: the reference "
+                         "cell's pre-projected attention with native qk_head_dim")
+    ap.add_argument("--causal", action="store_true", default=False, help="prefill: causal mask")
+    ap.add_argument("--dtype", choices=["f16", "bf16"], default="f16", help="prefill: I/O dtype")
+    ap.add_argument("--inputs-dir", default=None,
+                    help="prefill: replay a fixture set written in the reference's inputs/ layout")
+    ap.add_argument("--fixture", default="correctness_mla", help="prefill fixture shape name (mla_<fixture>_*.npy)")
     args = ap.parse_args()
     if not (args.smoke or args.bench or args.export_cubin):
         args.smoke = True
     H.banner()
     print()
     rc = H.EXIT_OK
+    iters = args.iters if args.iters is not None else ITERS
     if args.smoke:
-        if not run_smoke():
+        ok = run_prefill_smoke(args.inputs_dir, args.fixture) if args.mode == "prefill" else run_smoke()
+        if not ok:
             rc = H.EXIT_SMOKE_FAIL
         print()
     if args.bench:
-        run_bench(args.csv_out, args.iters if args.iters is not None else ITERS)
+        if args.mode == "prefill":
+            run_prefill_bench(args.csv_out, iters, args.causal, args.dtype)
+        else:
+            run_bench(args.csv_out, iters)
         print()
     if args.export_cubin:
         lib = importlib.import_module("cuda-oxide-bench_amd._lib")

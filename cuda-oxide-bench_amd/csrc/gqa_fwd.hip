@@ -56,28 +56,38 @@ constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 // clock (64 banks); a 16-byte read phase is 16 lanes, an 8-byte phase 32.
 //  * K fragment reads: 16 lanes read one chunk of 16 consecutive rows, so
 //    kswz spreads those rows over 16 distinct 16-byte slots (mod 256 B):
-//    r&15 for 256-byte rows, (r>>1)&7 for 128-byte rows (two per 256 B).
+//    r&15 for 256-byte rows; (r>>1)&7 for 128- and 384-byte rows (rows start
+//    at two bank phases, 0 and 128 B); (r>>2)&3 for 192-byte rows (four
+//    phases, 0/192/128/64 B).  The XOR only flips low chunk bits, so a chunk
+//    stays inside its row.
 //  * transposing V reads: 32 lanes read 4 consecutive rows x one aligned
 //    quad of chunks (64 B), so vswz gives each of the 4 rows its own quad:
 //    (r&3)<<2 for 256-byte rows, ((r>>1)&1)<<2 for 128-byte rows.  Rows 8
 //    and 16 apart share the swizzle, so fragment offsets stay immediates.
-template <int D>
+template <int ROW>
 __device__ __forceinline__ int kswz(int r) {
-  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+  if constexpr (ROW == 256) return r & 15;
+  else if constexpr (ROW == 192) return (r >> 2) & 3;
+  else return (r >> 1) & 7;
 }
-template <int D>
+template <int ROW>
 __device__ __forceinline__ int vswz(int r) {
-  return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
+  return ROW == 256 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
 }
 
-// One stage = K tile then V tile, [BN keys][D] each, unpadded swizzled rows.
-template <int D>
+// One stage = K tile [BN keys][DQK] then V tile [BN keys][DV], unpadded
+// swizzled rows.  Direct load n of a stage fills bytes 1024n .. 1024n+1023
+// of the stage (K tile first), whatever rows that spans.
+template <int DQK, int DV>
 struct Lds {
-  static constexpr int ROW = D * 2;
-  static constexpr int TILE = BN * ROW;
-  static constexpr int STAGE = 2 * TILE;
-  static constexpr int RPL = 1024 / ROW;           // rows per 1 KB direct load
+  static constexpr int ROWK = DQK * 2, ROWV = DV * 2;
+  static constexpr int TILEK = BN * ROWK, TILEV = BN * ROWV;
+  static constexpr int STAGE = TILEK + TILEV;
+  static constexpr int NLK = TILEK / 1024;           // direct loads per K tile
   static constexpr int LPW = STAGE / 1024 / NWAVES;  // direct loads per wave per stage
+  static_assert(TILEK % 1024 == 0 && TILEV % 1024 == 0 && STAGE % (1024 * NWAVES) == 0, "whole loads per wave");
+  static_assert((ROWK == 128 || ROWK == 192 || ROWK == 256 || ROWK == 384) && (ROWV == 128 || ROWV == 256),
+                "row sizes with a conflict-free swizzle");
 };
 
 template <int QT>
@@ -85,17 +95,17 @@ struct Ring {
   static constexpr int NS = QT == 1 ? 2 : 3;  // stages (QT=1 runs two workgroups per CU)
 };
 
-template <int D, typename T, bool CAUSAL, int QT>
+template <int DQK, int DV, typename T, bool CAUSAL, int QT>
 __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
                                                                      const uint16_t* __restrict__ K,
                                                                      const uint16_t* __restrict__ V,
                                                                      uint16_t* __restrict__ O, int B, int Hq,
                                                                      int Hkv, int S, float sl2, int hpw) {
   constexpr int QW = 32 * QT;         // queries per wave
-  constexpr int DC = D / 16;          // 16-deep k steps of QK^T
-  constexpr int DT = D / 32;          // 32-row d tiles of O^T
+  constexpr int DC = DQK / 16;        // 16-deep k steps of QK^T
+  constexpr int DT = DV / 32;         // 32-row d tiles of O^T
   constexpr int NS = Ring<QT>::NS;
-  using L = Lds<D>;
+  using L = Lds<DQK, DV>;
   extern __shared__ __align__(1024) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
@@ -123,8 +133,8 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   const int head = kvh * G + hg * hpw + (wave % hpw);
   const size_t q_head = ((size_t)b * Hq + head) * S;
   const size_t kv_head = ((size_t)b * Hkv + kvh) * S;
-  const unsigned char* Kh = reinterpret_cast<const unsigned char*>(K + kv_head * D);
-  const unsigned char* Vh = reinterpret_cast<const unsigned char*>(V + kv_head * D);
+  const unsigned char* Kh = reinterpret_cast<const unsigned char*>(K + kv_head * DQK);
+  const unsigned char* Vh = reinterpret_cast<const unsigned char*>(V + kv_head * DV);
 
   for (int rep = 0; rep < nrep; ++rep) {
   const int qb = CAUSAL ? (rep == 0 ? nqb - 1 - p : p) : p;
@@ -142,7 +152,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
     for (int dc = 0; dc < DC; ++dc) {
       // Fold the softmax scale (in log2 units) into Q once, so the score
       // MFMAs produce log2-domain scores directly.
-      const u32x4 x = ld128(Q + (q_head + min(qrow[qt], S - 1)) * D + dc * 16 + g * 8);
+      const u32x4 x = ld128(Q + (q_head + min(qrow[qt], S - 1)) * DQK + dc * 16 + g * 8);
       u32x4 y;
 #pragma unroll
       for (int w = 0; w < 4; ++w) y[w] = T::pack2(T::to_f32(x[w] & 0xffffu) * sl2, T::to_f32(x[w] >> 16) * sl2);
@@ -155,22 +165,29 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   const int nblk = (kv_end_wg + BN - 1) / BN;
   const int kv_end_w = CAUSAL ? min(S, q0w + QW) : S;
 
-  // ---- HBM -> LDS with direct loads: wave load n of a stage fills rows
-  // RPL*n .. RPL*n+RPL-1 of the K tile (n < BN/RPL) or of the V tile; lane i
-  // takes row RPL*n + i/(D/8), chunk (i%(D/8)) ^ k/vswz(row).  Rows past S
-  // re-read row S-1 (finite data that the mask or a zero P cancels). ----
+  // ---- HBM -> LDS with direct loads: wave load ld of a stage fills stage
+  // bytes 1024ld .. +1023 (the K tile, then the V tile); lane i takes byte
+  // 16i of it, i.e. row r = byte / ROW, chunk c = (byte % ROW) / 16, stored
+  // at chunk position c ^ k/vswz(r).  Rows past S re-read row S-1 (finite
+  // data that the mask or a zero P cancels). ----
   const uint32_t lds0 = lds_addr(smem);
-  const int l_row = lane / (D / 8);
-  const int l_pos = lane % (D / 8);
+  auto ld_row = [&](int ld) {
+    const bool vt = ld >= L::NLK;
+    return (1024 * (vt ? ld - L::NLK : ld) + 16 * lane) / (vt ? L::ROWV : L::ROWK);
+  };
+  auto ld_chunk = [&](int ld) {  // swizzled byte offset of this lane's chunk inside its row
+    const bool vt = ld >= L::NLK;
+    const int byte = 1024 * (vt ? ld - L::NLK : ld) + 16 * lane;
+    const int r = byte / (vt ? L::ROWV : L::ROWK), c = (byte % (vt ? L::ROWV : L::ROWK)) / 16;
+    return 16 * (c ^ (vt ? vswz<L::ROWV>(r) : kswz<L::ROWK>(r)));
+  };
   // Lane offsets of the wave's loads relative to the tile's first row, so a
   // full tile needs no VALU work: a scalar row base plus these.
   uint32_t ld_off[L::LPW];
 #pragma unroll
   for (int n = 0; n < L::LPW; ++n) {
-    const int ld = wave * L::LPW + n;                  // 0 .. 2*BN/RPL - 1
-    const int tile = ld / (BN / L::RPL);               // 0 = K, 1 = V
-    const int r = (ld % (BN / L::RPL)) * L::RPL + l_row;
-    ld_off[n] = (uint32_t)r * L::ROW + 16 * (l_pos ^ (tile ? vswz<D>(r) : kswz<D>(r)));
+    const int ld = wave * L::LPW + n;
+    ld_off[n] = (uint32_t)ld_row(ld) * (ld >= L::NLK ? L::ROWV : L::ROWK) + ld_chunk(ld);
   }
   auto issue = [&](int blk) {
     const int kv0 = blk * BN;
@@ -179,18 +196,16 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 #pragma unroll
       for (int n = 0; n < L::LPW; ++n) {
         const int ld = wave * L::LPW + n;
-        const int tile = ld / (BN / L::RPL);
-        dma16((tile ? Vh : Kh) + (size_t)kv0 * L::ROW, ld_off[n], st + ld * 1024);
+        const bool vt = ld >= L::NLK;
+        dma16((vt ? Vh + (size_t)kv0 * L::ROWV : Kh + (size_t)kv0 * L::ROWK), ld_off[n], st + ld * 1024);
       }
     } else {
 #pragma unroll
       for (int n = 0; n < L::LPW; ++n) {
         const int ld = wave * L::LPW + n;
-        const int tile = ld / (BN / L::RPL);
-        const int r = (ld % (BN / L::RPL)) * L::RPL + l_row;
-        const int kv = min(kv0 + r, S - 1);
-        const uint32_t off = (uint32_t)kv * L::ROW + 16 * (l_pos ^ (tile ? vswz<D>(r) : kswz<D>(r)));
-        dma16(tile ? Vh : Kh, off, st + ld * 1024);
+        const bool vt = ld >= L::NLK;
+        const int kv = min(kv0 + ld_row(ld), S - 1);
+        dma16(vt ? Vh : Kh, (uint32_t)kv * (vt ? L::ROWV : L::ROWK) + ld_chunk(ld), st + ld * 1024);
       }
     }
   };
@@ -205,7 +220,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   // position (2dc + g) ^ kswz(ql): one lane offset per dc, t an immediate.
   uint32_t koff[DC];  // absolute LDS addresses in stage 0
 #pragma unroll
-  for (int dc = 0; dc < DC; ++dc) koff[dc] = lds0 + ql * L::ROW + 16 * ((2 * dc + g) ^ kswz<D>(ql));
+  for (int dc = 0; dc < DC; ++dc) koff[dc] = lds0 + ql * L::ROWK + 16 * ((2 * dc + g) ^ kswz<L::ROWK>(ql));
   // Transposed V fragment: lane (half g, sub-group sg, 4j+a) reads key
   // 16c + 8r + 4g + j at column 32dt + 16sg + 4a, i.e. chunk 4dt + 2sg +
   // a/2 of a row whose swizzle is vswz(4g + j): one lane offset per dt.
@@ -215,7 +230,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   uint32_t v_off[DT];  // absolute LDS addresses in stage 0
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
-    v_off[dt] = lds0 + L::TILE + vrow * L::ROW + 16 * ((4 * dt + vw) ^ vswz<D>(vrow)) + 8 * (v_a & 1);
+    v_off[dt] = lds0 + L::TILEK + vrow * L::ROWV + 16 * ((4 * dt + vw) ^ vswz<L::ROWV>(vrow)) + 8 * (v_a & 1);
 
   // Softmax state per query (log2 units).  The score MFMAs start from
   // neg_m = -m_run instead of zero, so they return s - m_run directly.
@@ -256,13 +271,13 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       // 2*QT independent accumulator chains; each K fragment feeds QT
       // MFMAs and is read KLA k-steps ahead of its use.
       auto kread = [&](int t, int dc) {
-        return lds_ld128(koff[dc] + st + t * 32 * L::ROW);
+        return lds_ld128(koff[dc] + st + t * 32 * L::ROWK);
       };
       f32x16 s[QT][2];
       // Wave priority: the two waves sharing a SIMD issue their MFMA phases
       // ahead of the other's softmax VALU work, which then fills the gaps.
       __builtin_amdgcn_s_setprio(1);
-      constexpr int KLA = 2;  // read lookahead (k-steps)
+      constexpr int KLA = DQK > 128 ? 1 : 2;  // read lookahead (k-steps); 1 keeps the 192-wide Q in registers
       u32x4 kb[KLA + 1][2];
 #pragma unroll
       for (int i = 0; i < KLA; ++i) {
@@ -286,9 +301,9 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
       // V fragments of the first key chunk do not depend on the softmax:
       // issue them now so their latency hides under the VALU work below.
       auto vread = [&](int c, int dt) {
-        const uint32_t vb = v_off[dt] + st + (16 * c) * L::ROW;
+        const uint32_t vb = v_off[dt] + st + (16 * c) * L::ROWV;
         const u32x2 lo = lds_read_tr16_at(vb);
-        const u32x2 hi = lds_read_tr16_at(vb + 8 * L::ROW);
+        const u32x2 hi = lds_read_tr16_at(vb + 8 * L::ROWV);
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4 vb[2][DT];
@@ -412,7 +427,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
     const float l_tot = sum_xor32(l_run[qt]);
     const float inv = (l_tot > 0.f) ? 1.0f / l_tot : 0.f;
     if (qrow[qt] < S) {
-      uint16_t* orow = O + (q_head + qrow[qt]) * D;
+      uint16_t* orow = O + (q_head + qrow[qt]) * DV;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -427,7 +442,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
 }  // q-block loop
 }
 
-template <int D, typename T, bool CAUSAL, int QT>
+template <int DQK, int DV, typename T, bool CAUSAL, int QT>
 static int launch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
                   hipStream_t stream) {
   const int G = Hq / Hkv;
@@ -436,23 +451,44 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
   const int nqb = (S + QB - 1) / QB;
   const long long grid = (long long)(CAUSAL ? (nqb + 1) / 2 : nqb) * B * Hkv * (G / hpw);
   if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
-  auto kern = gqa_fwd_kernel<D, T, CAUSAL, QT>;
-  MX_RETURN_IF_HIP(
-      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Ring<QT>::NS * Lds<D>::STAGE));
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), Ring<QT>::NS * Lds<D>::STAGE, stream, (const uint16_t*)Q,
-                     (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, B, Hq, Hkv, S, scale * kLog2e, hpw);
+  auto kern = gqa_fwd_kernel<DQK, DV, T, CAUSAL, QT>;
+  constexpr int lds = Ring<QT>::NS * Lds<DQK, DV>::STAGE;
+  MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), lds, stream, (const uint16_t*)Q, (const uint16_t*)K,
+                     (const uint16_t*)V, (uint16_t*)O, B, Hq, Hkv, S, scale * kLog2e, hpw);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
 }
 
+template <int DQK, int DV, typename T, int QT>
+static int launch_c(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
+                    int causal, hipStream_t s) {
+  return causal ? launch<DQK, DV, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
+                : launch<DQK, DV, T, false, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+}
+
+// (qk head dim, v head dim) pairs with a kernel: the GQA head dims 64 and
+// 128, and the MLA prefill pairs 192/128 (DeepSeek-V3: 128 nope + 64 rope,
+// v 128) and 96/64 (the reference's correctness shape).
 template <typename T, int QT>
-static int dispatch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int D,
-                    float scale, int causal, hipStream_t s) {
-  if (D == 128) return causal ? launch<128, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
-                              : launch<128, T, false, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
-  if (D == 64) return causal ? launch<64, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
-                             : launch<64, T, false, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+static int dispatch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int dqk,
+                    int dv, float scale, int causal, hipStream_t s) {
+  if (dqk == 128 && dv == 128) return launch_c<128, 128, T, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
+  if (dqk == 64 && dv == 64) return launch_c<64, 64, T, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
+  if (dqk == 192 && dv == 128) return launch_c<192, 128, T, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
+  if (dqk == 96 && dv == 64) return launch_c<96, 64, T, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
   return MX_ERR_UNSUPPORTED;
+}
+
+static int check_args(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int dqk,
+                      float scale, int dtype) {
+  if (!Q || !K || !V || !O) return MX_ERR_NULL;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || Hq % Hkv) return MX_ERR_SHAPE;
+  if (!(scale > 0.f) || !__builtin_isfinite(scale)) return MX_ERR_SHAPE;
+  if ((long long)B * Hq * S * dqk > (1LL << 40)) return MX_ERR_SHAPE;
+  if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
+  if (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)O) & 15) return MX_ERR_ALIGN;
+  return MX_OK;
 }
 
 }  // namespace gqa
@@ -460,15 +496,23 @@ static int dispatch(const void* Q, const void* K, const void* V, void* O, int B,
 
 extern "C" int mx_gqa_fwd(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int D,
                           float scale, int causal, int dtype, void* stream) {
-  if (!Q || !K || !V || !O) return MX_ERR_NULL;
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || Hq % Hkv) return MX_ERR_SHAPE;
-  if (D != 64 && D != 128) return MX_ERR_SHAPE;
-  if (!(scale > 0.f) || !__builtin_isfinite(scale)) return MX_ERR_SHAPE;
-  if ((long long)B * Hq * S * D > (1LL << 40)) return MX_ERR_SHAPE;
-  if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
-  if (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)O) & 15) return MX_ERR_ALIGN;
+  if (D != 64 && D != 128) return (!Q || !K || !V || !O) ? MX_ERR_NULL : MX_ERR_SHAPE;
+  if (const int e = mx::gqa::check_args(Q, K, V, O, B, Hq, Hkv, S, D, scale, dtype)) return e;
   hipStream_t s = (hipStream_t)stream;
   constexpr int QT = MX_GQA_QT;
-  if (dtype == MX_DTYPE_BF16) return mx::gqa::dispatch<mx::BF16, QT>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, s);
-  return mx::gqa::dispatch<mx::F16, QT>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, s);
+  if (dtype == MX_DTYPE_BF16) return mx::gqa::dispatch<mx::BF16, QT>(Q, K, V, O, B, Hq, Hkv, S, D, D, scale, causal, s);
+  return mx::gqa::dispatch<mx::F16, QT>(Q, K, V, O, B, Hq, Hkv, S, D, D, scale, causal, s);
+}
+
+extern "C" int mx_mla_prefill_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H, int S, int d_qk,
+                                  int d_v, float scale, int causal, int dtype, void* stream) {
+  if (const int e = mx::gqa::check_args(Q, K, V, O, B, H, H, S, d_qk, scale, dtype)) return e;
+  if (!((d_qk == 192 && d_v == 128) || (d_qk == 96 && d_v == 64) || (d_qk == 128 && d_v == 128) ||
+        (d_qk == 64 && d_v == 64)))
+    return MX_ERR_UNSUPPORTED;
+  hipStream_t s = (hipStream_t)stream;
+  constexpr int QT = MX_GQA_QT;
+  if (dtype == MX_DTYPE_BF16)
+    return mx::gqa::dispatch<mx::BF16, QT>(Q, K, V, O, B, H, H, S, d_qk, d_v, scale, causal, s);
+  return mx::gqa::dispatch<mx::F16, QT>(Q, K, V, O, B, H, H, S, d_qk, d_v, scale, causal, s);
 }

@@ -10,7 +10,7 @@ contractions only.
 """
 from __future__ import annotations
 
-from .shapes import FP8GemmShape, GDNShape, GemmShape, GQAShape, MLADecodeShape
+from .shapes import FP8GemmShape, GDNShape, GemmShape, GQAShape, MLADecodeShape, MLAShape
 
 # MI355X published peaks (dense).
 PEAK_BF16_TFLOPS = 2500.0
@@ -50,6 +50,23 @@ def gqa_algorithmic_flops(s: GQAShape) -> int:
 def gqa_attention_bytes(s: GQAShape, dtype_bytes: int = 2) -> int:
     """Q, K, V read once, O written once (flops.py:54-66)."""
     return (2 * s.q_size + 2 * s.kv_size) * dtype_bytes
+
+
+def mla_attention_flops(s: MLAShape) -> int:
+    """2*B*n_h*S^2*(qk_head_dim + d_v) (flops_mla.py:32-45): full S x S,
+    the reference's convention also for a causal run."""
+    return 2 * s.batch * s.n_h * s.seq * s.seq * (s.qk_head_dim + s.d_v)
+
+
+def mla_algorithmic_flops(s: MLAShape) -> int:
+    """Work the kernel must do: full S x S, or S(S+1)/2 pairs when causal."""
+    pairs = s.seq * (s.seq + 1) // 2 if s.causal else s.seq * s.seq
+    return 2 * s.batch * s.n_h * pairs * (s.qk_head_dim + s.d_v)
+
+
+def mla_attention_bytes(s: MLAShape, dtype_bytes: int = 2) -> int:
+    """Q, K, V read once and O written once (flops_mla.py:52-64)."""
+    return (2 * s.q_size + 2 * s.v_size) * dtype_bytes
 
 
 def mla_decode_flops(s: MLADecodeShape) -> int:

@@ -19,7 +19,7 @@ import numpy as np
 import torch
 
 from .quant import quantize_fp8_blockwise
-from .shapes import FP8GemmShape, GDNShape, GemmShape, GQAShape, KDAShape, MLADecodeShape
+from .shapes import FP8GemmShape, GDNShape, GemmShape, GQAShape, KDAShape, MLADecodeShape, MLAShape
 
 SEED = 0xC0FFEE
 SAMPLE_SEED = 0xBEEF
@@ -69,6 +69,20 @@ def gqa_inputs(s: GQAShape, dtype: torch.dtype = torch.bfloat16, seed: int = SEE
         q = torch.randn(qs, generator=g, dtype=torch.float32)
         k = torch.randn(ks, generator=g, dtype=torch.float32)
         v = torch.randn(ks, generator=g, dtype=torch.float32)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def mla_prefill_inputs(s: MLAShape, dtype: torch.dtype = torch.float16, seed: int = SEED):
+    """q, k [B,n_h,S,qk_head_dim], v [B,n_h,S,d_v]: the draws of
+    make_qkv_mla (pytorch_reference_mla.py:84-108) -- one CPU generator,
+    q then k then v, q and k scaled by 1/sqrt(qk_head_dim), in fp32 -- cast
+    to `dtype`."""
+    g = _gen(seed)
+    qk = s.qk_head_dim
+    sc = 1.0 / math.sqrt(qk)
+    q = torch.randn((s.batch, s.n_h, s.seq, qk), generator=g, dtype=torch.float32) * sc
+    k = torch.randn((s.batch, s.n_h, s.seq, qk), generator=g, dtype=torch.float32) * sc
+    v = torch.randn((s.batch, s.n_h, s.seq, s.d_v), generator=g, dtype=torch.float32)
     return q.to(dtype), k.to(dtype), v.to(dtype)
 
 

@@ -129,6 +129,36 @@ def mla_decode_workspace_bytes(B: int, H: int, T: int, d_latent: int = 512) -> i
     return int(_lib.load().mx_mla_decode_workspace(B, H, T, d_latent))
 
 
+def mla_prefill_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
+                    scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Pre-projected MLA prefill attention, every head its own K/V.
+
+    Semantics of cutile-attn-mla/main.py:81-163 (scale defaults to
+    1/sqrt(qk_head_dim)) without its zero padding of qk_head_dim to a power
+    of two: q, k [B,H,S,d_qk], v [B,H,S,d_v] -> out [B,H,S,d_v], bf16 or
+    f16.  (d_qk, d_v) in {(192,128), (96,64), (128,128), (64,64)}.
+    """
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _require(t, n, _IO_DTYPES, 4)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    B, H, S, Dqk = q.shape
+    if tuple(k.shape) != (B, H, S, Dqk) or tuple(v.shape[:3]) != (B, H, S):
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    Dv = v.shape[3]
+    if scale is None:
+        scale = 1.0 / math.sqrt(Dqk)
+    if out is None:
+        out = torch.empty((B, H, S, Dv), dtype=q.dtype, device=q.device)
+    _require(out, "out", (q.dtype,), 4)
+    if tuple(out.shape) != (B, H, S, Dv):
+        raise ValueError(f"out must be {(B, H, S, Dv)}")
+    _same_device(q, k, v, out)
+    _lib.call("mx_mla_prefill_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, S, Dqk, Dv,
+              float(scale), int(bool(causal)), _IO_DTYPES[q.dtype], _stream())
+    return out
+
+
 def mla_decode(q: torch.Tensor, kv: torch.Tensor, scale: float, d_latent: int = 512,
                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Absorbed MLA decode.  q [B,H,576], kv [B,T,576] bf16 -> out [B,H,512].

@@ -49,6 +49,45 @@ class GQAShape:
 
 
 @dataclass(frozen=True)
+class MLAShape:
+    """Pre-projected MLA prefill (reference shapes_mla.py:26-67): every head
+    has its own up-projected Q and K of qk_head_dim = d_h + d_rope and V of
+    d_v; d_c (the latent rank) is carried but unused, as in the reference.
+    `causal` is this path's addition (the reference cell is non-causal)."""
+
+    name: str
+    batch: int
+    seq: int
+    n_h: int
+    d_h: int
+    d_rope: int
+    d_v: int
+    d_c: int
+    causal: bool = False
+
+    @property
+    def qk_head_dim(self) -> int:
+        return self.d_h + self.d_rope
+
+    @property
+    def scale(self) -> float:
+        return self.qk_head_dim ** -0.5
+
+    @property
+    def q_size(self) -> int:
+        return self.batch * self.seq * self.n_h * self.qk_head_dim
+
+    @property
+    def v_size(self) -> int:
+        return self.batch * self.seq * self.n_h * self.d_v
+
+    def assert_valid(self) -> None:
+        assert self.d_h > 0 and self.d_rope > 0 and self.d_v > 0
+        assert self.n_h > 0 and self.seq > 0 and self.batch > 0
+        assert self.d_c > 0
+
+
+@dataclass(frozen=True)
 class MLADecodeShape:
     """Weight-absorbed MLA decode: one query token per sequence, latent cache.
 
@@ -160,6 +199,11 @@ GQA_REGISTRY = {s.name: s for s in (GQA_CORRECTNESS, GQA_LLAMA3_8B, GQA_CORRECTN
 MLA_CORRECTNESS = MLADecodeShape("correctness_mla_decode", batch=2, n_h=16, ctx=200)
 MLA_BASELINE = MLADecodeShape("deepseek_v3_decode", batch=32, n_h=128, ctx=4096)
 MLA_REGISTRY = {s.name: s for s in (MLA_CORRECTNESS, MLA_BASELINE)}
+
+# MLA prefill (pre-projected Q/K/V; shapes_mla.py:70-93).
+MLA_PREFILL_CORRECTNESS = MLAShape("correctness_mla", batch=1, seq=128, n_h=4, d_h=64, d_rope=32, d_v=64, d_c=128)
+MLA_PREFILL_BENCH = MLAShape("deepseek_v3", batch=1, seq=2048, n_h=128, d_h=128, d_rope=64, d_v=128, d_c=512)
+MLA_PREFILL_REGISTRY = {s.name: s for s in (MLA_PREFILL_CORRECTNESS, MLA_PREFILL_BENCH)}
 
 # GDN: reference registry (cutile-attn-gdn/main.py:62-72, shapes_gdn.py:85-104)
 # and the Qwen3-Next-like batch-64 configuration this path is measured on.

@@ -121,6 +121,21 @@ int mx_gqa_fwd(const void* Q, const void* K, const void* V, void* O, int B, int 
                int D, float scale, int causal, int dtype, void* stream);
 
 /*
+ * Pre-projected MLA prefill attention (multi-head, every head its own K/V):
+ *   O[b,h,s,:] = softmax_t( scale * Q[b,h,s,:]·K[b,h,t,:] + mask ) · V[b,h,t,:]
+ * Q, K: [B, H, S, d_qk]; V, O: [B, H, S, d_v]; contiguous bf16 or f16;
+ * mask = -inf for t > s when causal != 0.  (d_qk, d_v) must be (192, 128)
+ * (DeepSeek-V3: 128 nope + 64 rope, v 128), (96, 64), (128, 128) or
+ * (64, 64); the qk head dim is used as is, not padded.  Same kernel family
+ * as mx_gqa_fwd (one KV head per query head).
+ * Replaces: cutile-attn-mla/main.py:250-253 (ct.launch of `mla_fwd`,
+ * kernel at :81-163, which zero-pads qk_head_dim 192 to 256 on the host,
+ * :179-206); causal and bf16 are the extensions this path specifies.
+ */
+int mx_mla_prefill_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H, int S, int d_qk,
+                       int d_v, float scale, int causal, int dtype, void* stream);
+
+/*
  * MLA absorbed decode (one query token per sequence, latent KV cache):
  *   O[b,h,:] = softmax_t( scale * Q[b,h,:]·KV[b,t,:] ) · KV[b,t,0:d_latent]
  * Q[B,H,d_latent+d_rope], KV[B,T,d_latent+d_rope], O[B,H,d_latent], all

@@ -1,4 +1,4 @@
-"""MLA absorbed-decode oracle (test infrastructure only).
+"""MLA oracles, pre-projected prefill and absorbed decode (test infrastructure only).
 
 The reference's MLA oracle (analysis/wave15-attention-architecture/reference/
 pytorch_reference_mla.py:66-81, mla_naive) is softmax attention with an
@@ -11,6 +11,27 @@ mla_naive with n_kv = 1, computed in fp32 per sequence.
 from __future__ import annotations
 
 import torch
+
+
+def mla_prefill_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
+                    heads: list[int] | None = None) -> torch.Tensor:
+    """Pre-projected MLA prefill: mla_naive of pytorch_reference_mla.py:66-81
+    (softmax(q k^T / sqrt(qk_head_dim)) v per head, fp32), plus this path's
+    causal mask.  q, k [B,H,S,d_qk], v [B,H,S,d_v] -> fp32 [B,H,S,d_v]."""
+    q = q.detach().cpu().float()
+    k = k.detach().cpu().float()
+    v = v.detach().cpu().float()
+    B, H, S, Dqk = q.shape
+    scale = 1.0 / (Dqk ** 0.5)
+    out = torch.zeros((B, H, S, v.shape[-1]), dtype=torch.float32)
+    mask = torch.ones((S, S), dtype=torch.bool).triu(1) if causal else None
+    for b in range(B):
+        for h in (heads if heads is not None else range(H)):
+            scores = (q[b, h] @ k[b, h].transpose(0, 1)) * scale
+            if mask is not None:
+                scores = scores.masked_fill(mask, float("-inf"))
+            out[b, h] = torch.softmax(scores, dim=-1) @ v[b, h]
+    return out
 
 
 def mla_decode_ref(q: torch.Tensor, kv: torch.Tensor, scale: float, d_latent: int = 512,

@@ -76,6 +76,12 @@ def main() -> int:
     save("mla_decode_h16_t40", q=bits16(q), kv=bits16(kv),
          o=omla.mla_decode_ref(q, kv, ms.scale).numpy(), scale=np.array([ms.scale], dtype=np.float64))
 
+    # MLA prefill: the reference's correctness shape and recipe (f16, qk 96, v 64).
+    mp = S.MLA_PREFILL_CORRECTNESS
+    q, k, v = inputs.mla_prefill_inputs(mp, dtype=torch.float16)
+    save("mla_prefill_correctness_f16", q=bits16(q), k=bits16(k), v=bits16(v),
+         o=omla.mla_prefill_ref(q, k, v).numpy())
+
     # GDN: reference correctness shape/distribution (f16) and a grouped bf16 case.
     d1 = S.GDN_CORRECTNESS
     x = inputs.gdn_inputs(d1, dtype=torch.float16, dist="reference")

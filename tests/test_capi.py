@@ -25,7 +25,7 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("mx_gemm_bf16", "mx_gemm_fp8_bs", "mx_gqa_fwd", "mx_mla_decode", "mx_mla_decode_workspace",
               "mx_gdn_decode", "mx_kda_decode", "mx_quant_fp8_act", "mx_gemm_bf16_batched", "mx_mla_decode_absorbed",
-              "mx_mla_decode_absorbed_workspace", "mx_strerror",
+              "mx_mla_decode_absorbed_workspace", "mx_mla_prefill_fwd", "mx_strerror",
               "mx_version"):
         assert n in names
 
@@ -77,6 +77,16 @@ def test_gqa_validation():
     assert f(P, P, P, P, 1, 4, 2, 16, 96, 0.125, 1, 0, None) == _lib.MX_ERR_SHAPE   # D
     assert f(P, P, P, P, 1, 4, 2, 16, 64, 0.125, 1, 7, None) == _lib.MX_ERR_DTYPE
     assert f(P, P, P, P, 1, 4, 2, 16, 64, -1.0, 1, 0, None) == _lib.MX_ERR_SHAPE
+
+
+def test_mla_prefill_validation():
+    f = _lib.load().mx_mla_prefill_fwd
+    assert f(None, P, P, P, 1, 4, 16, 192, 128, 0.07, 0, 0, None) == _lib.MX_ERR_NULL
+    assert f(P, P, P, P, 1, 4, 0, 192, 128, 0.07, 0, 0, None) == _lib.MX_ERR_SHAPE
+    assert f(P, P, P, P, 1, 4, 16, 160, 128, 0.07, 0, 0, None) == _lib.MX_ERR_UNSUPPORTED
+    assert f(P, P, P, P, 1, 4, 16, 192, 64, 0.07, 0, 0, None) == _lib.MX_ERR_UNSUPPORTED
+    assert f(P, P, P, P, 1, 4, 16, 192, 128, 0.07, 0, 5, None) == _lib.MX_ERR_DTYPE
+    assert f(P, P, P, P, 1, 4, 16, 192, 128, 0.0, 0, 0, None) == _lib.MX_ERR_SHAPE
 
 
 def test_mla_validation_and_workspace():

@@ -153,7 +153,7 @@ def test_cells_offer_fixture_replay():
     import subprocess
     import sys
 
-    for cell in ("hip-attn-gqa", "hip-attn-gdn", "hip-attn-kda"):
+    for cell in ("hip-attn-gqa", "hip-attn-gdn", "hip-attn-kda", "hip-attn-mla"):
         main = REPO_ROOT / "cuda-oxide-bench_amd" / "cells" / cell / "main.py"
         out = subprocess.run([sys.executable, str(main), "--help"], capture_output=True, text=True, timeout=120)
         assert out.returncode == 0 and "--inputs-dir" in out.stdout and "--fixture" in out.stdout

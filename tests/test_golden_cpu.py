@@ -37,6 +37,13 @@ def test_gqa_fixtures():
         assert np.allclose(ogqa.gqa_naive(q, k, v, causal=causal).numpy(), g["o"], atol=1e-6)
 
 
+def test_mla_prefill_fixture():
+    g = load_golden("mla_prefill_correctness_f16")
+    q, k, v = inputs.mla_prefill_inputs(shapes.MLA_PREFILL_CORRECTNESS, dtype=torch.float16)
+    assert torch.equal(from_bits(g["q"], torch.float16), q) and torch.equal(from_bits(g["v"], torch.float16), v)
+    assert np.allclose(omla.mla_prefill_ref(q, k, v).numpy(), g["o"], atol=1e-6)
+
+
 def test_mla_fixture():
     g = load_golden("mla_decode_h16_t40")
     q, kv = from_bits(g["q"], torch.bfloat16), from_bits(g["kv"], torch.bfloat16)

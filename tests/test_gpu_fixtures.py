@@ -59,6 +59,14 @@ def test_kda_replay(ops, tmp_path):
     assert cell("hip-attn-kda").run_smoke(str(tmp_path), "correctness")
 
 
+def test_mla_prefill_replay(ops, tmp_path):
+    announce("fixture replay mla_correctness_mla")
+    g = load_golden("mla_prefill_correctness_f16")
+    npy.save_fixture_set(tmp_path, "mla", "correctness_mla",
+                         {"q": f16(g["q"]), "k": f16(g["k"]), "v": f16(g["v"]), "expected": g["o"]})
+    assert cell("hip-attn-mla").run_prefill_smoke(str(tmp_path), "correctness_mla")
+
+
 def test_missing_set_fails_loudly(ops, tmp_path):
     with pytest.raises(npy.NpyError):
         cell("hip-attn-gqa").run_smoke(str(tmp_path), "absent")

@@ -63,3 +63,48 @@ def test_absorption_identity():
     # and the rounded oracle stays within bf16 distance of it
     r = omla.mla_absorbed_ref(x["q_nope"], x["q_rope"], kv, x["w_uk"], x["w_uv"], s.scale).double()
     assert (r - full).abs().max() / full.abs().max() < 2e-2
+
+
+# ---- pre-projected prefill (mla_naive of pytorch_reference_mla.py:66-81) ----
+
+def test_prefill_matches_sdpa_with_explicit_scale():
+    """The reference cross-checks mla_naive against SDPA with scale
+    1/sqrt(qk_head_dim) to < 1e-4 (pytorch_reference_mla.py:150-157)."""
+    s = shapes.MLA_PREFILL_CORRECTNESS
+    q, k, v = inputs.mla_prefill_inputs(s, dtype=torch.float32)
+    o = omla.mla_prefill_ref(q, k, v)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=s.scale)
+    assert (o - ref).abs().max() < 1e-5
+    oc = omla.mla_prefill_ref(q, k, v, causal=True)
+    refc = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, scale=s.scale)
+    assert (oc - refc).abs().max() < 1e-5
+
+
+def test_prefill_equals_the_references_zero_padded_form():
+    """The reference's kernel pads qk_head_dim 192 to 256 with zero columns
+    and keeps the scale at 1/sqrt(192) (cutile-attn-mla/main.py:89-106,
+    179-206): the unpadded result must be the same attention."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn((1, 2, 33, 192), generator=g) / 192 ** 0.5
+    k = torch.randn((1, 2, 33, 192), generator=g) / 192 ** 0.5
+    v = torch.randn((1, 2, 33, 128), generator=g)
+    pad = lambda t: torch.nn.functional.pad(t, (0, 64))  # noqa: E731
+    padded = ogqa.gqa_naive(pad(q), pad(k), v, causal=False, scale=192 ** -0.5)
+    assert torch.allclose(omla.mla_prefill_ref(q, k, v), padded, atol=1e-6)
+
+
+def test_prefill_special_cases():
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn((2, 3, 20, 96), generator=g)
+    k = torch.randn((2, 3, 20, 96), generator=g)
+    v = torch.randn((2, 3, 20, 64), generator=g)
+    oc = omla.mla_prefill_ref(q, k, v, causal=True)
+    assert torch.allclose(oc[:, :, 0], v[:, :, 0])                     # causal row 0 sees only key 0
+    assert torch.allclose(omla.mla_prefill_ref(q, k, torch.ones_like(v)), torch.ones_like(v))
+    # fp64 brute force, one (b, h, s) at a time
+    b, h, i = 1, 2, 7
+    sc = [sum(float(q[b, h, i, d]) * float(k[b, h, t, d]) for d in range(96)) / 96 ** 0.5 for t in range(20)]
+    mx = max(sc)
+    w = [pow(2.718281828459045, x - mx) for x in sc]
+    ref = [sum(w[t] * float(v[b, h, t, c]) for t in range(20)) / sum(w) for c in range(64)]
+    assert torch.allclose(omla.mla_prefill_ref(q, k, v)[b, h, i], torch.tensor(ref, dtype=torch.float32), atol=1e-5)
