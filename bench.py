@@ -346,7 +346,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / F.PEAK_BF16_TFLOPS, 5),
             "traffic": traffic,
-            "kernel": "gqa_fwd_kernel<128, BF16, causal>",
+            "kernel": "gqa_fwd_kernel<128, 128, BF16, causal, 1>",
             "launch_mean_ms": round(g["mean_ms"], 5),
         },
         "cpu_baseline": g.get("cpu"),
