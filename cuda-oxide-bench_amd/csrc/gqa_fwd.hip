@@ -18,10 +18,11 @@
 //    V is never transposed in registers.
 //  * A wave owns QT tiles of 32 queries of one head; every K and V fragment
 //    read from LDS feeds QT MFMAs, which is what bounds LDS traffic per FLOP.
-//  * One workgroup = 4 waves = (up to 4 query heads sharing a KV head) x
-//    (query sub-blocks).  K and V tiles of 64 keys are staged once in LDS
-//    (double buffered, next tile's global loads in flight during the
-//    current tile's MFMAs, one barrier per tile) and shared by the 4 waves.
+//  * One workgroup = 8 waves (two per SIMD, one workgroup per CU) or 4
+//    waves (two workgroups per CU) = (up to 4 query heads sharing a KV
+//    head) x (query sub-blocks).  K and V tiles of 64 keys are staged once
+//    in LDS (double buffered, next tile's global loads in flight during the
+//    current tile's MFMAs, one barrier per tile) and shared by all waves.
 //  * Softmax: the running max only moves when a lane's block max exceeds it
 //    by more than 2^8 (lazy rescale, wave-uniform vote), the scale is folded
 //    into the exp2 argument (one FMA + one exp2 per score), and the row sum
@@ -46,8 +47,6 @@ namespace mx {
 namespace gqa {
 
 constexpr int BN = 64;      // key/value positions per tile
-constexpr int NWAVES = 4;
-constexpr int NT = 64 * NWAVES;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 
@@ -78,7 +77,7 @@ __device__ __forceinline__ int vswz(int r) {
 // One stage = K tile [BN keys][DQK] then V tile [BN keys][DV], unpadded
 // swizzled rows.  Direct load n of a stage fills bytes 1024n .. 1024n+1023
 // of the stage (K tile first), whatever rows that spans.
-template <int DQK, int DV>
+template <int DQK, int DV, int NWAVES>
 struct Lds {
   static constexpr int ROWK = DQK * 2, ROWV = DV * 2;
   static constexpr int TILEK = BN * ROWK, TILEV = BN * ROWV;
@@ -90,13 +89,21 @@ struct Lds {
                 "row sizes with a conflict-free swizzle");
 };
 
+// Waves per workgroup: 8 (two per SIMD, one workgroup per CU) when a stage
+// splits into whole 1 KB loads for 8 waves, else 4 (two workgroups per CU).
+// With 8, twice the queries share every K/V tile staged in LDS.
+template <int DQK, int DV>
+constexpr int waves_for() {
+  return ((DQK + DV) * 2 * BN / 1024) % 8 == 0 ? 8 : 4;
+}
+
 template <int QT>
 struct Ring {
-  static constexpr int NS = QT == 1 ? 2 : 3;  // stages (QT=1 runs two workgroups per CU)
+  static constexpr int NS = QT == 1 ? 2 : 3;  // stages (QT=1 keeps two waves per SIMD)
 };
 
-template <int DQK, int DV, typename T, bool CAUSAL, int QT>
-__global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
+template <int DQK, int DV, typename T, bool CAUSAL, int QT, int NWAVES>
+__global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
                                                                      const uint16_t* __restrict__ K,
                                                                      const uint16_t* __restrict__ V,
                                                                      uint16_t* __restrict__ O, int B, int Hq,
@@ -105,7 +112,7 @@ __global__ __launch_bounds__(NT, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint
   constexpr int DC = DQK / 16;        // 16-deep k steps of QK^T
   constexpr int DT = DV / 32;         // 32-row d tiles of O^T
   constexpr int NS = Ring<QT>::NS;
-  using L = Lds<DQK, DV>;
+  using L = Lds<DQK, DV, NWAVES>;
   extern __shared__ __align__(1024) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
@@ -447,14 +454,15 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
                   hipStream_t stream) {
   const int G = Hq / Hkv;
   const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
+  constexpr int NWAVES = waves_for<DQK, DV>();
   const int QB = 32 * QT * (NWAVES / hpw);
   const int nqb = (S + QB - 1) / QB;
   const long long grid = (long long)(CAUSAL ? (nqb + 1) / 2 : nqb) * B * Hkv * (G / hpw);
   if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
-  auto kern = gqa_fwd_kernel<DQK, DV, T, CAUSAL, QT>;
-  constexpr int lds = Ring<QT>::NS * Lds<DQK, DV>::STAGE;
+  auto kern = gqa_fwd_kernel<DQK, DV, T, CAUSAL, QT, NWAVES>;
+  constexpr int lds = Ring<QT>::NS * Lds<DQK, DV, NWAVES>::STAGE;
   MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NT), lds, stream, (const uint16_t*)Q, (const uint16_t*)K,
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NWAVES), lds, stream, (const uint16_t*)Q, (const uint16_t*)K,
                      (const uint16_t*)V, (uint16_t*)O, B, Hq, Hkv, S, scale * kLog2e, hpw);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
