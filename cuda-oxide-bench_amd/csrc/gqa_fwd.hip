@@ -196,6 +196,15 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
     const int ld = wave * L::LPW + n;
     ld_off[n] = (uint32_t)ld_row(ld) * (ld >= L::NLK ? L::ROWV : L::ROWK) + ld_chunk(ld);
   }
+  // load n of tile blk, rows past S-1 clamped to S-1 (no branch: it can sit
+  // between the MFMAs of a k step)
+  auto issue_part = [&](int blk, int n) {
+    const int ld = wave * L::LPW + n;
+    const bool vt = ld >= L::NLK;
+    const int kv = min(blk * BN + ld_row(ld), S - 1);
+    dma16(vt ? Vh : Kh, (uint32_t)kv * (vt ? L::ROWV : L::ROWK) + ld_chunk(ld),
+          lds0 + (blk % NS) * L::STAGE + ld * 1024);
+  };
   auto issue = [&](int blk) {
     const int kv0 = blk * BN;
     const uint32_t st = lds0 + (blk % NS) * L::STAGE;
@@ -268,8 +277,13 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
       wait_vmcnt<0>();
     }
     __syncthreads();
-    if (blk + NS - 1 < nblk) issue(blk + NS - 1);
+    // the next tile's loads go out one per k step of the S^T MFMAs below
+    // rather than all at once, which queues every wave's loads behind the
+    // barrier
+    const bool load_next = blk + NS - 1 < nblk;
     const int kv0 = blk * BN;
+    // a wave that skips this tile still issues its share of the next one
+    if (kv0 >= kv_end_w && load_next) issue(blk + NS - 1);
 
     if (kv0 < kv_end_w) {
       constexpr uint32_t st = STG * L::STAGE;
@@ -302,6 +316,9 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt)
             s[qt][t] = mfma32<T>(kb[dc % (KLA + 1)][t], qf[qt][dc], dc == 0 ? neg_m[qt] : s[qt][t]);
+#pragma unroll
+        for (int n = 0; n < L::LPW; ++n)
+          if (dc == n * DC / L::LPW && load_next) issue_part(blk + NS - 1, n);
         __builtin_amdgcn_sched_barrier(0);  // keep the read lookahead
       }
 
