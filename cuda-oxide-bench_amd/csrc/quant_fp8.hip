@@ -13,9 +13,20 @@
 //    128-bit store of 16 e4m3 bytes); 8 lanes cover a block, a wave 8
 //    blocks, so every wave streams 2 KB of input in one pass;
 //  * the block amax is a 3-step xor butterfly over the 8 lanes;
-//  * X / s is a correctly rounded fp32 division, so the codes are
-//    bit-identical to the host recipe; the packed converts
-//    (v_cvt_pk_fp8_f32, round to nearest even) do the e4m3 encoding.
+//  * X / s is the correctly rounded fp32 quotient, so the codes are
+//    bit-identical to the host recipe.  A full IEEE division costs ~10 VALU
+//    instructions; all 16 values of a lane share s, so the lane takes one
+//    correctly rounded reciprocal r = RN(1/s) and refines per value:
+//    q0 = RN(x r) (up to ~1.5 ulp off: r's half ulp plus the product's),
+//    q1 = RN(q0 + (x - q0 s) r) (within one ulp), q2 = RN(q1 + (x - q1 s) r).
+//    By Markstein's theorem (r correctly rounded, q1 within one ulp of x/s,
+//    no underflow or overflow; the residual x - q1 s is then exact in one
+//    FMA) q2 = RN(x/s); its sign is taken from x so that -0 stays -0.
+//    Blocks with s outside [2^-90, 2^100] (tiny or
+//    infinite amax) take the plain division, so every residual that can
+//    reach a nonzero e4m3 code is a normal fp32 number;
+//  * the packed converts (v_cvt_pk_fp8_f32, round to nearest even) do the
+//    e4m3 encoding.
 #include "mx_common.h"
 
 namespace mx {
@@ -56,12 +67,30 @@ __global__ __launch_bounds__(NT) void quant_fp8_act_kernel(const uint16_t* __res
   for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 8));
   const float s = amax > 0.f ? amax / kE4M3Max : 1.0f;
 
+  // x / s correctly rounded: the reciprocal refinement when every lane's
+  // block allows it (the common case), else the plain division
+  float q[16];
+  if (__all(s >= 0x1p-90f && s <= 0x1p100f)) {
+    const float r = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float q0 = v[i] * r;
+      const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, s, v[i]), r, q0);
+      // x = -0 would come out +0 (the residual is +0), where -0 / s is -0;
+      // every other quotient already carries x's sign
+      q[i] = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q1, s, v[i]), r, q1), v[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = v[i] / s;
+  }
+
   u32x4 out;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     float y[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(v[4 * w + j] / s, -kE4M3Max), kE4M3Max);
+    for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(q[4 * w + j], -kE4M3Max), kE4M3Max);
     int p = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
     p = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], p, true);
     out[w] = (uint32_t)p;

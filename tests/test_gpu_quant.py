@@ -66,6 +66,40 @@ def test_edge_cases(ops):
         assert ofp8.e4m3_decode(q[1:2, 5])[0] == -448.0
 
 
+def test_bit_exact_wide_range_and_near_midpoints(ops):
+    """The kernel forms x/s as a reciprocal refinement (r = RN(1/s), q =
+    RN(x r), q' = RN(q + (x - q s) r)) and keeps the plain division for
+    blocks whose scale is below 2^-90 or above 2^100.  Both must give the
+    host recipe's codes: rows over a wide exponent range (some on the
+    plain-division side), and blocks whose values are bf16(t * s) for every
+    e4m3 midpoint t, i.e. quotients within rounding distance of a code
+    boundary under non-trivial scales, plus signed zeros."""
+    announce("quant_fp8 wide range + near-midpoint blocks")
+    g = torch.Generator().manual_seed(20261202)
+    m, k = 1024, 4096
+    x = torch.randn((m, k), generator=g) * torch.exp(torch.randn((m, 1), generator=g) * 6)
+    x[::97] *= 1e-33                                   # scales < 2^-90: plain division
+    pos = ofp8.e4m3_decode(np.arange(0, 0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = ((pos[1:] + pos[:-1]) / 2).astype(np.float32)  # 126 midpoints
+    rng = np.random.default_rng(7)
+    amax = torch.from_numpy(np.exp(rng.uniform(-40, 40, size=512)).astype(np.float32)).to(torch.bfloat16).float()
+    blk = torch.zeros((512, 128))
+    for i in range(512):
+        sc = np.float32(amax[i].item()) / np.float32(448.0)
+        vals = torch.from_numpy(mids * sc).to(torch.bfloat16).float()
+        sign = torch.from_numpy(rng.choice([-1.0, 1.0], size=126).astype(np.float32))
+        blk[i, :126] = vals * sign
+        blk[i, 126] = -0.0 if i % 2 else 0.0            # signed zeros keep their sign: -0 -> code 0x80
+        blk[i, 127] = amax[i]
+    x[m - 512:, :128] = blk                             # 512 rows, first block each
+    xb = x.to(torch.bfloat16)
+    q, s = quant(ops, xb)
+    qe, se = expect(xb)
+    assert np.array_equal(s, se)
+    bad = np.argwhere(q != qe)
+    assert bad.size == 0, f"{len(bad)} code mismatches, first at {bad[:5].tolist()}"
+
+
 def test_feeds_fp8_gemm(ops):
     """Device-quantised activations into the block-scaled fp8 GEMM equal the
     oracle GEMM of the same dequantised operands."""
