@@ -450,6 +450,7 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 // parallelism.
 constexpr int CMB_WG = 256;
 constexpr int CMB_PER = VT * 4 * 32 / CMB_WG;  // workgroups per (b, 32-head group) = 8
+constexpr int CMB_MAXS = 64;                    // splits whose (m, l) are staged in LDS (16 KB)
 
 __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __restrict__ ws_o,
                                                             const float* __restrict__ ws_ml,
@@ -463,10 +464,20 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
   const int lane0 = 2 * lp;                     // lanes lane0, lane0 + 1
   const int l32 = lane0 & 31, hsel = lane0 >> 5;
   const size_t g0 = (size_t)b * nsplit * HW + hw;  // tile of split 0; split stride HW
-  const float* ml = ws_ml + g0 * 64 + 2 * l32;     // (m, l) of heads l32, l32 + 1
+  // The (m, l) pairs of the tile's 32 heads for every split (256 B per
+  // split) are read once per workgroup into LDS, not once per thread.
+  __shared__ f32x4 ml_lds[CMB_MAXS * 16];
+  const int nst = min(nsplit, CMB_MAXS);
+  for (int i = threadIdx.x; i < nst * 16; i += CMB_WG)
+    ml_lds[i] = *reinterpret_cast<const f32x4*>(ws_ml + (g0 + (size_t)(i >> 4) * HW) * 64 + 4 * (i & 15));
+  __syncthreads();
+  auto mlv_of = [&](int s) {  // (m, l) of heads l32, l32 + 1 in split s
+    return s < CMB_MAXS ? ml_lds[s * 16 + (l32 >> 1)]
+                        : *reinterpret_cast<const f32x4*>(ws_ml + (g0 + (size_t)s * HW) * 64 + 2 * l32);
+  };
   float2 mmax{-1e30f, -1e30f};
   for (int s = 0; s < nsplit; ++s) {
-    const f32x4 x = *reinterpret_cast<const f32x4*>(ml + (size_t)s * HW * 64);
+    const f32x4 x = mlv_of(s);
     mmax.x = fmaxf(mmax.x, x[0]);
     mmax.y = fmaxf(mmax.y, x[2]);
   }
@@ -492,13 +503,12 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       p[u] = ld128(po + (size_t)(s + u) * sstride);
-      mlv[u] = *reinterpret_cast<const f32x4*>(ml + (size_t)(s + u) * HW * 64);
+      mlv[u] = mlv_of(s + u);
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc1(p[u], mlv[u]);
   }
-  for (; s < nsplit; ++s)
-    acc1(ld128(po + (size_t)s * sstride), *reinterpret_cast<const f32x4*>(ml + (size_t)s * HW * 64));
+  for (; s < nsplit; ++s) acc1(ld128(po + (size_t)s * sstride), mlv_of(s));
   const int vt = slot >> 2, i = slot & 3;
   const int head0 = hw * HPW + l32;
   const float inv0 = l0 > 0.f ? 1.f / l0 : 0.f, inv1 = l1 > 0.f ? 1.f / l1 : 0.f;
