@@ -73,18 +73,25 @@ struct Cfg {
 
 // gridDim.y indexes a batch of independent products whose operands sit
 // sA / sB / sC elements apart (0 and gridDim.y = 1 for a single GEMM).
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(
+// KS > 1 splits K inside the workgroup: KS groups of WM x WN waves, each
+// with its own double buffer, take consecutive runs of K tiles of the same
+// C tile, and their fp32 accumulators are summed through LDS at the end.
+// For grids of about one tile per CU, where the serial K loop's load latency
+// (not the MFMAs) sets the time, it runs KS loads in flight per CU.
+template <int BM, int BN, int WM, int WN, int KS = 1>
+__global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C, int M,
     int N, int K, int lda, int ldb, int ldc, long long sA, long long sB, long long sC) {
   using CF = Cfg<BM, BN, WM, WN>;
   constexpr int NT = CF::NT, FM = CF::FM, FN = CF::FN;
-  extern __shared__ __align__(16) unsigned char smem[];
+  extern __shared__ __align__(16) unsigned char smem_all[];
   A += (size_t)blockIdx.y * sA;
   B += (size_t)blockIdx.y * sB;
   C += (size_t)blockIdx.y * sC;
 
-  const int tid = threadIdx.x;
+  const int grp = KS > 1 ? (int)threadIdx.x / NT : 0;  // K group
+  unsigned char* const smem = smem_all + grp * 2 * CF::LDS_STAGE;
+  const int tid = (int)threadIdx.x % NT;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -165,14 +172,23 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(
   const int b_sg = (lane >> 4) & 1, b_j = (lane >> 2) & 3, b_a = lane & 3;
   const int b_off = (8 * g + b_j) * CF::B_ROW + (wn * CF::TN + 16 * b_sg + 4 * b_a) * 2;
 
-  const int nk = (K + BK - 1) / BK;
-  load_tile(0);
-  store_tile(0);
+  // this group's K tiles: [kt0, kt0 + cnt); every group runs nkg loop trips
+  // so the barriers match
+  const int nk_all = (K + BK - 1) / BK;
+  const int nkg = (nk_all + KS - 1) / KS;
+  const int kt0 = grp * nkg;
+  const int nk = max(0, min(nkg, nk_all - kt0));
+  if (nk > 0) {
+    load_tile(kt0 * BK);
+    store_tile(0);
+  }
   __syncthreads();
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load_tile((kt + 1) * BK);
+  for (int it = 0; it < nkg; ++it) {
+    const int kt = kt0 + it;
+    const int cur = it & 1;
+    if (it < nk) {
+    if (it + 1 < nk) load_tile((kt + 1) * BK);
     const unsigned char* sa = smem + cur * CF::LDS_STAGE;
     const unsigned char* sb = sa + CF::LDS_A;
 #pragma unroll
@@ -192,8 +208,36 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_kernel(
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<BF16>(bfr[j], af[i], acc[i][j]);
     }
-    if (kt + 1 < nk) store_tile(cur ^ 1);
+    if (it + 1 < nk) store_tile(cur ^ 1);
+    }
     __syncthreads();
+  }
+
+  if constexpr (KS > 1) {
+    // Sum the groups' accumulators into group 0's (the loop's last barrier
+    // freed every stage).  Element e of thread t of group g >= 1 sits at
+    // float ((g-1)·E + e)·NT + t: consecutive threads, consecutive banks.
+    constexpr int E = FM * FN * 16;
+    static_assert((KS - 1) * E * NT * 4 <= KS * 2 * CF::LDS_STAGE, "the partial sums fit in the stages");
+    float* red = reinterpret_cast<float*>(smem_all);
+    if (grp > 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) red[((grp - 1) * E + (i * FN + j) * 16 + e) * NT + tid] = acc[i][j][e];
+    }
+    __syncthreads();
+    if (grp > 0) return;  // no barrier follows
+#pragma unroll
+    for (int q = 1; q < KS; ++q)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((q - 1) * E + (i * FN + j) * 16 + e) * NT + tid];
   }
 
   // ---- epilogue: lane holds C[m][n .. n+3], m = row of lane, n = 8r + 4g ----
@@ -467,16 +511,17 @@ static int launch_dma(const void* A, const void* B, void* C, int M, int N, int K
   return MX_OK;
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int KS = 1>
 static int launch(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
                   hipStream_t stream, int batch = 1, long long sA = 0, long long sB = 0, long long sC = 0) {
   using CF = Cfg<BM, BN, WM, WN>;
   const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7fffffffLL || batch > 65535) return MX_ERR_SHAPE;
-  const size_t smem = 2 * CF::LDS_STAGE;
-  auto kern = gemm_bf16_kernel<BM, BN, WM, WN>;
+  const size_t smem = (size_t)KS * 2 * CF::LDS_STAGE;
+  static_assert(KS * 2 * CF::LDS_STAGE <= 160 * 1024, "double buffers fit in the LDS");
+  auto kern = gemm_bf16_kernel<BM, BN, WM, WN, KS>;
   MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)batch), dim3(CF::NT), smem, stream, (const uint16_t*)A,
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)batch), dim3(CF::NT * KS), smem, stream, (const uint16_t*)A,
                      (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
@@ -667,6 +712,10 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   // 256 CUs twice, else smaller tiles for parallelism.
   if (tiles256 >= 512) return mx::gemm::launch<256, 256, 2, 4>(A, B, C, M, N, K, lda, ldb, ldc, s);
   if (tiles128 >= 256) return mx::gemm::launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
+  // About one 64x64 tile per CU or fewer and a long K (e.g. 1024^3): split
+  // K between two wave groups of each workgroup.
+  const long long tiles64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles64 <= 256 && K >= 512) return mx::gemm::launch<64, 64, 2, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
   return mx::gemm::launch<64, 64, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
 }
 
