@@ -78,7 +78,9 @@ struct Cfg {
 // C tile, and their fp32 accumulators are summed through LDS at the end.
 // For grids of about one tile per CU, where the serial K loop's load latency
 // (not the MFMAs) sets the time, it runs KS loads in flight per CU.
-template <int BM, int BN, int WM, int WN, int KS = 1>
+// PF = 2 stages the global loads two K tiles ahead in two register sets
+// (the LDS double buffer is unchanged), for the same latency-bound case.
+template <int BM, int BN, int WM, int WN, int KS = 1, int PF = 1>
 __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C, int M,
     int N, int K, int lda, int ldb, int ldc, long long sA, long long sB, long long sC) {
@@ -112,21 +114,23 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
 
   // ---- global -> register staging.  A: chunk q -> row q/8, chunk q%8.
   //      B: chunk q -> k row q/(BN/8), column chunk q%(BN/8). ----
-  u32x4 ra[CF::A_CHUNKS], rb[CF::B_CHUNKS];
+  static_assert(PF == 1 || PF == 2, "one or two register sets");
+  u32x4 ra[PF][CF::A_CHUNKS], rb[PF][CF::B_CHUNKS];
   constexpr int BCH = BN / 8;
 
-  auto load_tile = [&](int k0) {
+  auto load_tile = [&](int k0, auto set_tag) {
+    constexpr int SET = decltype(set_tag)::value;
     const bool full = interior && (k0 + BK <= K);  // uniform
 #pragma unroll
     for (int i = 0; i < CF::A_CHUNKS; ++i) {
       const int q = tid + i * NT;
       const int gm = m0 + (q >> 3), gk = k0 + (q & 7) * 8;
       if (full) {
-        ra[i] = ld128(A + (size_t)gm * lda + gk);
+        ra[SET][i] = ld128(A + (size_t)gm * lda + gk);
       } else {
         const bool ok = gm < M && gk < K;
         const u32x4 x = ld128(A + (size_t)min(gm, M - 1) * lda + min(gk, K - 8));
-        ra[i] = ok ? x : u32x4{0, 0, 0, 0};
+        ra[SET][i] = ok ? x : u32x4{0, 0, 0, 0};
       }
     }
 #pragma unroll
@@ -134,27 +138,28 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
       const int q = tid + i * NT;
       const int gk = k0 + q / BCH, gn = n0 + (q % BCH) * 8;
       if (full) {
-        rb[i] = ld128(B + (size_t)gk * ldb + gn);
+        rb[SET][i] = ld128(B + (size_t)gk * ldb + gn);
       } else {
         const bool ok = gk < K && gn < N;
         const u32x4 x = ld128(B + (size_t)min(gk, K - 1) * ldb + min(gn, N - 8));
-        rb[i] = ok ? x : u32x4{0, 0, 0, 0};
+        rb[SET][i] = ok ? x : u32x4{0, 0, 0, 0};
       }
     }
   };
 
-  auto store_tile = [&](int stage) {
+  auto store_tile = [&](int stage, auto set_tag) {
+    constexpr int SET = decltype(set_tag)::value;
     unsigned char* sa = smem + stage * CF::LDS_STAGE;
     unsigned char* sb = sa + CF::LDS_A;
 #pragma unroll
     for (int i = 0; i < CF::A_CHUNKS; ++i) {
       const int q = tid + i * NT;
-      *reinterpret_cast<u32x4*>(sa + (q >> 3) * CF::A_ROW + (q & 7) * 16) = ra[i];
+      *reinterpret_cast<u32x4*>(sa + (q >> 3) * CF::A_ROW + (q & 7) * 16) = ra[SET][i];
     }
 #pragma unroll
     for (int i = 0; i < CF::B_CHUNKS; ++i) {
       const int q = tid + i * NT;
-      *reinterpret_cast<u32x4*>(sb + (q / BCH) * CF::B_ROW + (q % BCH) * 16) = rb[i];
+      *reinterpret_cast<u32x4*>(sb + (q / BCH) * CF::B_ROW + (q % BCH) * 16) = rb[SET][i];
     }
   };
 
@@ -178,18 +183,11 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
   const int nkg = (nk_all + KS - 1) / KS;
   const int kt0 = grp * nkg;
   const int nk = max(0, min(nkg, nk_all - kt0));
-  if (nk > 0) {
-    load_tile(kt0 * BK);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int it = 0; it < nkg; ++it) {
-    const int kt = kt0 + it;
-    const int cur = it & 1;
-    if (it < nk) {
-    if (it + 1 < nk) load_tile((kt + 1) * BK);
-    const unsigned char* sa = smem + cur * CF::LDS_STAGE;
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, PF - 1>;
+  // MFMAs of the K tile in LDS stage `stage`
+  auto compute = [&](int stage) {
+    const unsigned char* sa = smem + stage * CF::LDS_STAGE;
     const unsigned char* sb = sa + CF::LDS_A;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
@@ -208,9 +206,44 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<BF16>(bfr[j], af[i], acc[i][j]);
     }
-    if (it + 1 < nk) store_tile(cur ^ 1);
+  };
+
+  if (nk > 0) {
+    load_tile(kt0 * BK, S0{});
+    store_tile(0, S0{});
+  }
+  if constexpr (PF == 2) {
+    if (nk > 1) load_tile((kt0 + 1) * BK, S1{});
+  }
+  __syncthreads();
+
+  if constexpr (PF == 2) {
+    // Iteration it: register set it&1 (its tile already in LDS) takes tile
+    // it+2; stage it&1 holds tile it; set (it+1)&1, loaded one iteration
+    // earlier, goes to stage (it+1)&1, freed by the previous barrier.
+    auto step = [&](int it, auto par) {
+      constexpr int P = decltype(par)::value;
+      if (it < nk) {
+        if (it + 2 < nk) load_tile((kt0 + it + 2) * BK, std::integral_constant<int, P>{});
+        compute(P);
+        if (it + 1 < nk) store_tile(P ^ 1, std::integral_constant<int, P ^ 1>{});
+      }
+      __syncthreads();
+    };
+    for (int it = 0; it < nkg; it += 2) {
+      step(it, S0{});
+      if (it + 1 < nkg) step(it + 1, S1{});
     }
-    __syncthreads();
+  } else {
+    for (int it = 0; it < nkg; ++it) {
+      const int cur = it & 1;
+      if (it < nk) {
+        if (it + 1 < nk) load_tile((kt0 + it + 1) * BK, S0{});
+        compute(cur);
+        if (it + 1 < nk) store_tile(cur ^ 1, S0{});
+      }
+      __syncthreads();
+    }
   }
 
   if constexpr (KS > 1) {
@@ -511,7 +544,7 @@ static int launch_dma(const void* A, const void* B, void* C, int M, int N, int K
   return MX_OK;
 }
 
-template <int BM, int BN, int WM, int WN, int KS = 1>
+template <int BM, int BN, int WM, int WN, int KS = 1, int PF = 1>
 static int launch(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
                   hipStream_t stream, int batch = 1, long long sA = 0, long long sB = 0, long long sC = 0) {
   using CF = Cfg<BM, BN, WM, WN>;
@@ -519,7 +552,7 @@ static int launch(const void* A, const void* B, void* C, int M, int N, int K, in
   if (tiles > 0x7fffffffLL || batch > 65535) return MX_ERR_SHAPE;
   const size_t smem = (size_t)KS * 2 * CF::LDS_STAGE;
   static_assert(KS * 2 * CF::LDS_STAGE <= 160 * 1024, "double buffers fit in the LDS");
-  auto kern = gemm_bf16_kernel<BM, BN, WM, WN, KS>;
+  auto kern = gemm_bf16_kernel<BM, BN, WM, WN, KS, PF>;
   MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)batch), dim3(CF::NT * KS), smem, stream, (const uint16_t*)A,
                      (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
@@ -715,8 +748,8 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   // About one 64x64 tile per CU or fewer and a long K (e.g. 1024^3): split
   // K between two wave groups of each workgroup.
   const long long tiles64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
-  if (tiles64 <= 256 && K >= 512) return mx::gemm::launch<64, 64, 2, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
-  return mx::gemm::launch<64, 64, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
+  if (tiles64 <= 256 && K >= 512) return mx::gemm::launch<64, 64, 2, 2, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
+  return mx::gemm::launch<64, 64, 2, 2, 1, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
 }
 
 extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda,
@@ -738,5 +771,5 @@ extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int b
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * batch;
   if (M >= 128 && t128 >= 256)
     return mx::gemm::launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
-  return mx::gemm::launch<64, 64, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
+  return mx::gemm::launch<64, 64, 2, 2, 1, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
 }
