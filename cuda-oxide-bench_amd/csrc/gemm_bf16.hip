@@ -536,8 +536,8 @@ static int launch_dma(const void* A, const void* B, void* C, int M, int N, int K
   const long long tiles = (long long)((M + CF::BM - 1) / CF::BM) * ((N + CF::BN - 1) / CF::BN);
   if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
   const int smem = NS * CF::STAGE;
-  auto kern = gemm_bf16_dma_kernel<BK, NS, WM, WN>;
-  MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem));
+  constexpr auto kern = gemm_bf16_dma_kernel<BK, NS, WM, WN>;
+  MX_RETURN_IF_HIP(lds_limit_once<kern>(smem));
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CF::NT), smem, stream, (const uint16_t*)A,
                      (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
   MX_RETURN_IF_HIP(hipGetLastError());
@@ -552,8 +552,8 @@ static int launch(const void* A, const void* B, void* C, int M, int N, int K, in
   if (tiles > 0x7fffffffLL || batch > 65535) return MX_ERR_SHAPE;
   const size_t smem = (size_t)KS * 2 * CF::LDS_STAGE;
   static_assert(KS * 2 * CF::LDS_STAGE <= 160 * 1024, "double buffers fit in the LDS");
-  auto kern = gemm_bf16_kernel<BM, BN, WM, WN, KS, PF>;
-  MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+  constexpr auto kern = gemm_bf16_kernel<BM, BN, WM, WN, KS, PF>;
+  MX_RETURN_IF_HIP(lds_limit_once<kern>((int)smem));
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)batch), dim3(CF::NT * KS), smem, stream, (const uint16_t*)A,
                      (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
   MX_RETURN_IF_HIP(hipGetLastError());
@@ -752,9 +752,28 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   return mx::gemm::launch<64, 64, 2, 2, 1, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
 }
 
-extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda,
-                                    int ldb, int ldc, long long strideA, long long strideB, long long strideC,
-                                    void* stream) {
+namespace mx {
+namespace gemm {
+
+// Which kernel mx_gemm_bf16_batched runs for these sizes.
+enum class BatchedPath { SmallM, T128, T64 };
+
+static BatchedPath batched_path(int batch, int M, int N, int K, int lda, int ldb) {
+  // Decode-sized items (M <= 32, whole 64-deep K chunks): the
+  // weight-streaming small-M kernel.  Its lane offsets are 32-bit.
+  if (M <= 32 && K % 64 == 0 && (long long)lda * 2 * 32 <= 0xffffffffLL && (long long)ldb * 2 * 64 <= 0xffffffffLL)
+    return BatchedPath::SmallM;
+  // Otherwise the register-staged kernel with tiles sized to the item.
+  const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * batch;
+  if (M >= 128 && t128 >= 256) return BatchedPath::T128;
+  return BatchedPath::T64;
+}
+
+// Every check mx_gemm_bf16_batched makes before it launches, the grid
+// limits of the kernel it would pick included, so a caller that chains
+// several products can validate them all before enqueuing any.
+int batched_check(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda, int ldb, int ldc,
+                  long long strideA, long long strideB, long long strideC) {
   if (!A || !B || !C) return MX_ERR_NULL;
   if (batch <= 0 || M <= 0 || N <= 0 || K <= 0) return MX_ERR_SHAPE;
   if (batch > 65535 || strideA < 0 || strideB < 0 || strideC < 0) return MX_ERR_SHAPE;
@@ -762,14 +781,30 @@ extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int b
   if ((K % 8) || (N % 8) || (lda % 8) || (ldb % 8) || (ldc % 8)) return MX_ERR_ALIGN;
   if ((strideA % 8) || (strideB % 8) || (strideC % 8)) return MX_ERR_ALIGN;
   if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15) return MX_ERR_ALIGN;
+  long long grid = 0;
+  switch (batched_path(batch, M, N, K, lda, ldb)) {
+    case BatchedPath::SmallM: grid = (long long)batch * ((N + 31) / 32); break;  // widest grid of the three widths
+    case BatchedPath::T128: grid = (long long)((M + 127) / 128) * ((N + 127) / 128); break;
+    case BatchedPath::T64: grid = (long long)((M + 63) / 64) * ((N + 63) / 64); break;
+  }
+  return grid > 0x7fffffffLL ? MX_ERR_SHAPE : MX_OK;
+}
+
+}  // namespace gemm
+}  // namespace mx
+
+extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda,
+                                    int ldb, int ldc, long long strideA, long long strideB, long long strideC,
+                                    void* stream) {
+  using namespace mx::gemm;
+  if (const int e = batched_check(A, B, C, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC)) return e;
   hipStream_t s = (hipStream_t)stream;
-  // Decode-sized items (M <= 32, whole 64-deep K chunks): the
-  // weight-streaming small-M kernel.  Its lane offsets are 32-bit.
-  if (M <= 32 && K % 64 == 0 && (long long)lda * 2 * 32 <= 0xffffffffLL && (long long)ldb * 2 * 64 <= 0xffffffffLL)
-    return mx::gemm::launch_smallm(A, B, C, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, s);
-  // Otherwise the register-staged kernel with tiles sized to the item.
-  const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * batch;
-  if (M >= 128 && t128 >= 256)
-    return mx::gemm::launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
-  return mx::gemm::launch<64, 64, 2, 2, 1, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
+  switch (batched_path(batch, M, N, K, lda, ldb)) {
+    case BatchedPath::SmallM:
+      return launch_smallm(A, B, C, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, s);
+    case BatchedPath::T128:
+      return launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
+    default:
+      return launch<64, 64, 2, 2, 1, 2>(A, B, C, M, N, K, lda, ldb, ldc, s, batch, strideA, strideB, strideC);
+  }
 }

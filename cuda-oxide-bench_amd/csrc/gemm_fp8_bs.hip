@@ -281,8 +281,8 @@ static int launch(const void* A, const float* sA, const void* B, const float* sB
   const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
   const size_t smem = 2 * CF::STAGE;
-  auto kern = gemm_fp8_bs_kernel<BM, BN>;
-  MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+  constexpr auto kern = gemm_fp8_bs_kernel<BM, BN>;
+  MX_RETURN_IF_HIP(lds_limit_once<kern>((int)smem));
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NT), smem, stream, (const uint8_t*)A, sA, (const uint8_t*)B,
                      sB, (uint16_t*)C, M, N, K);
   MX_RETURN_IF_HIP(hipGetLastError());

@@ -476,9 +476,9 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
   const int nqb = (S + QB - 1) / QB;
   const long long grid = (long long)(CAUSAL ? (nqb + 1) / 2 : nqb) * B * Hkv * (G / hpw);
   if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
-  auto kern = gqa_fwd_kernel<DQK, DV, T, CAUSAL, QT, NWAVES>;
+  constexpr auto kern = gqa_fwd_kernel<DQK, DV, T, CAUSAL, QT, NWAVES>;
   constexpr int lds = Ring<QT>::NS * Lds<DQK, DV, NWAVES>::STAGE;
-  MX_RETURN_IF_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+  MX_RETURN_IF_HIP(lds_limit_once<kern>(lds));
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NWAVES), lds, stream, (const uint16_t*)Q, (const uint16_t*)K,
                      (const uint16_t*)V, (uint16_t*)O, B, Hq, Hkv, S, scale * kLog2e, hpw);
   MX_RETURN_IF_HIP(hipGetLastError());

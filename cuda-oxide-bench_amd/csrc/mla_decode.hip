@@ -526,18 +526,27 @@ inline size_t workspace_bytes(int B, int H, int T) {
   return (size_t)B * sp.nsplit * HW * (PT_U32 * sizeof(uint32_t) + 2 * HPW * sizeof(float));
 }
 
-// The decode (+ combine) launches of one call; arguments already checked.
+// Grid limits of the decode and combine launches.
+static int check_grid(int B, int H, int T) {
+  const Split sp = pick_split(B, H, T);
+  const long long HGB = (H + HPG - 1) / HPG;
+  const long long HW = (H + HPW - 1) / HPW;
+  const long long grid = (long long)B * HGB * sp.nsplit;
+  if (grid > 0x7fffffffLL || (long long)B * HW * CMB_PER > 0x7fffffffLL) return MX_ERR_SHAPE;
+  return MX_OK;
+}
+
+// The decode (+ combine) launches of one call; arguments (check_decode,
+// check_grid) already checked.
 static int launch_decode(const void* Q, const void* Qr, int q_ld, int qr_ld, const void* KV, void* O, int B, int H,
                          int T, float scale, void* workspace, hipStream_t s) {
   const Split sp = pick_split(B, H, T);
   const long long HGB = (H + HPG - 1) / HPG;
   const long long HW = (H + HPW - 1) / HPW;
   const long long grid = (long long)B * HGB * sp.nsplit;
-  if (grid > 0x7fffffffLL || (long long)B * HW * CMB_PER > 0x7fffffffLL) return MX_ERR_SHAPE;
   uint32_t* ws_o = (uint32_t*)workspace;
   float* ws_ml = sp.nsplit > 1 ? reinterpret_cast<float*>(ws_o + (size_t)B * sp.nsplit * HW * PT_U32) : nullptr;
-  MX_RETURN_IF_HIP(
-      hipFuncSetAttribute((const void*)mla_decode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
+  MX_RETURN_IF_HIP(lds_limit_once<mla_decode_kernel>(LDS_BYTES));
   hipLaunchKernelGGL(mla_decode_kernel, dim3((unsigned)grid), dim3(NT), LDS_BYTES, s, (const uint16_t*)Q,
                      (const uint16_t*)Qr, (const uint16_t*)KV, (uint16_t*)O, ws_o, ws_ml, B, H, T, scale * kLog2e,
                      sp.nsplit, sp.tps, q_ld, qr_ld);
@@ -555,7 +564,7 @@ static int check_decode(const void* KV, int B, int H, int T, float scale) {
   if (!(scale > 0.f) || !__builtin_isfinite(scale)) return MX_ERR_SHAPE;
   if ((long long)B * T * DQK > (1LL << 40) || (long long)B * H > (1LL << 30)) return MX_ERR_SHAPE;
   if ((uintptr_t)KV & 15) return MX_ERR_ALIGN;
-  return MX_OK;
+  return check_grid(B, H, T);
 }
 
 // Workspace of the absorbed step: q_lat [B,H,512] and o_lat [B,H,512] bf16,
@@ -571,6 +580,12 @@ inline size_t absorbed_workspace_bytes(int B, int H, int T) {
 extern "C" int mx_gemm_bf16_batched(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda,
                                     int ldb, int ldc, long long strideA, long long strideB, long long strideC,
                                     void* stream);
+namespace mx {
+namespace gemm {
+int batched_check(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda, int ldb, int ldc,
+                  long long strideA, long long strideB, long long strideC);
+}  // namespace gemm
+}  // namespace mx
 
 extern "C" size_t mx_mla_decode_workspace(int B, int H, int T, int d_latent) {
   if (B <= 0 || H <= 0 || T <= 0 || d_latent != mx::mla::DV) return 0;
@@ -615,14 +630,20 @@ extern "C" int mx_mla_decode_absorbed(const void* q_nope, const void* q_rope, co
   void* q_lat = ws;
   void* o_lat = ws + lat;
   void* dws = workspace_bytes(B, H, T) ? (void*)(ws + 2 * lat) : nullptr;
+  // Both products are checked before anything is enqueued.
   // q_lat[b,h,:] = q_nope[b,h,:] . W_UK[h]   (one product per head)
-  int rc = mx_gemm_bf16_batched(q_nope, w_uk, q_lat, H, B, DV, d_nope, H * d_nope, DV, H * DV, d_nope,
-                                (long long)d_nope * DV, DV, stream);
+  const long long sq_uk = (long long)d_nope * DV, sq_uv = (long long)DV * d_v;
+  if (const int e = mx::gemm::batched_check(q_nope, w_uk, q_lat, H, B, DV, d_nope, H * d_nope, DV, H * DV, d_nope,
+                                            sq_uk, DV))
+    return e;
+  // o[b,h,:] = o_lat[b,h,:] . W_UV[h]
+  if (const int e = mx::gemm::batched_check(o_lat, w_uv, O, H, B, d_v, DV, H * DV, d_v, H * d_v, DV, sq_uv, d_v))
+    return e;
+  int rc = mx_gemm_bf16_batched(q_nope, w_uk, q_lat, H, B, DV, d_nope, H * d_nope, DV, H * DV, d_nope, sq_uk, DV,
+                                stream);
   if (rc) return rc;
   // latent attention with Q = [q_lat, q_rope]
   rc = launch_decode(q_lat, q_rope, DV, DQK - DV, KV, o_lat, B, H, T, scale, dws, s);
   if (rc) return rc;
-  // o[b,h,:] = o_lat[b,h,:] . W_UV[h]
-  return mx_gemm_bf16_batched(o_lat, w_uv, O, H, B, d_v, DV, H * DV, d_v, H * d_v, DV, (long long)DV * d_v, d_v,
-                              stream);
+  return mx_gemm_bf16_batched(o_lat, w_uv, O, H, B, d_v, DV, H * DV, d_v, H * d_v, DV, sq_uv, d_v, stream);
 }

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "mx_kernels.h"
 
 namespace mx {
@@ -322,3 +324,27 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     hipError_t _e = (expr);                      \
     if (_e != hipSuccess) return MX_ERR_LAUNCH;  \
   } while (0)
+
+namespace mx {
+
+// Raise kernel F's dynamic-LDS limit to `bytes` once per device and
+// process (thread-safe), instead of on every launch: the attribute call
+// is host work that the few-microsecond decode launches would otherwise
+// pay each time.  `bytes` is a constant of each kernel instantiation.
+constexpr int kMaxDevices = 64;
+template <auto F>
+inline hipError_t lds_limit_once(int bytes) {
+  static std::once_flag once[kMaxDevices];
+  static hipError_t rc[kMaxDevices];
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices)
+    return hipFuncSetAttribute((const void*)F, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  std::call_once(once[dev], [&] {
+    rc[dev] = hipFuncSetAttribute((const void*)F, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  });
+  return rc[dev];
+}
+
+}  // namespace mx

@@ -26,7 +26,10 @@
 //    infinite amax) take the plain division, so every residual that can
 //    reach a nonzero e4m3 code is a normal fp32 number;
 //  * the packed converts (v_cvt_pk_fp8_f32, round to nearest even) do the
-//    e4m3 encoding.
+//    e4m3 encoding;
+//  * non-finite inputs follow the host recipe: a block holding a NaN gets
+//    scale 1, a block whose amax is infinite gets scale inf (its finite
+//    values encode to +-0, its infinities to NaN), and NaN stays NaN.
 #include "mx_common.h"
 
 namespace mx {
@@ -60,17 +63,30 @@ __global__ __launch_bounds__(NT) void quant_fp8_act_kernel(const uint16_t* __res
     v[8 + 2 * w] = T::to_f32(b[w] & 0xffffu);
     v[8 + 2 * w + 1] = T::to_f32(b[w] >> 16);
   }
+  // Block amax; a NaN anywhere in the block makes its scale 1 (the host
+  // recipe's amax is then NaN and `amax > 0` false).
   float amax = 0.f;
+  int nan = 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  for (int i = 0; i < 16; ++i) {
+    amax = fmaxf(amax, fabsf(v[i]));
+    nan |= v[i] != v[i];
+  }
 #pragma unroll
-  for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 8));
-  const float s = amax > 0.f ? amax / kE4M3Max : 1.0f;
+  for (int off = 1; off < 8; off <<= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, off, 8));
+    nan |= __shfl_xor(nan, off, 8);
+  }
+  const float s = nan ? 1.0f : (amax > 0.f ? amax / kE4M3Max : 1.0f);
 
-  // x / s correctly rounded: the reciprocal refinement when every lane's
-  // block allows it (the common case), else the plain division
-  float q[16];
-  if (__all(s >= 0x1p-90f && s <= 0x1p100f)) {
+  // y = clamp(x / s, -448, 448) with x / s correctly rounded: the
+  // reciprocal refinement when every lane's block allows it (finite values,
+  // s in range: the common case), else the plain division, which also
+  // carries the non-finite cases (x / 1 in a block with a NaN; +-0 and
+  // inf / inf = NaN in a block whose amax is infinite) with NaN kept NaN
+  // through the clamp.
+  float y[16];
+  if (__all(!nan && s >= 0x1p-90f && s <= 0x1p100f)) {
     const float r = 1.0f / s;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -78,21 +94,22 @@ __global__ __launch_bounds__(NT) void quant_fp8_act_kernel(const uint16_t* __res
       const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, s, v[i]), r, q0);
       // x = -0 would come out +0 (the residual is +0), where -0 / s is -0;
       // every other quotient already carries x's sign
-      q[i] = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q1, s, v[i]), r, q1), v[i]);
+      const float q = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q1, s, v[i]), r, q1), v[i]);
+      y[i] = fminf(fmaxf(q, -kE4M3Max), kE4M3Max);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) q[i] = v[i] / s;
+    for (int i = 0; i < 16; ++i) {
+      const float q = v[i] / s;
+      y[i] = q != q ? q : fminf(fmaxf(q, -kE4M3Max), kE4M3Max);
+    }
   }
 
   u32x4 out;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    float y[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(q[4 * w + j], -kE4M3Max), kE4M3Max);
-    int p = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
-    p = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], p, true);
+    int p = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * w], y[4 * w + 1], 0, false);
+    p = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * w + 2], y[4 * w + 3], p, true);
     out[w] = (uint32_t)p;
   }
   if (live) {

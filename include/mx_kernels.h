@@ -7,9 +7,13 @@
  * passed as `stream` (NULL = the legacy default stream) and returns an int
  * status: MX_OK (0) or a negative MX_ERR_* code.  No entry point exits,
  * aborts, synchronises the device or allocates device memory.  Arguments
- * are validated before anything is launched, so an error return means
- * nothing was enqueued.  The library holds no state: calls are re-entrant
- * and may be issued from several host threads on different streams.
+ * are validated before anything is launched — for an entry point that
+ * launches several kernels, the arguments of all of them — so any error
+ * return other than MX_ERR_LAUNCH means nothing was enqueued.
+ * MX_ERR_LAUNCH reports that the HIP runtime refused a launch; in a
+ * multi-kernel entry point the kernels before it may already be enqueued.
+ * The library holds no per-call state: calls are re-entrant and may be
+ * issued from several host threads on different streams.
  *
  * The reference (baladithyab/cuda-oxide-bench) launches each of these
  * operations from a Python harness through `ct.launch(stream.ptr, grid,
@@ -96,7 +100,11 @@ int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, const float* s
  * leading dimension ldx >= K, in elements):
  *   scales[m,kb] = max_{k in kb} |X[m,k]| / 448   (1.0 for an all-zero block)
  *   Q[m,k]       = e4m3fn(RNE(clamp(X[m,k] / scales[m,kb], -448, 448)))
- * Q is [M,K] row-major bytes, scales [M, K/128] fp32.  Requires K % 128 == 0,
+ * Q is [M,K] row-major bytes, scales [M, K/128] fp32.  Non-finite values
+ * follow the same recipe: a block holding a NaN has scale 1 (its amax is
+ * NaN, not > 0), a block with an infinite amax has scale +inf (its finite
+ * values encode to +-0, its infinities to NaN), and NaN encodes to a NaN
+ * code (0x7F or 0xFF).  Requires K % 128 == 0,
  * ldx % 8 == 0, 16-byte aligned X and Q.
  * Replaces: the host-side generation of the fp8 GEMM operands
  * (mojo-matmul-fp8/matmul_fp8.mojo:262-270 fills them on the CPU), extended

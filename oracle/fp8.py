@@ -69,9 +69,15 @@ def quantize_blockwise(x: np.ndarray, block: tuple[int, int]) -> tuple[np.ndarra
     blk = x.reshape(R // br, br, C // bc, bc)
     amax = np.abs(blk).max(axis=(1, 3))
     scale = np.where(amax > 0, amax / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
-    y = (blk / scale[:, None, :, None]).astype(np.float32)
-    y = np.clip(y, -E4M3_MAX, E4M3_MAX)
-    codes = e4m3_encode(y.reshape(R, C))
+    with np.errstate(invalid="ignore", divide="ignore"):
+        y = (blk / scale[:, None, :, None]).astype(np.float32)
+    y = np.clip(y, -E4M3_MAX, E4M3_MAX).reshape(R, C)
+    # Non-finite inputs: a NaN amax fails `amax > 0` (scale 1), an infinite
+    # one gives scale inf (finite values -> +-0, inf / inf -> NaN); NaN
+    # stays NaN through the clip and takes the NaN code 0x7F.
+    nan = np.isnan(y)
+    codes = e4m3_encode(np.where(nan, 0.0, y))
+    codes[nan] = 0x7F
     return codes, scale
 
 
@@ -87,6 +93,18 @@ def gemm_fp8_bs_ref(a_codes: np.ndarray, sa: np.ndarray, b_codes: np.ndarray, sb
     a = torch.from_numpy(dequantize_blockwise(a_codes, sa, (1, 128)))
     b = torch.from_numpy(dequantize_blockwise(b_codes, sb, (128, 128)))
     return (a @ b).numpy()
+
+
+def gemm_fp8_bs_ref_torch(a8: torch.Tensor, sa: torch.Tensor, b8: torch.Tensor, sb: torch.Tensor) -> torch.Tensor:
+    """gemm_fp8_bs_ref on torch.float8_e4m3fn tensors: the same dequantised
+    fp32 operands (torch's exact e4m3 -> fp32 cast times the block scales)
+    and the same fp32 product, without the numpy decode table, so it runs
+    at 8192^3 in seconds (the bench's CPU baseline)."""
+    a = a8.detach().cpu().to(torch.float32) * sa.detach().cpu().float().repeat_interleave(128, dim=1)
+    n = b8.shape[1]
+    sbf = sb.detach().cpu().float().repeat_interleave(128, dim=0).repeat_interleave(128, dim=1)[:, :n]
+    b = b8.detach().cpu().to(torch.float32) * sbf
+    return a @ b
 
 
 def fp8_tensor_codes(t: torch.Tensor) -> np.ndarray:

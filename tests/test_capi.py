@@ -151,3 +151,20 @@ def test_mla_absorbed_validation():
     assert f(P, P, P, P, P, P, 32, 128, 4096, 128, 128, 0.07, P, need - 1, None) == _lib.MX_ERR_WORKSPACE
     assert f(P, P, P, P, P, P, 32, 128, 4096, 100, 128, 0.07, P, need, None) == _lib.MX_ERR_SHAPE
     assert f(P, P, P, P, P, P, 32, 128, 4096, 128, 128, -1.0, P, need, None) == _lib.MX_ERR_SHAPE
+
+
+def test_mla_absorbed_checks_every_launch_before_the_first():
+    # Without a GPU any launch attempt returns MX_ERR_LAUNCH, so a validation
+    # code shows the call returned before enqueuing the first projection.
+    lib = _lib.load()
+    f = lib.mx_mla_decode_absorbed
+    need = lib.mx_mla_decode_absorbed_workspace(32, 128, 4096)
+    bad = ctypes.c_void_p(0x10008)
+    # output projection invalid, absorption valid
+    assert f(P, P, P, P, bad, P, 32, 128, 4096, 128, 128, 0.07, P, need, None) == _lib.MX_ERR_ALIGN  # W_UV
+    assert f(P, P, P, P, P, bad, 32, 128, 4096, 128, 128, 0.07, P, need, None) == _lib.MX_ERR_ALIGN  # O
+    assert f(P, P, P, P, P, P, 32, 128, 4096, 128, 4104, 0.07, P, need, None) == _lib.MX_ERR_SHAPE   # d_v
+    # decode invalid, both projections valid
+    assert f(P, P, bad, P, P, P, 32, 128, 4096, 128, 128, 0.07, P, need, None) == _lib.MX_ERR_ALIGN  # KV
+    # a valid call gets as far as the runtime
+    assert f(P, P, P, P, P, P, 32, 128, 4096, 128, 128, 0.07, P, need, None) == _lib.MX_ERR_LAUNCH

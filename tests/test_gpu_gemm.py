@@ -117,6 +117,23 @@ def test_target_size_sampled(ops):
     assert np.abs(got - ref).max() / scale <= TOL
 
 
+@pytest.mark.parametrize("mnk,path", [((2048, 2048, 2048), "register-staged 128x128 (tiles128 >= 256)"),
+                                      ((4096, 8192, 264), "register-staged 256x256 (tiles256 >= 512, K % 32 != 0)"),
+                                      ((2048, 2048, 72), "register-staged 128x128, K tail of 8")])
+def test_register_staged_paths(ops, mnk, path):
+    """Single GEMMs that land on the register-staged 128x128 and 256x256
+    kernels (and their one-stage-ahead load loop): 2048^3 is also a size of
+    the reference's mixed-dtype harness sweep (cutile-matmul-tiled-mixed/main.py:60)."""
+    m, n, k = mnk
+    announce(f"gemm_bf16 {m}x{n}x{k} {path}")
+    a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
+    c = run(ops, a, b)
+    ref = ogemm.gemm_ref(a, b)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+
+
 def test_rejects_bad_arguments(ops):
     a = torch.zeros((64, 60), dtype=torch.bfloat16, device="cuda")  # K % 8 != 0
     b = torch.zeros((60, 64), dtype=torch.bfloat16, device="cuda")
@@ -125,9 +142,10 @@ def test_rejects_bad_arguments(ops):
 
 
 @pytest.mark.parametrize("bmnk", [(1, 64, 64, 64), (7, 100, 136, 72), (128, 32, 512, 128), (128, 32, 128, 512), (16, 5, 40, 192),
-                                  (3, 300, 264, 520)])
+                                  (3, 300, 264, 520), (4, 1024, 1024, 256)])
 def test_batched_vs_oracle(ops, bmnk):
-    """Strided-batched GEMM: every item against the fp32 oracle."""
+    """Strided-batched GEMM: every item against the fp32 oracle (small-M,
+    64x64 and, at 4 x 1024x1024x256, the 128x128 register-staged kernel)."""
     nb, m, n, k = bmnk
     announce(f"gemm_bf16_batched {nb}x{m}x{n}x{k}")
     g = torch.Generator().manual_seed(nb * 131 + m)

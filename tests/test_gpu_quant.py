@@ -122,3 +122,31 @@ def test_feeds_fp8_gemm(ops):
 def test_rejects_bad_k(ops):
     with pytest.raises(Exception):
         ops.quant_fp8_act(torch.zeros((4, 96), dtype=torch.bfloat16, device="cuda"))
+
+
+def _nan_codes_as_one(c):
+    c = np.asarray(c, dtype=np.uint8).copy()
+    c[(c & 0x7F) == 0x7F] = 0x7F
+    return c
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_non_finite_blocks(ops, dt):
+    """NaN and inf in the input, as the host recipe treats them: a block
+    holding a NaN has scale 1 (inf in it clamps to +-448), a block with an
+    infinite amax has scale inf (finite values -> +-0, infinities -> NaN);
+    NaN codes compared as NaN whatever their sign bit."""
+    announce(f"quant_fp8 non-finite {dt}")
+    x = torch.randn((4, 512), generator=torch.Generator().manual_seed(8))
+    x[0, 3] = float("nan")
+    x[0, 200] = float("inf")
+    x[1, 130] = float("-inf")
+    x[1, 131] = float("nan")
+    x[2, 300] = float("inf")
+    x[2, 301] = float("-inf")
+    x[3, 400] = -float("nan")
+    x = x.to(dt)
+    q, s = quant(ops, x)
+    qe, se = expect(x)
+    assert np.array_equal(s, se)
+    assert np.array_equal(_nan_codes_as_one(q), _nan_codes_as_one(qe))

@@ -85,3 +85,43 @@ def test_scale_linearity_oracle():
     assert np.allclose(c1[3], 4 * c0[3], rtol=1e-6, atol=1e-6)
     # only e4m3 quantisation noise separates it from the exact fp32 product
     assert np.abs(c0 - a @ b).max() / np.abs(a @ b).max() < 5e-2
+
+
+def test_torch_dequant_reference_matches_numpy_table():
+    # The bench's CPU baseline uses the torch form of the dequantised product:
+    # it must give the same fp32 result as the table-driven numpy oracle
+    # (identical dequantised operands, one fp32 matmul), ragged N included.
+    g = torch.Generator().manual_seed(11)
+    a = torch.randn((40, 384), generator=g)
+    b = torch.randn((384, 200), generator=g)
+    a8, sa = quant.quantize_fp8_blockwise(a, (1, 128))
+    b8, sb = quant.quantize_fp8_blockwise(b, (128, 128))
+    ref = ofp8.gemm_fp8_bs_ref(ofp8.fp8_tensor_codes(a8), sa.numpy(), ofp8.fp8_tensor_codes(b8), sb.numpy())
+    got = ofp8.gemm_fp8_bs_ref_torch(a8, sa, b8, sb).numpy()
+    assert np.array_equal(got, ref)
+
+
+def _nan_codes_as_one(c):
+    c = np.asarray(c, dtype=np.uint8).copy()
+    c[(c & 0x7F) == 0x7F] = 0x7F
+    return c
+
+
+def test_non_finite_blocks_follow_the_torch_recipe():
+    # A NaN in a block makes its scale 1 (NaN amax is not > 0); an infinite
+    # amax makes it inf (finite values -> +-0, inf -> NaN).  The oracle must
+    # agree with the package's torch quantiser, whose e4m3 cast is torch's.
+    x = np.random.default_rng(5).standard_normal((4, 384)).astype(np.float32)
+    x[0, 3] = np.nan
+    x[0, 200] = np.inf            # block 1 of row 0: inf amax
+    x[1, 130] = -np.inf
+    x[1, 131] = np.nan            # NaN and inf in one block: scale 1, inf -> -448
+    x[2, 300] = np.inf
+    x[2, 301] = -np.inf           # inf and -inf: both NaN, the rest +-0
+    codes, scales = ofp8.quantize_blockwise(x, (1, 128))
+    tq, ts = quant.quantize_fp8_blockwise(torch.from_numpy(x), (1, 128))
+    assert np.array_equal(scales, ts.numpy())
+    assert np.array_equal(_nan_codes_as_one(codes), _nan_codes_as_one(tq.view(torch.uint8).numpy()))
+    assert scales[0, 0] == 1.0 and scales[0, 1] == np.inf and scales[1, 1] == 1.0
+    assert codes[1, 130] == 0xFE  # -inf / 1 clipped to -448
+    assert codes[0, 3] == 0x7F and codes[0, 200] == 0x7F
