@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple] = {
     "mx_mla_decode": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "mx_mla_prefill_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _i, _vp]),
     "mx_mla_decode_workspace": (_sz, [_i, _i, _i, _i]),
+    "mx_mla_decode_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "mx_gdn_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "mx_kda_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "mx_quant_fp8_act": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),

@@ -606,6 +606,59 @@ extern "C" int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int 
   return launch_decode(Q, (const uint16_t*)Q + DV, DQK, DQK, KV, O, B, H, T, scale, workspace, (hipStream_t)stream);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split partials go to a library-owned device
+// array instead of a caller workspace.  `scratch` is a host-side stand-in
+// for the array in host code, not a device address: its device address
+// is looked up once per device (with that device current) and only that
+// address is ever passed to a kernel.  Every call on one GPU shares that
+// GPU's array, so calls that overlap on one GPU race; the kernels write
+// every partial before the combine reads it, so nothing needs clearing.
+// ---------------------------------------------------------------------------
+namespace mx {
+namespace mla {
+
+static __device__ __align__(256) unsigned char scratch[MX_MLA_SCRATCH_BYTES];
+
+static std::once_flag scratch_once[kMaxDevices];
+static void* scratch_dev[kMaxDevices];
+static hipError_t scratch_rc[kMaxDevices];
+
+// Device address of this device's `scratch`, looked up on the first call.
+static int scratch_ptr(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MX_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxDevices) return MX_ERR_UNSUPPORTED;
+  std::call_once(scratch_once[dev], [dev] {
+    void* p = nullptr;
+    scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    scratch_dev[dev] = scratch_rc[dev] == hipSuccess ? p : nullptr;
+  });
+  if (scratch_rc[dev] != hipSuccess || !scratch_dev[dev]) return MX_ERR_LAUNCH;
+  *out = scratch_dev[dev];
+  return MX_OK;
+}
+
+}  // namespace mla
+}  // namespace mx
+
+extern "C" int mx_mla_decode_noalloc(const void* Q, const void* KV, void* O, int B, int H, int T, int d_latent,
+                                     int d_rope, float scale, void* stream) {
+  using namespace mx::mla;
+  if (!Q || !KV || !O) return MX_ERR_NULL;
+  if (B <= 0 || H <= 0 || T <= 0) return MX_ERR_SHAPE;
+  if (d_latent != DV || d_rope != DQK - DV) return MX_ERR_UNSUPPORTED;
+  if (const int e = check_decode(KV, B, H, T, scale)) return e;
+  if (((uintptr_t)Q | (uintptr_t)O) & 15) return MX_ERR_ALIGN;
+  const size_t need = workspace_bytes(B, H, T);
+  if (need > (size_t)MX_MLA_SCRATCH_BYTES) return MX_ERR_WORKSPACE;
+  void* ws = nullptr;
+  if (need > 0) {
+    if (const int e = scratch_ptr(&ws)) return e;
+  }
+  return launch_decode(Q, (const uint16_t*)Q + DV, DQK, DQK, KV, O, B, H, T, scale, ws, (hipStream_t)stream);
+}
+
 extern "C" size_t mx_mla_decode_absorbed_workspace(int B, int H, int T) {
   if (B <= 0 || H <= 0 || T <= 0) return 0;
   return mx::mla::absorbed_workspace_bytes(B, H, T);

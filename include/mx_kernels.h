@@ -164,6 +164,22 @@ int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int H, int T, i
 size_t mx_mla_decode_workspace(int B, int H, int T, int d_latent);
 
 /*
+ * Allocation-free MLA decode: mx_mla_decode without a workspace argument.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The same kernels and results as mx_mla_decode; the split
+ * partials go to a library-owned device array of MX_MLA_SCRATCH_BYTES per
+ * GPU (held from the library's load until the process ends).  Problems
+ * whose mx_mla_decode_workspace(B, H, T, d_latent) exceeds that size return
+ * MX_ERR_WORKSPACE.  All calls on one GPU share its array: calls that
+ * overlap on one GPU (concurrent streams or host threads) race and must be
+ * serialised by the caller.  The caller still allocates Q, KV and O.
+ */
+#define MX_MLA_SCRATCH_BYTES (128u << 20)
+int mx_mla_decode_noalloc(const void* Q, const void* KV, void* O, int B, int H, int T, int d_latent,
+                          int d_rope, float scale, void* stream);
+
+/*
  * The whole weight-absorbed MLA decode step (DeepSeek-V3 form):
  *   q_lat[b,h,:] = q_nope[b,h,:] · W_UK[h]              (d_nope -> 512)
  *   o_lat[b,h,:] = mx_mla_decode with Q = [q_lat, q_rope] over KV[b]
