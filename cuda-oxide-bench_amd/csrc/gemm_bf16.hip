@@ -486,6 +486,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_dma_kernel(const ui
   };
   static_assert(KS % 2 == 0, "k-step 0 of every tile uses buffer 0");
 
+  land_args(C);  // C is used only after the K loop
   // Prologue: tiles 0 .. NS-2 in flight (as in every step, tiles past the
   // end re-load the last one), wait for tile 0.
 #pragma unroll

@@ -24,24 +24,33 @@
 //    128(m) x 64(n): the fp32 accumulators stay in architectural VGPRs,
 //    where the promotion FMAs can reach them.  Grids under 256 such tiles
 //    use 128x128 tiles.
-//  * A and B tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR
-//    staging) in their natural row-major layouts, double buffered.  A^T
-//    fragments are plain ds_read_b128; B^T fragments come from k-major B
-//    rows through gfx950's transposing read ds_read_b64_tr_b8: in each
+//  * A and B go HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging)
+//    in 64-byte-deep stages (half a scale block) through a 5-slot ring that
+//    fills the 160 KB of LDS: while a wave computes scale block j (stages
+//    2j, 2j+1) the stages 2j+2 .. 2j+4 are in flight, one and a half scale
+//    blocks ahead, with one barrier per scale block.  Every block issues
+//    exactly two stages (past the end, the last stage again into slots
+//    nobody reads), so the wait counts are the same in every block.
+//  * The block scales are read with vector loads issued as inline asm and
+//    waited for by the same vmcnt wait that lands the stages, as operands
+//    of that wait: the compiler tracks neither, so it never inserts a
+//    vmcnt(0) of its own that would drain the ring.
+//  * A^T fragments are plain ds_read_b128; B^T fragments come from k-major
+//    B rows through gfx950's transposing read ds_read_b64_tr_b8: in each
 //    16-lane group, lane 8h+b receives byte b of the 8-byte rows addressed
 //    by lanes 2j+h, so pointing lane 2j+h at k-row j, columns 8h..8h+7
 //    gives every lane 8 consecutive k-bytes of its own column.  No VALU
 //    transposes.
 //  * 16-byte chunks are XOR-swizzled per row so every fragment read phase
 //    is bank-conflict free.
-#include <type_traits>
-
 #include "mx_common.h"
 
 namespace mx {
 namespace gemm8 {
 
-constexpr int BK = 128;   // bytes of K per tile = one scale block
+constexpr int SBK = 128;   // bytes of K per scale block
+constexpr int BKS = 64;    // bytes of K per LDS stage (one 32x32x64 k-step)
+constexpr int NS = 5;      // ring slots
 constexpr int NWAVES = 8;  // 2 (m) x 4 (n), two waves per SIMD
 constexpr int NT = 64 * NWAVES;
 constexpr int GROUP_M = 8;
@@ -59,27 +68,54 @@ __device__ __forceinline__ u32x2 lds_read_tr8_at(uint32_t addr) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32*)(uintptr_t)addr));
 }
 
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// A 4-byte vector load the compiler does not track (see the file comment):
+// the result may only be read after a wait_scales() that names it.
+__device__ __forceinline__ float ld_scale(const float* sbase, uint32_t voff) {
+  float x;
+  asm volatile("global_load_dword %0, %1, %2" : "=v"(x) : "v"(voff), "s"(sbase) : "memory");
+  return x;
+}
+// s_waitcnt vmcnt(N) that also lands the untracked scale loads: the scale
+// registers are operands, so no read of them is scheduled before it.
+template <int N, int FM>
+__device__ __forceinline__ void wait_scales(float (&sa)[FM], float& sb) {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  static_assert(FM == 2 || FM == 4, "scale registers");
+  if constexpr (FM == 4)
+    asm volatile("s_waitcnt vmcnt(%5)" : "+v"(sa[0]), "+v"(sa[1]), "+v"(sa[2]), "+v"(sa[3]), "+v"(sb) : "i"(N)
+                 : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(sa[0]), "+v"(sa[1]), "+v"(sb) : "i"(N) : "memory");
+}
+#pragma clang diagnostic pop
+
 template <int BM, int BN>
 struct Cfg {
   static constexpr int WM = 2, WN = 4;
   static constexpr int TM = BM / WM, TN = BN / WN;   // wave tile
   static constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments
-  static constexpr int A_B = BM * BK;                // A stage: BM rows of 128 B
-  static constexpr int B_B = BK * BN;                // B stage: 128 k-rows of BN B
-  static constexpr int STAGE = A_B + B_B;
-  static constexpr int A_LPW = A_B / 1024 / NWAVES;  // 1 KB direct loads per wave
-  static constexpr int B_LPW = B_B / 1024 / NWAVES;
+  static constexpr int A_S = BM * BKS;               // A stage: BM rows of 64 B
+  static constexpr int B_S = BKS * BN;               // B stage: 64 k-rows of BN B
+  static constexpr int STAGE = A_S + B_S;
+  static constexpr int LDS = NS * STAGE;
+  static constexpr int A_LPW = A_S / 1024 / NWAVES;  // 1 KB direct loads per wave per stage
+  static constexpr int B_LPW = B_S / 1024 / NWAVES;
+  static constexpr int LPS = A_LPW + B_LPW;
   static constexpr int B_CH = BN / 16;               // 16-byte chunks per B row
   static constexpr int B_RPL = 1024 / BN;            // B rows per 1 KB load
   static_assert(FM >= 1 && FN >= 1 && A_LPW >= 1 && B_LPW >= 1, "tile split");
   static_assert(TN <= 128 && 128 % TN == 0, "a wave's columns share one weight-scale block");
   static_assert(BN == 128 || BN == 256, "B row swizzle");
+  static_assert(LDS <= 160 * 1024, "LDS ring");
 };
 
-// Chunk position swizzles.  A rows (128 B): a 16-lane b128 phase reads one
-// chunk of 16 consecutive rows, two rows per 256 B.  B rows: a 32-lane
-// transposing phase reads 8 consecutive k-rows x 2 adjacent chunks.
-__device__ __forceinline__ int swz_a(int m) { return (m >> 1) & 7; }
+// Chunk position swizzles.  A rows (64 B, 4 chunks): a 16-lane b128 phase
+// reads one chunk of 16 consecutive rows, four rows per 256 B, so the
+// position takes (m/4)%4.  B rows: a 32-lane transposing phase reads 8
+// consecutive k-rows x 2 adjacent chunks.
+__device__ __forceinline__ int swz_a(int m) { return (m >> 2) & 3; }
 template <int BN>
 __device__ __forceinline__ int swz_b(int k) {
   return BN == 256 ? ((k & 7) << 1) : (((k >> 1) & 3) << 1);
@@ -92,7 +128,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
                                                            const float* __restrict__ sB,
                                                            uint16_t* __restrict__ C, int M, int N, int K) {
   using CF = Cfg<BM, BN>;
-  constexpr int FM = CF::FM, FN = CF::FN;
+  constexpr int FM = CF::FM, FN = CF::FN, LPS = CF::LPS;
   extern __shared__ __align__(1024) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
@@ -109,11 +145,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   const int tm = first_m + (id % per_group) % gsz;
   const int tn = (id % per_group) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kblocks = K / BK;
+  const int kblocks = K / SBK;
+  const int nst = 2 * kblocks;  // 64-byte stages
   const int nblocks_n = (N + 127) / 128;
 
-  // ---- direct loads.  A load n: rows 8n .. 8n+7 (lane i: row 8n + i/8,
-  // chunk (i%8) ^ swz_a(row)); B load n: k-rows B_RPL*n .. (lane i: k-row
+  // ---- direct loads.  A load n: rows 16n .. 16n+15 (lane i: row 16n + i/4,
+  // chunk (i%4) ^ swz_a(row)); B load n: k-rows B_RPL*n .. (lane i: k-row
   // B_RPL*n + i/B_CH, chunk (i%B_CH) ^ swz_b(row)).  Rows past M and
   // columns past N re-read the last valid ones (never stored). ----
   const uint32_t lds0 = lds_addr(smem);
@@ -121,9 +158,9 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   uint32_t a_off[CF::A_LPW], b_off[CF::B_LPW];
 #pragma unroll
   for (int n = 0; n < CF::A_LPW; ++n) {
-    const int row = 8 * (wave * CF::A_LPW + n) + (lane >> 3);
+    const int row = 16 * (wave * CF::A_LPW + n) + (lane >> 2);
     const int gm = full_m ? m0 + row : min(m0 + row, M - 1);
-    a_off[n] = (uint32_t)(gm - m0) * K + 16 * ((lane & 7) ^ swz_a(row));
+    a_off[n] = (uint32_t)(gm - m0) * K + 16 * ((lane & 3) ^ swz_a(row));
   }
 #pragma unroll
   for (int n = 0; n < CF::B_LPW; ++n) {
@@ -132,42 +169,39 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     if (!full_n) col = min(n0 + col, N - 16) - n0;
     b_off[n] = (uint32_t)row * N + col;
   }
-  // LDS layout [A0 | A1 | B0 | B1]: one base register per fragment reaches
-  // both stages of its operand with the 16-bit immediate offset of ds_read.
-  auto issue = [&](int kb, int stage) {
-    const uint32_t sa = lds0 + stage * CF::A_B, sb = lds0 + 2 * CF::A_B + stage * CF::B_B;
-    const uint8_t* abase = A + (size_t)m0 * K + (size_t)kb * BK;
-    const uint8_t* bbase = B + (size_t)kb * BK * N + n0;
-#pragma unroll
-    for (int n = 0; n < CF::A_LPW; ++n) dma16(abase, a_off[n], sa + (wave * CF::A_LPW + n) * 1024);
-#pragma unroll
-    for (int n = 0; n < CF::B_LPW; ++n) dma16(bbase, b_off[n], sb + (wave * CF::B_LPW + n) * 1024);
+  const uint8_t* a_tile = A + (size_t)m0 * K;
+  const uint8_t* b_tile = B + n0;
+  // Stage s (64 bytes of K) into slot s % NS; stages past the end re-load
+  // the last one (into a slot no later block reads).
+  auto issue_part = [&](int s, int slot, int n) {
+    const int src = min(s, nst - 1);
+    const uint32_t st = lds0 + slot * CF::STAGE;
+    if (n < CF::A_LPW)
+      dma16(a_tile + (size_t)src * BKS, a_off[n], st + (wave * CF::A_LPW + n) * 1024);
+    else
+      dma16(b_tile + (size_t)src * BKS * N, b_off[n - CF::A_LPW],
+            st + CF::A_S + (wave * CF::B_LPW + n - CF::A_LPW) * 1024);
   };
 
-  // ---- fragment lane addresses (stage 0; stage 1 is an immediate away) ----
-  // A^T (B operand): row m = wm*TM + 32 mf + l%32, chunks 4 ks + 2 (l/32) + {0,1}.
+  // ---- fragment lane addresses in slot 0 (a slot is STAGE bytes on) ----
+  // A^T (B operand): row m = wm*TM + 32 mf + l%32, chunks 2 (l/32) + {0,1}.
   const int am = wm * CF::TM + (lane & 31);
-  const uint32_t a_row = lds0 + am * BK;
-  const int a_x = swz_a(am);  // same for every mf (32 rows apart)
+  const int a_x = swz_a(am);  // the same for every mf (32 rows apart)
+  uint32_t a_col[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) a_col[h] = lds0 + am * BKS + 16 * ((2 * (lane >> 5) + h) ^ a_x);
   // B^T (A operand) via tr_b8: in 16-lane group q, lane 2j+h reads k-row
-  // 64 ks + 32 (q>>1) + 8 r + j, columns wn*TN + 32 nf + 16 (q&1) + 8 h.
+  // 32 (q>>1) + 8 r + j, columns wn*TN + 32 nf + 16 (q&1) + 8 h.
   const int q = lane >> 4, jj = (lane & 15) >> 1, hh = lane & 1;
-  const int b_k0 = 32 * (q >> 1) + jj;                       // plus 64 ks + 8 r
+  const int b_k0 = 32 * (q >> 1) + jj;                       // plus 8 r
   const int b_c0 = wn * CF::TN + 16 * (q & 1) + 8 * hh;      // plus 32 nf
-  const uint32_t b_row = lds0 + 2 * CF::A_B + b_k0 * BN;
   const int b_x = swz_b<BN>(b_k0);  // rows 8 apart share it
   uint32_t b_col[FN];
 #pragma unroll
   for (int nf = 0; nf < FN; ++nf) {
     const int col = b_c0 + 32 * nf;
-    b_col[nf] = b_row + 16 * ((col >> 4) ^ b_x) + (col & 15);
+    b_col[nf] = lds0 + CF::A_S + b_k0 * BN + 16 * ((col >> 4) ^ b_x) + (col & 15);
   }
-  const int a_c = 2 * (lane >> 5);
-  uint32_t a_col[2][2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) a_col[ks][h] = a_row + 16 * ((4 * ks + a_c + h) ^ a_x);
 
   f32x16 acc[FN][FM];
 #pragma unroll
@@ -175,85 +209,130 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
 
-  // Block scales: sA row of this lane per m fragment, sB per wave.  The
-  // scales of tile kb+1 are loaded before its tile loads are issued, so
-  // the wait that lands the tile also lands them.
-  int sa_row[FM];
+  // Block scales: the sA row of this lane per m fragment, the sB of this
+  // wave's 128-column block (wave-uniform, read by every lane).
+  uint32_t sa_off[FM];
 #pragma unroll
-  for (int mf = 0; mf < FM; ++mf) sa_row[mf] = min(m0 + am + 32 * mf, M - 1) * kblocks;
-  const int wave_nb = min((n0 + wn * CF::TN) / 128, nblocks_n - 1);
-  // The weight scale is wave-uniform, but it is loaded with a vector load
-  // (an opaque per-lane zero offset): a scalar load would share lgkmcnt with
-  // the LDS reads and return out of order, turning every LDS wait of the
-  // tile into lgkmcnt(0).
-  int vzero;
-  asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
-  float sa_c[FM], sb_c;
-  auto load_scales = [&](int kb) {
-    sb_c = sB[(size_t)kb * nblocks_n + wave_nb + vzero];
+  for (int mf = 0; mf < FM; ++mf) sa_off[mf] = (uint32_t)min(m0 + am + 32 * mf, M - 1) * (uint32_t)kblocks * 4u;
+  const uint32_t sb_off = (uint32_t)min((n0 + wn * CF::TN) / 128, nblocks_n - 1) * 4u;
+  float sa_n[FM], sb_n;
+  auto load_scales = [&](int j) {
+    const int jb = min(j, kblocks - 1);
+    sb_n = ld_scale(sB + (size_t)jb * nblocks_n, sb_off);
 #pragma unroll
-    for (int mf = 0; mf < FM; ++mf) sa_c[mf] = sA[sa_row[mf] + kb];
+    for (int mf = 0; mf < FM; ++mf) sa_n[mf] = ld_scale(sA + jb, sa_off[mf]);
   };
 
-  // One K tile (= one scale block) in stage STG.  Reads go out in the order
-  // the MFMAs consume them; the A^T fragment of each k half is re-read for
-  // the next row block right after its MFMAs are issued.  The fragments of
-  // one row block build their partials side by side, so no MFMA waits for
-  // the one just before it; each partial is promoted with one FMA per
-  // element.
-  auto tile = [&](int kb, auto stg_tag) {
-    constexpr int STG = decltype(stg_tag)::value;
-    constexpr uint32_t oa = STG * CF::A_B, ob = STG * CF::B_B;
-    wait_vmcnt<0>();  // this wave's loads of tile kb and its scales landed
-    lds_barrier();    // tile kb visible to all waves; the other stage is free
+  auto read_b = [&](uint32_t so, int nf) {
+    u32x2 v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = lds_read_tr8_at(b_col[nf] + so + 8 * r * BN);
+    return i32x8{(int)v[0][0], (int)v[0][1], (int)v[1][0], (int)v[1][1],
+                 (int)v[2][0], (int)v[2][1], (int)v[3][0], (int)v[3][1]};
+  };
+  auto read_a = [&](uint32_t so, int mf) {
+    const uint32_t r = so + 32 * mf * BKS;
+    const u32x4 lo = lds_ld128(a_col[0] + r);
+    const u32x4 hi = lds_ld128(a_col[1] + r);
+    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+
+  land_args(C);  // C is used only after the loop
+
+  // Prologue: the scales of block 0 and stages 0..2 in flight.
+  load_scales(0);
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+#pragma unroll
+    for (int n = 0; n < LPS; ++n) issue_part(s, s, n);
+
+  // Scale block j: stages 2j (slot s0) and 2j+1 (slot s1).  The two MFMAs
+  // of each fragment build a fresh fp32 partial over the block's 128 k; the
+  // fragments of one row block build theirs side by side, then each is
+  // promoted with one FMA per element: acc += (sA sB) * partial.  Stages
+  // 2j+3 and 2j+4 are issued spread over the row blocks.
+  int s0 = 0;  // slot of stage 2j
+  for (int j = 0; j < kblocks; ++j) {
+    // Stages 2j, 2j+1 and the scales of block j landed (stage 2j+2 may be
+    // in flight); after the barrier every wave has finished block j-1, so
+    // its slots take stages 2j+3 and 2j+4.
+    wait_scales<LPS>(sa_n, sb_n);
+    lds_barrier();
     float s_m[FM];
 #pragma unroll
-    for (int mf = 0; mf < FM; ++mf) s_m[mf] = sa_c[mf] * sb_c;
-    if (kb + 1 < kblocks) {
-      load_scales(kb + 1);
-      issue(kb + 1, STG ^ 1);
-    }
-    auto read_b = [&](int ks, int nf) {
-      u32x2 v[4];
+    for (int mf = 0; mf < FM; ++mf) s_m[mf] = sa_n[mf] * sb_n;
+    load_scales(j + 1);
+    const int s1 = s0 == NS - 1 ? 0 : s0 + 1;
+    const int s3 = s0 >= 2 ? s0 - 2 : s0 + 3;  // slot of stage 2j+3 (= that of 2j-2)
+    const int s4 = s3 == NS - 1 ? 0 : s3 + 1;
+    const uint32_t so0 = s0 * CF::STAGE, so1 = s1 * CF::STAGE;
+
+    // Issue order (pinned by sched barriers): at most ~10 LDS reads in
+    // flight (lgkmcnt counts 15), each MFMA waiting only for its own
+    // fragments; the promotion of partial nf of row block mf is issued
+    // after the MFMA that follows its last one, so its FMAs run in that
+    // MFMA's shadow; a partial is rewritten only after its FMAs issued.
+    i32x8 bf0[FN], bf1[FN], a0, a1;
+    f32x16 p[FN];
+    bf0[0] = read_b(so0, 0);
+    a0 = read_a(so0, 0);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = lds_read_tr8_at(b_col[nf] + ob + (64 * ks + 8 * r) * BN);
-      return i32x8{(int)v[0][0], (int)v[0][1], (int)v[1][0], (int)v[1][1],
-                   (int)v[2][0], (int)v[2][1], (int)v[3][0], (int)v[3][1]};
+    for (int nf = 1; nf < FN; ++nf) bf0[nf] = read_b(so0, nf);
+    __builtin_amdgcn_sched_barrier(0);
+    auto promote = [&](int nf, int mf) { acc[nf][mf] += s_m[mf] * p[nf]; };
+    auto dma_share = [&](int mf) {
+#pragma unroll
+      for (int n = (2 * LPS * mf) / FM; n < (2 * LPS * (mf + 1)) / FM; ++n) {
+        if (n < LPS)
+          issue_part(2 * j + 3, s3, n);
+        else
+          issue_part(2 * j + 4, s4, n - LPS);
+      }
     };
-    auto read_a = [&](int mf, int ks) {
-      const uint32_t r = oa + 32 * mf * BK;
-      const u32x4 lo = lds_ld128(a_col[ks][0] + r);
-      const u32x4 hi = lds_ld128(a_col[ks][1] + r);
-      return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-    };
-    i32x8 bf[2][FN], a[2];
-    bf[0][0] = read_b(0, 0);
-    a[0] = read_a(0, 0);
-#pragma unroll
-    for (int nf = 1; nf < FN; ++nf) bf[0][nf] = read_b(0, nf);
-#pragma unroll
-    for (int nf = 0; nf < FN; ++nf) bf[1][nf] = read_b(1, nf);
-    a[1] = read_a(0, 1);
 #pragma unroll
     for (int mf = 0; mf < FM; ++mf) {
-      f32x16 p[FN];
 #pragma unroll
-      for (int nf = 0; nf < FN; ++nf) p[nf] = mfma32_fp8(bf[0][nf], a[0], f32x16{});
-      if (mf + 1 < FM) a[0] = read_a(mf + 1, 0);
+      for (int nf = 0; nf < FN; ++nf) {
+        p[nf] = mfma32_fp8(bf0[nf], a0, f32x16{});
+        __builtin_amdgcn_sched_barrier(0);
+        if (nf == 0) {
+          if (mf == 0) {
+            bf1[0] = read_b(so1, 0);
+            a1 = read_a(so1, 0);
+          } else if (FN > 1) {
+            promote(FN - 1, mf - 1);  // the previous row block's last partial, in this MFMA's shadow
+          }
+        }
+        if (nf == FN - 1) {
+          if (mf == 0) {
 #pragma unroll
-      for (int nf = 0; nf < FN; ++nf) p[nf] = mfma32_fp8(bf[1][nf], a[1], p[nf]);
-      if (mf + 1 < FM) a[1] = read_a(mf + 1, 1);
+            for (int n2 = 1; n2 < FN; ++n2) bf1[n2] = read_b(so1, n2);
+          }
+          if (mf + 1 < FM) a0 = read_a(so0, mf + 1);
+          dma_share(mf);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-      for (int nf = 0; nf < FN; ++nf) acc[nf][mf] += s_m[mf] * p[nf];
+      for (int nf = 0; nf < FN; ++nf) {
+        p[nf] = mfma32_fp8(bf1[nf], a1, p[nf]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (mf + 1 < FM) a1 = read_a(so1, mf + 1);
+      // every partial but the last is promoted in the shadow of the
+      // MFMAs still running; the last one at the next row block's first
+      if constexpr (FN == 1) {
+        promote(0, mf);
+      } else {
+#pragma unroll
+        for (int nf = 0; nf + 1 < FN; ++nf) promote(nf, mf);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-  };
-
-  load_scales(0);
-  issue(0, 0);
-  for (int kb = 0; kb < kblocks; kb += 2) {
-    tile(kb, std::integral_constant<int, 0>{});
-    if (kb + 1 < kblocks) tile(kb + 1, std::integral_constant<int, 1>{});
+    if constexpr (FN > 1) promote(FN - 1, FM - 1);
+    s0 = s0 >= NS - 2 ? s0 - (NS - 2) : s0 + 2;
   }
+  wait_scales<0>(sa_n, sb_n);  // no DMA may land in LDS after the workgroup ends
 
   // ---- store C: lane holds m = m0 + am + 32 mf, n = n0 + wn*TN + 32 nf + 8 i + 4 (l/32) + j ----
 #pragma unroll
@@ -280,7 +359,7 @@ static int launch(const void* A, const float* sA, const void* B, const float* sB
   using CF = Cfg<BM, BN>;
   const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
-  const size_t smem = 2 * CF::STAGE;
+  const size_t smem = CF::LDS;
   constexpr auto kern = gemm_fp8_bs_kernel<BM, BN>;
   MX_RETURN_IF_HIP(lds_limit_once<kern>((int)smem));
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NT), smem, stream, (const uint8_t*)A, sA, (const uint8_t*)B,

@@ -226,6 +226,7 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
     }
   };
   if (rep > 0) __syncthreads();  // every wave is done with the previous block's ring
+  land_args(O);  // O is used only after the tile loop
   issue(0);
   wait_vmcnt<0>();  // the Q loads and stage 0 complete together
 #pragma unroll

@@ -204,6 +204,7 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 #pragma unroll
     for (int n = 0; n < LPW; ++n) issue_p(i, n);
   };
+  land_args(O, ws_o, ws_ml);  // used only after the stage loop
   // Ring prologue.
   issue(0);
   if (nblk > 1) issue(1);

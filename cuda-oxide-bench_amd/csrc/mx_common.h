@@ -276,6 +276,20 @@ __device__ __forceinline__ void interleave_mfma_ds() {
   }
 }
 
+// Make the kernel-argument loads of `xs` complete here.  Arguments used
+// only after a kernel's main loop (an output pointer) are otherwise loaded
+// before the loop and left pending; the compiler then treats the lgkm
+// counter as unordered at the loop head (scalar loads return out of order)
+// and waits for every outstanding LDS read there (lgkmcnt(0)).
+template <typename T>
+__device__ __forceinline__ void land_arg(const T& x) {
+  asm volatile("" ::"s"(x));
+}
+template <typename... Ts>
+__device__ __forceinline__ void land_args(const Ts&... xs) {
+  (land_arg(xs), ...);
+}
+
 // 32-bit LDS byte address of a pointer into __shared__ memory.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) unsigned char*)p);

@@ -51,6 +51,21 @@ def test_parity_vs_oracle(ops, mnk):
     assert err <= TOL, f"normwise rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("mnk", [(4096, 4096, 128), (4096, 4096, 384), (4000, 4352, 640), (4096, 4112, 256)])
+def test_large_tile_path(ops, mnk):
+    """Shapes on the 256x256 kernel (>= 256 such tiles): one scale block
+    (fewer stages than the ring holds), an odd block count, ragged M and N
+    (N = 4352 and 4112: a partial last column tile, and a last 128-column
+    scale block only 16 wide)."""
+    m, n, k = mnk
+    announce(f"fp8 256-tile {m}x{n}x{k}")
+    a8, sa, b8, sb = inputs.fp8_gemm_inputs(shapes.FP8GemmShape("t", m, n, k))
+    c = run(ops, a8, sa, b8, sb)
+    ref = ofp8.gemm_fp8_bs_ref_torch(a8, sa, b8, sb)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+
+
 def test_bit_exact_kat(ops):
     """Operands that are multiples of 1/16 in [0, 0.9375] with unit scales: the
     fp32 sums are exact, so the bf16 output equals the bf16 rounding of the
