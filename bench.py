@@ -14,7 +14,9 @@ Every other BASELINE config is measured the same way and reported under
   mla_decode       MLA absorbed decode B32 H128 T4096 576/512
   gdn_decode       GDN decode B64 Hk16 Hv32 d128
 and the widened rows (absorbed MLA step, KDA decode, fp8 activation
-quantiser, MLA prefill) without a CPU leg.
+quantiser, MLA prefill) without a CPU leg, plus hipblaslt_8192: the
+vendor library's bf16 and per-tensor fp8 GEMMs at 8192^3 on the same GPU,
+a labelled reference line.
 
 Timing: W untimed warm-up launches, then exactly K launches between
 torch.cuda.synchronize() calls with one HIP event pair on the launching
@@ -288,6 +290,34 @@ def case_gemm_fp8_8192(c: Ctx) -> dict:
     return rec
 
 
+def case_hipblaslt_8192(c: Ctx) -> dict:
+    """The vendor library beside this repo's GEMMs, same box and run: torch.matmul
+    (hipBLASLt) on the bf16 8192^3 inputs of gemm_bf16_8192, and
+    torch._scaled_mm (hipBLASLt fp8, one per-tensor scale each, column-major
+    B) at 8192^3.  A reference line, not this repository's kernels: the
+    library has no 1x128/128x128 block-scaled fp8 GEMM to compare against."""
+    import torch
+
+    shape = c.S.GEMM_TARGET
+    a, b = c.I.gemm_inputs(shape)
+    ad, bd = a.cuda(), b.cuda()
+    out = torch.empty((shape.m, shape.n), dtype=torch.bfloat16, device="cuda")
+    ms_bf16, _ = time_graph(lambda: torch.matmul(ad, bd, out=out), c.steps, c.warmup)
+    del ad, bd
+    g = torch.Generator().manual_seed(c.I.SEED)
+    a8 = torch.randn((shape.m, shape.k), generator=g).to(torch.float8_e4m3fn).cuda()
+    b8 = torch.randn((shape.n, shape.k), generator=g).to(torch.float8_e4m3fn).cuda().t()  # column-major [K, N]
+    one = torch.ones((), dtype=torch.float32, device="cuda")
+    ms_fp8, _ = time_graph(lambda: torch._scaled_mm(a8, b8, scale_a=one, scale_b=one, out_dtype=torch.bfloat16),
+                           c.steps, c.warmup)
+    fl = c.F.gemm_flops(shape)
+    return {"workload": "hipBLASLt reference: bf16 torch.matmul and fp8 per-tensor torch._scaled_mm, 8192^3",
+            "unit": "TFLOPS", "mean_ms": ms_bf16, "wall_ms": ms_bf16, "value": c.F.tflops(fl, ms_bf16),
+            "bf16_tflops": c.F.tflops(fl, ms_bf16), "fp8_per_tensor_tflops": c.F.tflops(fl, ms_fp8),
+            "fp8_per_tensor_mean_ms": ms_fp8,
+            "note": "vendor library on the same GPU for comparison; not part of this repository's path"}
+
+
 def case_mla_decode(c: Ctx) -> dict:
     import torch
 
@@ -418,6 +448,7 @@ CASES = {
     "kda_decode": case_kda_decode,
     "quant_fp8_act": case_quant_fp8_act,
     "mla_prefill": case_mla_prefill,
+    "hipblaslt_8192": case_hipblaslt_8192,
 }
 # the BASELINE.json configs, which carry a roofline block and a CPU leg
 BASELINE_CASES = ("gqa", "gemm_bf16_1024", "gemm_bf16_8192", "gemm_fp8_8192", "mla_decode", "gdn_decode")

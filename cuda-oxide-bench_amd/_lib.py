@@ -42,8 +42,10 @@ SIGNATURES: dict[str, tuple] = {
     "mx_mla_decode": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "mx_mla_prefill_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _i, _vp]),
     "mx_mla_decode_workspace": (_sz, [_i, _i, _i, _i]),
+    "mx_mla_decode_splits": (_i, [_i, _i, _i]),
     "mx_mla_decode_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "mx_gdn_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "mx_gdn_decode_block_v": (_i, [_i, _i, _i, _i]),
     "mx_kda_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "mx_quant_fp8_act": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "mx_gemm_bf16_batched": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _ll, _ll, _ll, _vp]),

@@ -12,6 +12,11 @@ the reference columns (impl,kernel,batch,n_heads,d_k,d_v,block_v,iter,
 gpu_us,gbps,tflops) plus n_k_heads,dtype,frac_hbm at the end.  The
 registry adds qwen3_next_b64 (B64, Hk16, Hv32, d128, bf16, exp(-softplus)
 / sigmoid gates), the configuration this path is measured on.
+--sweep times the reference sweep's shapes (qwen3_next_decode, tiny, small,
+large, wide; only --shape's when --shape is given) with --warmup/--iters
+(2/50) and writes results_sweep.csv (or --sweep-csv) with the columns of
+cuda-attn-gdn-tma/bench_sweep.cu:314-315 (impl,kernel,shape,batch,n_heads,
+d_k,d_v,block_v,n_blocks,iter,gpu_ms,gbps,gflops).
 """
 from __future__ import annotations
 
@@ -70,7 +75,7 @@ def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness") -> bo
     return ok_o and ok_s
 
 
-def run_bench(shape, csv_path: str) -> None:
+def run_bench(shape, csv_path: str, iters: int = ITERS) -> None:
     import torch
 
     pkg = H.package()
@@ -87,13 +92,14 @@ def run_bench(shape, csv_path: str) -> None:
     nb, fl = F.gdn_decode_bytes(shape), F.gdn_decode_flops(shape)
     print(f"[bench] flops/iter = {fl / 1e6:.3f} MFLOPS   bytes/iter = {nb / 1024:.1f} KB")
     ms = H.time_iters(lambda: ops.gdn_decode(x["q"], x["k"], x["v"], x["alpha"], x["beta"], x["S_in"],
-                                             S_out=so, o=o), WARMUP, ITERS)
+                                             S_out=so, o=o), WARMUP, iters)
+    bv = ops.gdn_block_v(shape.batch, shape.n_heads, shape.d_k, shape.d_v)
     dname = "bf16" if dt == torch.bfloat16 else "f16"
     rows = []
     for i, m in enumerate(ms):
-        if i < 3 or i == ITERS - 1:
+        if i < 3 or i == iters - 1:
             print(f"[bench] iter={i:2d} gpu_us={m * 1e3:.2f} gbps={F.gbps(nb, m):.1f} tflops={F.tflops(fl, m):.3f}")
-        rows.append(["hip", "gdn_decode_fused", shape.batch, shape.n_heads, shape.d_k, shape.d_v, shape.d_v, i,
+        rows.append(["hip", "gdn_decode_fused", shape.batch, shape.n_heads, shape.d_k, shape.d_v, bv, i,
                      f"{m * 1e3:.3f}", f"{F.gbps(nb, m):.3f}", f"{F.tflops(fl, m):.6f}", shape.hk, dname,
                      f"{F.gbps(nb, m) / F.PEAK_HBM_GBPS:.5f}"])
     H.write_csv(csv_path, ["impl", "kernel", "batch", "n_heads", "d_k", "d_v", "block_v", "iter", "gpu_us", "gbps",
@@ -106,6 +112,48 @@ def run_bench(shape, csv_path: str) -> None:
                                "frac_hbm_peak_median": F.gbps(nb, st["median_ms"]) / F.PEAK_HBM_GBPS})
 
 
+SWEEP_HEADER = ["impl", "kernel", "shape", "batch", "n_heads", "d_k", "d_v", "block_v", "n_blocks", "iter",
+                "gpu_ms", "gbps", "gflops"]
+
+
+def run_sweep(names, csv_path: str, warmup: int, iters: int) -> None:
+    """The reference sweep (cuda-attn-gdn-tma/bench_sweep.cu:302-380): every
+    shape on its reference-distribution f16 inputs, one CSV row per (shape,
+    iteration), then a best-of summary table."""
+    import torch
+
+    pkg = H.package()
+    ops = pkg.load_ops()
+    F = pkg.flops
+    reg = pkg.shapes.GDN_REGISTRY
+    rows, summary = [], []
+    for name in names:
+        shape = reg[name]
+        x = {n: t.cuda() for n, t in pkg.inputs.gdn_inputs(shape, dtype=torch.float16, dist="reference").items()}
+        so = torch.empty_like(x["S_in"])
+        o = torch.empty((shape.batch, shape.n_heads, shape.d_v), dtype=torch.float16, device="cuda")
+        bv = ops.gdn_block_v(shape.batch, shape.n_heads, shape.d_k, shape.d_v)
+        nblk = shape.batch * shape.n_heads * (shape.d_v // bv)
+        print(f"[sweep] ===== shape={name} B={shape.batch} H={shape.n_heads} d_k={shape.d_k} d_v={shape.d_v}  "
+              f"BV={bv}  n_blocks={nblk} =====")
+        ms = H.time_iters(lambda: ops.gdn_decode(x["q"], x["k"], x["v"], x["alpha"], x["beta"], x["S_in"],
+                                                 S_out=so, o=o), warmup, iters)
+        nb, fl = F.gdn_decode_bytes(shape), F.gdn_decode_flops(shape)
+        for i, m in enumerate(ms):
+            rows.append(["hip", "gdn_decode_fused", name, shape.batch, shape.n_heads, shape.d_k, shape.d_v, bv, nblk, i,
+                         f"{m:.6f}", f"{F.gbps(nb, m):.3f}", f"{fl / (m * 1e-3) / 1e9:.3f}"])
+        best = min(ms)
+        summary.append((name, shape, nblk, best * 1e3, F.gbps(nb, best), fl / (best * 1e-3) / 1e9))
+        del x, so, o
+    H.write_csv(csv_path, SWEEP_HEADER, rows)
+    print()
+    print(f"{'shape':20s} {'(B,H,d_k,d_v)':22s} {'n_blocks':9s} {'best_us':9s} {'best_gbps':9s} {'best_gf':7s}")
+    for name, sh, nblk, us, gb, gf in summary:
+        shp = f"({sh.batch},{sh.n_heads},{sh.d_k},{sh.d_v})"
+        print(f"{name:20s} {shp:22s} {nblk:<9d} {us:<9.2f} {gb:<9.1f} {gf:<7.2f}")
+    print(f"[sweep] CSV: {csv_path}  (one row per (shape, iter))")
+
+
 def main() -> int:
     pkg = H.package()
     reg = pkg.shapes.GDN_REGISTRY
@@ -115,12 +163,17 @@ def main() -> int:
     ap.add_argument("--export-cubin", action="store_true", default=False)
     ap.add_argument("--csv-out", default="results.csv")
     ap.add_argument("--cubin-out", default="gdn_decode_fused.cubin")
-    ap.add_argument("--shape", default="qwen3_next_decode", choices=sorted(reg.keys()))
+    ap.add_argument("--shape", default=None, choices=sorted(reg.keys()),
+                    help="bench shape (default qwen3_next_decode); with --sweep, only this shape")
+    ap.add_argument("--sweep", action="store_true", default=False)
+    ap.add_argument("--sweep-csv", default="results_sweep.csv")
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--iters", type=int, default=50)
     ap.add_argument("--inputs-dir", default=None,
                     help="replay a fixture set written in the reference's inputs/ layout")
     ap.add_argument("--fixture", default="correctness", help="fixture shape name (gdn_<fixture>_*.npy)")
     args = ap.parse_args()
-    if not (args.smoke or args.bench or args.export_cubin):
+    if not (args.smoke or args.bench or args.export_cubin or args.sweep):
         args.smoke = True
     H.banner()
     print()
@@ -130,7 +183,11 @@ def main() -> int:
             rc = H.EXIT_SMOKE_FAIL
         print()
     if args.bench:
-        run_bench(reg[args.shape], args.csv_out)
+        run_bench(reg[args.shape or "qwen3_next_decode"], args.csv_out, args.iters)
+        print()
+    if args.sweep:
+        run_sweep([args.shape] if args.shape else list(pkg.shapes.GDN_SWEEP), args.sweep_csv, args.warmup,
+                  args.iters)
         print()
     if args.export_cubin:
         lib = importlib.import_module("cuda-oxide-bench_amd._lib")

@@ -15,6 +15,16 @@ configuration this path is measured on: --shape baseline (S4096, causal,
 bf16, N(0,1) inputs), --causal, --dtype.  TFLOPS uses the reference's
 convention (4*B*Hq*S^2*D, flops.py:31-47); tflops_causal the causal
 algorithmic count 2*B*Hq*D*S*(S+1).
+
+Tile overrides keep the reference's pick_blocks semantics
+(cutile-attn-gqa/main.py:202-230): --block-m (default 64) and --block-n
+(default: --block-m) must divide the sequence, checked by assertion, and
+must name the tile the gfx950 kernel runs for the shape — BLOCK_N = 64 keys
+per LDS stage and BLOCK_M = 256/hpw queries of a head per workgroup, where
+the workgroup's 8 waves of 32 queries cover hpw = 4, 2 or 1 heads of a KV
+group (G % 4 == 0, G % 2 == 0, else): 64 at the bench shape's G = 4, 128 at
+the correctness shape's G = 2.  Any other pair fails the same way the
+reference's assertion does.  The tile in use is what results.csv reports.
 """
 from __future__ import annotations
 
@@ -29,10 +39,39 @@ H = importlib.import_module("cuda-oxide-bench_amd.harness")
 
 WARMUP = 2
 ITERS = 10
-BLOCK_M, BLOCK_N = 32, 64   # queries per wave tile, keys per LDS tile (fixed in the kernel)
+BLOCK_N = 64  # keys per LDS stage
 
 
-def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness") -> bool:
+def kernel_tile(n_q: int, n_kv: int) -> tuple[int, int]:
+    """(BLOCK_M, BLOCK_N) the kernel runs: 8 waves of 32 queries cover hpw
+    heads of a KV group, so a workgroup holds 256/hpw queries of each head."""
+    g = n_q // n_kv
+    hpw = 4 if g % 4 == 0 else (2 if g % 2 == 0 else 1)
+    return 256 // hpw, BLOCK_N
+
+
+def pick_blocks(seq: int, n_q: int, n_kv: int, block_m_override: int | None = None,
+                block_n_override: int | None = None):
+    """(BLOCK_M, BLOCK_N) for a sequence length, with the reference's override
+    semantics (cutile-attn-gqa/main.py:202-230): an override defaults the
+    other side (BLOCK_N to BLOCK_M, BLOCK_M to 64) and must divide seq.
+    Without overrides the kernel's own tile runs at any seq (ragged tiles
+    are masked)."""
+    tile = kernel_tile(n_q, n_kv)
+    if block_m_override is not None or block_n_override is not None:
+        bm = block_m_override if block_m_override is not None else 64
+        bn = block_n_override if block_n_override is not None else bm
+        assert seq % bm == 0, f"BLOCK_M={bm} does not divide seq={seq}"
+        assert seq % bn == 0, f"BLOCK_N={bn} does not divide seq={seq}"
+        assert (bm, bn) == tile, (
+            f"BLOCK_M={bm} BLOCK_N={bn} is not the gfx950 kernel's tile for n_q={n_q} n_kv={n_kv}: "
+            f"{tile} (BLOCK_M queries of a head per workgroup, BLOCK_N keys per LDS stage)")
+        return bm, bn
+    return tile
+
+
+def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness", block_m: int | None = None,
+              block_n: int | None = None) -> bool:
     """The correctness check: the committed golden set, or with inputs_dir a
     fixture set in the reference's inputs/ layout (gqa_<fixture>_*.npy,
     f16 inputs, f32 expected output; cutile-attn-gqa/main.py:177-183)."""
@@ -53,6 +92,8 @@ def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness") -> bo
         g = H.load_golden("gqa_correctness_f16")
         q, k, v = (H.from_bits(g[x], torch.float16).cuda() for x in "qkv")
         expected = g["o"]
+    bm, bn = pick_blocks(q.shape[2], q.shape[1], k.shape[1], block_m, block_n)
+    print(f"[smoke] BLOCK_M={bm} BLOCK_N={bn}")
     o = ops.gqa_fwd(q, k, v, causal=False)
     torch.cuda.synchronize()
     o32 = o.float().cpu().numpy()
@@ -68,7 +109,8 @@ def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness") -> bo
     return ok
 
 
-def run_bench(shape, dtype, dist, csv_path: str, iters: int) -> None:
+def run_bench(shape, dtype, dist, csv_path: str, iters: int, block_m: int | None = None,
+              block_n: int | None = None) -> None:
     import torch
 
     pkg = H.package()
@@ -76,6 +118,8 @@ def run_bench(shape, dtype, dist, csv_path: str, iters: int) -> None:
     F = pkg.flops
     print(f"[bench] shape={shape.name} B={shape.batch} S={shape.seq} n_q={shape.n_q} n_kv={shape.n_kv} "
           f"d={shape.d_head} causal={shape.causal} dtype={dtype}")
+    bm, bn = pick_blocks(shape.seq, shape.n_q, shape.n_kv, block_m, block_n)
+    print(f"[bench] BLOCK_M={bm} BLOCK_N={bn}")
     q, k, v = (t.cuda() for t in pkg.inputs.gqa_inputs(shape, dtype=dtype, dist=dist))
     out = torch.empty_like(q)
     ms = H.time_iters(lambda: ops.gqa_fwd(q, k, v, causal=shape.causal, out=out), WARMUP, iters)
@@ -85,8 +129,8 @@ def run_bench(shape, dtype, dist, csv_path: str, iters: int) -> None:
     rows = []
     for i, m in enumerate(ms):
         print(f"[bench] iter={i} gpu_ms={m:.3f} tflops={F.tflops(conv, m):.3f}")
-        rows.append(["hip", "gqa_fwd_fused", shape.batch, shape.seq, shape.n_q, shape.n_kv, shape.d_head, BLOCK_M,
-                     BLOCK_N, i, f"{m:.6f}", f"{F.tflops(conv, m):.6f}", int(shape.causal), dname,
+        rows.append(["hip", "gqa_fwd_fused", shape.batch, shape.seq, shape.n_q, shape.n_kv, shape.d_head, bm,
+                     bn, i, f"{m:.6f}", f"{F.tflops(conv, m):.6f}", int(shape.causal), dname,
                      f"{F.tflops(alg, m):.6f}"])
     H.write_csv(csv_path, ["impl", "kernel", "batch", "seq", "n_q", "n_kv", "d_head", "block_m", "block_n", "iter",
                            "gpu_ms", "tflops", "causal", "dtype", "tflops_causal"], rows)
@@ -127,12 +171,11 @@ def main() -> int:
 
     H.banner()
     if args.block_m is not None or args.block_n is not None:
-        print(f"[tile] requested BLOCK_M={args.block_m} BLOCK_N={args.block_n}; the gfx950 kernel uses "
-              f"{BLOCK_M} queries per wave x {BLOCK_N} keys per LDS tile")
+        print(f"[tile] override: BLOCK_M={args.block_m} BLOCK_N={args.block_n}")
     print()
     rc = H.EXIT_OK
     if args.smoke:
-        if not run_smoke(args.inputs_dir, args.fixture):
+        if not run_smoke(args.inputs_dir, args.fixture, args.block_m, args.block_n):
             rc = H.EXIT_SMOKE_FAIL
         print()
     if args.bench:
@@ -145,7 +188,8 @@ def main() -> int:
             shape = dataclasses.replace(shape, causal=True)
         if args.dtype is not None:
             dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
-        run_bench(shape, dtype, dist, args.csv_out, args.iters if args.iters is not None else ITERS)
+        run_bench(shape, dtype, dist, args.csv_out, args.iters if args.iters is not None else ITERS, args.block_m,
+                  args.block_n)
         print()
     if args.export_cubin:
         lib = importlib.import_module("cuda-oxide-bench_amd._lib")

@@ -63,7 +63,7 @@ def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness") -> bo
     return ok
 
 
-def run_bench(shape, csv_path: str) -> None:
+def run_bench(shape, csv_path: str, iters: int = ITERS) -> None:
     import torch
 
     pkg = H.package()
@@ -77,12 +77,13 @@ def run_bench(shape, csv_path: str) -> None:
     nb, fl = F.kda_decode_bytes(shape), F.kda_decode_flops(shape)
     print(f"[bench] flops/iter = {fl / 1e6:.3f} MFLOPS   bytes/iter = {nb / 1024:.1f} KB")
     ms = H.time_iters(lambda: ops.kda_decode(x["q"], x["k"], x["v"], x["g"], x["beta"], x["S_in"],
-                                             S_out=so, o=o), WARMUP, ITERS)
+                                             S_out=so, o=o), WARMUP, iters)
+    bv = ops.gdn_block_v(shape.batch, shape.n_heads, shape.d_k, shape.d_v)
     rows = []
     for i, m in enumerate(ms):
-        if i < 3 or i == ITERS - 1:
+        if i < 3 or i == iters - 1:
             print(f"[bench] iter={i:2d} gpu_us={m * 1e3:.2f} gbps={F.gbps(nb, m):.1f} tflops={F.tflops(fl, m):.3f}")
-        rows.append(["hip", "kda_decode_fused", shape.batch, shape.n_heads, shape.d_k, shape.d_v, shape.d_v, i,
+        rows.append(["hip", "kda_decode_fused", shape.batch, shape.n_heads, shape.d_k, shape.d_v, bv, i,
                      f"{m * 1e3:.3f}", f"{F.gbps(nb, m):.3f}", f"{F.tflops(fl, m):.6f}", "f16",
                      f"{F.gbps(nb, m) / F.PEAK_HBM_GBPS:.5f}"])
     H.write_csv(csv_path, ["impl", "kernel", "batch", "n_heads", "d_k", "d_v", "block_v", "iter", "gpu_us", "gbps",
@@ -105,6 +106,7 @@ def main() -> int:
     ap.add_argument("--csv-out", default="results.csv")
     ap.add_argument("--cubin-out", default="kda_decode_fused.cubin")
     ap.add_argument("--shape", default="kimi_linear_decode", choices=sorted(reg.keys()))
+    ap.add_argument("--iters", type=int, default=ITERS, help="timed launches (default 50)")
     ap.add_argument("--inputs-dir", default=None,
                     help="replay a fixture set written in the reference's inputs/ layout")
     ap.add_argument("--fixture", default="correctness", help="fixture shape name (kda_<fixture>_*.npy)")
@@ -119,7 +121,7 @@ def main() -> int:
             rc = H.EXIT_SMOKE_FAIL
         print()
     if args.bench:
-        run_bench(reg[args.shape], args.csv_out)
+        run_bench(reg[args.shape], args.csv_out, args.iters)
         print()
     if args.export_cubin:
         lib = importlib.import_module("cuda-oxide-bench_amd._lib")

@@ -72,7 +72,7 @@ def run_bench(csv_path: str, iters: int) -> None:
     out = torch.empty((s.batch, s.n_h, s.d_latent), dtype=torch.bfloat16, device="cuda")
     ws_bytes = ops.mla_decode_workspace_bytes(s.batch, s.n_h, s.ctx)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
-    n_split = ws_bytes // (s.batch * s.n_h * (s.d_latent + 2) * 4) if ws_bytes else 1
+    n_split = ops.mla_decode_splits(s.batch, s.n_h, s.ctx)
     ms = H.time_iters(lambda: ops.mla_decode(q, kv, s.scale, out=out, workspace=ws), WARMUP, iters)
     fl, nb = F.mla_decode_flops(s), F.mla_decode_bytes(s)
     rows = []

@@ -87,7 +87,7 @@ def run_correctness(n: int, dist: str):
     return n_fail == 0 and exact is not False, float(abs_err.max()), float(rel_err.max()), n_fail, exact
 
 
-def run_bench(n: int, dist: str, csv_path: str) -> dict:
+def run_bench(n: int, dist: str, csv_path: str, iters: int = ITERS) -> dict:
     import torch
 
     pkg = H.package()
@@ -95,7 +95,7 @@ def run_bench(n: int, dist: str, csv_path: str) -> dict:
     a8, sa, b8, sb = (t.cuda() for t in make_inputs(n, dist))
     out = torch.empty((n, n), dtype=torch.bfloat16, device="cuda")
     flops = 2.0 * n ** 3
-    ms = H.time_iters(lambda: ops.gemm_fp8_bs(a8, sa, b8, sb, out=out), WARMUP, ITERS)
+    ms = H.time_iters(lambda: ops.gemm_fp8_bs(a8, sa, b8, sb, out=out), WARMUP, iters)
     rows = [["hip", "matmul_fp8_bs", n, i, f"{m:.6f}", f"{flops / 1e12 / (m / 1e3):.6f}"] for i, m in enumerate(ms)]
     H.write_csv(csv_path, ["impl", "kernel", "n", "iter", "gpu_ms", "tflops"], rows)
     st = H.summarize_ms(ms)
@@ -118,6 +118,7 @@ def main() -> int:
     ap.add_argument("--n", type=int, default=None)
     ap.add_argument("--csv-out", default="results.csv")
     ap.add_argument("--dist", choices=["baseline", "kat"], default="baseline")
+    ap.add_argument("--iters", type=int, default=ITERS, help="timed launches")
     args = ap.parse_args()
     if not args.smoke and not args.bench:
         args.bench = True
@@ -127,7 +128,7 @@ def main() -> int:
         return H.EXIT_CORRECTNESS_FAIL
 
     H.banner()
-    print(f"kernel: mx_gemm_fp8_bs (16x16x128 f8f6f4 MFMA, per-128-K scale promotion)  N={n}")
+    print(f"kernel: mx_gemm_fp8_bs (32x32x64 f8f6f4 MFMA, per-128-K scale promotion)  N={n}")
     print()
     print(f"=== correctness ({NUM_SAMPLES} hashed cells, N={n}, dist={args.dist}) ===")
     ok, mae, mre, n_fail, exact = run_correctness(n, args.dist)
@@ -140,7 +141,7 @@ def main() -> int:
     if args.smoke and not args.bench:
         return H.EXIT_OK
     print()
-    run_bench(n, args.dist, args.csv_out)
+    run_bench(n, args.dist, args.csv_out, args.iters)
     return H.EXIT_OK
 
 

@@ -65,7 +65,7 @@ def run_correctness(n: int, dist: str):
     return n_fail == 0, float(abs_err.max()), float(rel_err.max()), n_fail
 
 
-def run_bench(sizes: list[int], dist: str, csv_path: str) -> dict:
+def run_bench(sizes: list[int], dist: str, csv_path: str, iters: int = ITERS) -> dict:
     import torch
 
     pkg = H.package()
@@ -76,7 +76,7 @@ def run_bench(sizes: list[int], dist: str, csv_path: str) -> dict:
         out = torch.empty((n, n), dtype=torch.bfloat16, device="cuda")
         flops = 2.0 * n ** 3
         t0 = time.perf_counter()
-        ms = H.time_iters(lambda: ops.gemm_bf16(a, b, out=out), WARMUP, ITERS)
+        ms = H.time_iters(lambda: ops.gemm_bf16(a, b, out=out), WARMUP, iters)
         wall = time.perf_counter() - t0
         for i, m in enumerate(ms):
             rows.append(["hip", "matmul_tc_bf16", n, i, f"{m:.6f}", f"{flops / 1e12 / (m / 1e3):.6f}"])
@@ -84,7 +84,7 @@ def run_bench(sizes: list[int], dist: str, csv_path: str) -> dict:
         tf_best = flops / 1e12 / (st["best_ms"] / 1e3)
         tf_med = flops / 1e12 / (st["median_ms"] / 1e3)
         H.print_summary(f"bf16 GEMM N={n}", st, tf_best, tf_med, "TFLOPS", pkg.flops.PEAK_BF16_TFLOPS)
-        print(f"  CPU wall: {wall:.3f} s for {WARMUP + ITERS} dispatches")
+        print(f"  CPU wall: {wall:.3f} s for {WARMUP + iters} timed and warm-up samples")
         summaries[str(n)] = {**st, "tflops_best": tf_best, "tflops_median": tf_med,
                              "frac_mfma_peak_median": tf_med / pkg.flops.PEAK_BF16_TFLOPS}
         del a, b, out
@@ -102,13 +102,14 @@ def main() -> int:
     ap.add_argument("--csv-out", default="results.csv")
     ap.add_argument("--dist", choices=["reference", "baseline"], default="reference")
     ap.add_argument("--sweep", action="store_true", help="bench N in 1024, 2048, 4096, 8192")
+    ap.add_argument("--iters", type=int, default=ITERS, help="timed launches (default 50)")
     args = ap.parse_args()
     if not args.smoke and not args.bench:
         args.bench = True
     n = args.n if args.n is not None else (512 if args.smoke and not args.bench else N)
 
     H.banner()
-    print(f"kernel: mx_gemm_bf16 (32x32x16 bf16 MFMA, BK=64)  N={n}  ITERS={ITERS}")
+    print(f"kernel: mx_gemm_bf16 (32x32x16 bf16 MFMA)  N={n}  ITERS={args.iters}")
     print()
     print(f"=== correctness (sampled, N={n}) ===")
     ok, mae, mre, n_fail = run_correctness(n, args.dist)
@@ -120,7 +121,7 @@ def main() -> int:
     if args.smoke and not args.bench:
         return H.EXIT_OK
     print()
-    run_bench(SWEEP if args.sweep else [n], args.dist, args.csv_out)
+    run_bench(SWEEP if args.sweep else [n], args.dist, args.csv_out, args.iters)
     return H.EXIT_OK
 
 

@@ -24,7 +24,7 @@
 //    column of S is independent, so the d_v split needs no cross-workgroup
 //    reduction (the reference tiles d_v the same way, main.py:228-246).  BV
 //    is chosen at launch so that small batches still spread over the CUs;
-//  * NT = d_k*BV/64 threads so every thread keeps exactly 16 rows x 4
+//  * NT = d_k*BV/64 threads (<= 1024) so every thread keeps exactly 16 rows x 4
 //    columns (64 fp32) of the state in VGPRs between the read and the
 //    write — S is read once and written once, with 128-bit loads and
 //    non-temporal stores, BV/4 threads covering a row segment;
@@ -171,7 +171,9 @@ static int launch(const void* q, const void* k, const void* v, const Gates& gt, 
   return MX_OK;
 }
 
-// Column-block width.  Start from d_v and halve while the grid has fewer
+// Column-block width.  At most 65536/d_k columns, so a workgroup of
+// d_k*BV/64 threads stays within 1024 (d_k = 512: BV <= 128).  Start from
+// that and halve while the grid has fewer
 // than 4096 workgroups (16 per CU: small workgroups keep the last wave of
 // the grid short) but not below 64 columns (256-byte row segments stream
 // well; 64-byte ones do not: 4.0 vs 6.5 TB/s at B4 H64 d256).  Only when
@@ -183,7 +185,7 @@ static int launch(const void* q, const void* k, const void* v, const Gates& gt, 
 static int pick_bv(int B, int Hv, int dk, int dv) {
   const int min_bv = (4096 / dk > 16) ? 4096 / dk : 16;
   auto groups = [&](int bv) { return (long long)B * Hv * (dv / bv); };
-  int bv = dv;
+  int bv = dv < 65536 / dk ? dv : 65536 / dk;
   while (bv / 2 >= 64 && bv / 2 >= min_bv && groups(bv) < 4096) bv /= 2;
   while (bv / 2 >= min_bv && groups(bv) < 1024) bv /= 2;
   return bv;
@@ -195,7 +197,8 @@ static int dispatch_dk(const void* q, const void* k, const void* v, const Gates&
   const int bv = pick_bv(B, Hv, DK, dv);
 #define MX_GDN_BV(BV_)                                                                                     \
   if (bv == BV_) {                                                                                         \
-    if constexpr (DK * BV_ >= 4096) return launch<DK, BV_, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s); \
+    if constexpr (DK * BV_ >= 4096 && DK * BV_ <= 65536)                                                   \
+      return launch<DK, BV_, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s);                        \
   }
   MX_GDN_BV(16)
   MX_GDN_BV(32)
@@ -212,6 +215,7 @@ static int dispatch(const void* q, const void* k, const void* v, const Gates& gt
   if (dk == 64) return dispatch_dk<64, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s);
   if (dk == 128) return dispatch_dk<128, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s);
   if (dk == 256) return dispatch_dk<256, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s);
+  if (dk == 512) return dispatch_dk<512, T, KDA>(q, k, v, gt, S_in, S_out, o, B, Hk, Hv, dv, s);
   return MX_ERR_UNSUPPORTED;
 }
 
@@ -232,7 +236,12 @@ static int check_state(const float* S_in, const float* S_out, const void* v, con
 }  // namespace gdn
 }  // namespace mx
 
-static bool mx_is_dim(int d) { return d == 64 || d == 128 || d == 256; }
+static bool mx_is_dim(int d) { return d == 64 || d == 128 || d == 256 || d == 512; }
+
+extern "C" int mx_gdn_decode_block_v(int B, int Hv, int dk, int dv) {
+  if (B <= 0 || Hv <= 0 || !mx_is_dim(dk) || !mx_is_dim(dv)) return 0;
+  return mx::gdn::pick_bv(B, Hv, dk, dv);
+}
 
 extern "C" int mx_gdn_decode(const void* q, const void* k, const void* v, const float* alpha, const float* beta,
                              const float* S_in, float* S_out, void* o, int B, int Hk, int Hv, int dk, int dv,

@@ -593,6 +593,11 @@ extern "C" size_t mx_mla_decode_workspace(int B, int H, int T, int d_latent) {
   return mx::mla::workspace_bytes(B, H, T);
 }
 
+extern "C" int mx_mla_decode_splits(int B, int H, int T) {
+  if (B <= 0 || H <= 0 || T <= 0) return 0;
+  return mx::mla::pick_split(B, H, T).nsplit;
+}
+
 extern "C" int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int H, int T, int d_latent, int d_rope,
                              float scale, void* workspace, size_t ws_bytes, void* stream) {
   using namespace mx::mla;

@@ -129,6 +129,11 @@ def mla_decode_workspace_bytes(B: int, H: int, T: int, d_latent: int = 512) -> i
     return int(_lib.load().mx_mla_decode_workspace(B, H, T, d_latent))
 
 
+def mla_decode_splits(B: int, H: int, T: int) -> int:
+    """How many slices of T the decode splits each sequence into (1: no merge)."""
+    return int(_lib.load().mx_mla_decode_splits(B, H, T))
+
+
 def mla_prefill_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
                     scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """Pre-projected MLA prefill attention, every head its own K/V.
@@ -228,6 +233,15 @@ def gdn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, alpha: torch.T
               S_in.data_ptr(), S_out.data_ptr(), o.data_ptr(), B, Hk, Hv, dk, dv, _IO_DTYPES[q.dtype],
               _stream())
     return o, S_out
+
+
+def gdn_block_v(B: int, Hv: int, dk: int, dv: int) -> int:
+    """Width of the d_v column blocks the GDN/KDA kernels use for this
+    problem (the reference's `pick_block_v`, cutile-attn-gdn/main.py:228-246)."""
+    bv = int(_lib.load().mx_gdn_decode_block_v(B, Hv, dk, dv))
+    if bv <= 0:
+        raise ValueError(f"unsupported GDN/KDA sizes B={B} Hv={Hv} dk={dk} dv={dv}")
+    return bv
 
 
 def kda_decode(q, k, v, g, beta, S_in, S_out=None, o=None):

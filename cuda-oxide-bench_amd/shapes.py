@@ -215,7 +215,10 @@ GDN_REGISTRY = {s.name: s for s in (
     GDNShape("tiny", batch=1, n_heads=4, d_k=64, d_v=64),
     GDNShape("small", batch=1, n_heads=8, d_k=128, d_v=128),
     GDNShape("large", batch=4, n_heads=64, d_k=256, d_v=256),
+    GDNShape("wide", batch=1, n_heads=16, d_k=512, d_v=512),
 )}
+# The reference sweep's shapes, in its order (cuda-attn-gdn-tma/bench_sweep.cu:302-309).
+GDN_SWEEP = ("qwen3_next_decode", "tiny", "small", "large", "wide")
 
 # KDA: reference registry (cutile-attn-kda/main.py:77-104).  "large" is the
 # configuration this path is measured on (it fills the GPU).

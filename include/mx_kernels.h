@@ -163,6 +163,12 @@ int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int H, int T, i
  * invalid sizes). */
 size_t mx_mla_decode_workspace(int B, int H, int T, int d_latent);
 
+/* Number of slices T is split into (one workgroup per sequence, slice and
+ * 128-head group; 1 = no merge pass) for this problem, 0 on invalid sizes.
+ * No counterpart in the reference (its kernel does not split T); harnesses
+ * report it next to the timing. */
+int mx_mla_decode_splits(int B, int H, int T);
+
 /*
  * Allocation-free MLA decode: mx_mla_decode without a workspace argument.
  * No counterpart in the reference: it is for callers that cannot allocate
@@ -208,13 +214,22 @@ size_t mx_mla_decode_absorbed_workspace(int B, int H, int T);
  * q, k: [B, Hk, dk]; v, o: [B, Hv, dv] (dtype as given); alpha, beta:
  * [B, Hv] fp32; S_in, S_out: [B, Hv, dk, dv] fp32 with dv contiguous.
  * S_out may equal S_in (in-place update); partial overlap is rejected.
- * dk and dv must be 64, 128 or 256; Hv % Hk == 0.
+ * dk and dv must be 64, 128, 256 or 512; Hv % Hk == 0.
  * Replaces: cutile-attn-gdn/main.py:268-272 (ct.launch of `gdn_decode`,
  * kernel at :92-185), extended with Hk != Hv grouping.
  */
 int mx_gdn_decode(const void* q, const void* k, const void* v, const float* alpha,
                   const float* beta, const float* S_in, float* S_out, void* o, int B, int Hk,
                   int Hv, int dk, int dv, int dtype, void* stream);
+
+/*
+ * Width of the d_v column blocks mx_gdn_decode and mx_kda_decode split
+ * each head into (one workgroup per (b, head, block)); 0 for unsupported
+ * sizes.  For harnesses that report the block (the reference's results.csv
+ * `block_v` column and its sweep's `n_blocks`).
+ * Replaces: cutile-attn-gdn/main.py:228-246 (`pick_block_v`).
+ */
+int mx_gdn_decode_block_v(int B, int Hv, int dk, int dv);
 
 /*
  * Kimi-Delta-Attention (KDA) single-token recurrent decode: GDN with a
@@ -227,7 +242,7 @@ int mx_gdn_decode(const void* q, const void* k, const void* v, const float* alph
  * type `dtype` (the reference's f16 gate and beta); S_in, S_out:
  * [B, H, dk, dv] fp32 with dv contiguous.  q is used as given (no 1/sqrt(dk)
  * inside).  S_out may equal S_in; partial overlap is rejected.  dk and dv
- * must be 64, 128 or 256.
+ * must be 64, 128, 256 or 512.
  * Replaces: cutile-attn-kda/main.py:357-360 (ct.launch of `kda_decode`,
  * kernel at :187-271; bench launches at :428, :438).
  */

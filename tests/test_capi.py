@@ -168,3 +168,17 @@ def test_mla_absorbed_checks_every_launch_before_the_first():
     assert f(P, P, bad, P, P, P, 32, 128, 4096, 128, 128, 0.07, P, need, None) == _lib.MX_ERR_ALIGN  # KV
     # a valid call gets as far as the runtime
     assert f(P, P, P, P, P, P, 32, 128, 4096, 128, 128, 0.07, P, need, None) == _lib.MX_ERR_LAUNCH
+
+
+def test_gdn_block_v_choices():
+    """The column-block widths the GDN/KDA kernels use (no GPU needed): within
+    the workgroup limit (d_k*BV/64 <= 1024 threads), dividing d_v, and the
+    measured choices for the reference and BASELINE shapes."""
+    f = _lib.load().mx_gdn_decode_block_v
+    assert f(64, 32, 128, 128) == 64      # BASELINE B64 Hv32 d128
+    assert f(4, 64, 256, 256) == 64       # reference "large"
+    assert f(1, 16, 256, 256) == 16       # reference qwen3_next_decode
+    for B, H, dk, dv in ((1, 16, 512, 512), (1, 4, 64, 64), (8, 8, 512, 64), (2, 2, 64, 512)):
+        bv = f(B, H, dk, dv)
+        assert bv >= 16 and dv % bv == 0 and dk * bv // 64 <= 1024
+    assert f(1, 16, 96, 128) == 0 and f(0, 16, 128, 128) == 0

@@ -48,7 +48,8 @@ def test_golden(ops, name, dt):
         assert np.abs(s.numpy() - g["S_out"]).max() < 5e-3
 
 
-DIMS = [(64, 64), (64, 128), (128, 64), (128, 128), (128, 256), (256, 128), (256, 256), (64, 256), (256, 64)]
+DIMS = [(64, 64), (64, 128), (128, 64), (128, 128), (128, 256), (256, 128), (256, 256), (64, 256), (256, 64),
+        (512, 512), (512, 64), (64, 512), (512, 256)]
 
 
 @pytest.mark.parametrize("dk,dv", DIMS)
@@ -60,6 +61,22 @@ def test_all_head_dims(ops, dk, dv):
     ro, rs = ogdn.gdn_decode_ref(**x)
     assert normwise_rel_err(o, ro) <= TOL_O
     assert normwise_rel_err(so, rs) <= TOL_S
+
+
+def test_wide_reference_shape(ops):
+    """The reference registry's `wide` shape (B1 H16 d_k = d_v = 512,
+    cutile-attn-gdn/main.py:65) on reference-distribution f16 inputs, with
+    the column blocks the kernel picks reported by mx_gdn_decode_block_v."""
+    announce("gdn wide B1 H16 d512 f16")
+    s = shapes.GDN_REGISTRY["wide"]
+    bv = ops.gdn_block_v(s.batch, s.n_heads, s.d_k, s.d_v)
+    assert 16 <= bv <= 128 and s.d_v % bv == 0
+    x = inputs.gdn_inputs(s, dtype=torch.float16, dist="reference")
+    o, so = run(ops, x)
+    ro, rs = ogdn.gdn_decode_ref(**x)
+    assert normwise_rel_err(o, ro) <= TOL_O
+    assert normwise_rel_err(so, rs) <= TOL_S
+    assert np.abs(so.numpy() - rs.numpy()).max() < 5e-3  # the reference's S gate (main.py:298)
 
 
 def test_baseline_config(ops):

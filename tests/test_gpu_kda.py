@@ -58,7 +58,7 @@ def test_reference_shapes(ops, name):
     check(o, s, ro, rs)
 
 
-DIMS = [(64, 64), (64, 256), (128, 128), (256, 64), (256, 256)]
+DIMS = [(64, 64), (64, 256), (128, 128), (256, 64), (256, 256), (512, 512), (512, 128)]
 
 
 @pytest.mark.parametrize("dk,dv", DIMS)
