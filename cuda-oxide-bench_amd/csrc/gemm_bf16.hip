@@ -47,6 +47,10 @@
 #ifndef MX_BF16_WN
 #define MX_BF16_WN 4
 #endif
+// 1: the 16x16x32-MFMA direct-load kernel (BK fixed at 32), 0: the 32x32x16 one
+#ifndef MX_BF16_MFMA16
+#define MX_BF16_MFMA16 1
+#endif
 
 namespace mx {
 namespace gemm {
@@ -545,6 +549,277 @@ static int launch_dma(const void* A, const void* B, void* C, int M, int N, int K
   return MX_OK;
 }
 
+// ---------------------------------------------------------------------------
+// gemm_bf16_dma16_kernel: the direct-load design above on 16x16x32 MFMAs.
+// Under a sustained full-chip MFMA load the 16x16x32 shape delivers about
+// 11% more bf16 throughput than 32x32x16 on MI355X (same FLOPs, less
+// operand/accumulator traffic per FLOP, so less power at the same clock
+// cap), which is what sets the large-GEMM rate.
+//
+//  * 256x256 tile, BK = 32 (one 16x16x32 k-step per K tile), WM x WN waves,
+//    each owning (256/WM) x (256/WN) of C as 16x16 fragments.
+//  * Operand layouts (16x16x32): the "A" operand holds 8 consecutive k of
+//    row l%16 at k-group l/16; "B" the same for column l%16; D holds rows
+//    4(l/16)..+3 of column l%16.  Issued as D^T = B^T . A^T: B^T fragments
+//    come from the K-major B tile by transposing reads (lane (kg, j, a)
+//    reads k-row 8kg + 4r + j, columns 4a..+3, r = 0, 1), A^T fragments are
+//    one 16-byte read of an A row; each lane's D is four consecutive n of
+//    one row of C (an 8-byte store).
+//  * A rows are 64 B: a 16-lane read phase (one k-group) covers 16 rows,
+//    chunk kg ^ ((m >> 2) & 3) puts them on 16 distinct 16-byte slots.  B
+//    rows are 512 B (same banks every row): a 32-lane phase of transposing
+//    reads covers 8 k-rows (two k-groups x 4) of 32 bytes each, and chunk
+//    c ^ 2((k & 3) | ((k >> 3) & 1) << 2) gives the 8 rows distinct 32-byte
+//    slots.  The DMA applies the same XOR on the global side.
+//  * Ring of NS stages, one barrier per K tile (as above).  Tile kt+1's
+//    fragments are read during step kt: B^T ones into the other half of a
+//    parity double buffer at the step's start, each A^T one in place right
+//    after the four MFMAs that consumed the previous tile's.
+// ---------------------------------------------------------------------------
+template <int NS, int WM, int WN>
+struct D16Cfg {
+  static constexpr int BM = 256, BN = 256, BK = 32;
+  static constexpr int NW = WM * WN, NT = 64 * NW;
+  static constexpr int TM = BM / WM, TN = BN / WN;  // wave block
+  static constexpr int FM = TM / 16, FN = TN / 16;  // 16x16 fragments
+  static constexpr int RA = BK * 2, RB = BN * 2;    // LDS row bytes
+  static constexpr int A_B = BM * RA, B_B = BK * RB;
+  static constexpr int STAGE = A_B + B_B;
+  static constexpr int A_LPW = A_B / 1024 / NW;  // 1 KB loads per wave per stage
+  static constexpr int B_LPW = B_B / 1024 / NW;
+  static constexpr int LPW = A_LPW + B_LPW;
+  static constexpr int A_CH = RA / 16, A_RPL = 1024 / RA;  // chunks per A row, A rows per load
+  static constexpr int B_CH = RB / 16, B_RPL = 1024 / RB;
+  static_assert(NS >= 3 && NS <= 5 && NS * STAGE <= 160 * 1024, "LDS ring");
+  static_assert((NS - 3) * LPW < 64, "vmcnt range");
+  static_assert(A_LPW >= 1 && B_LPW >= 1 && FM >= 1 && FN >= 1, "tile split");
+};
+__device__ __forceinline__ int swz_a16(int m) { return (m >> 2) & 3; }
+// Schedule of one K tile: per row block FN MFMAs, then LDS reads: the 2FN
+// B^T reads spread over the first half of the row blocks, each A^T read
+// right behind its row block.
+template <int FM, int FN, int I = 0>
+__device__ __forceinline__ void interleave_rows16() {
+  if constexpr (I < FM) {
+    constexpr int HB = FM / 2;
+    constexpr int nb = I < HB ? (2 * FN * (I + 1)) / HB - (2 * FN * I) / HB : 0;
+    __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1 + nb, 0);
+    interleave_rows16<FM, FN, I + 1>();
+  }
+}
+__device__ __forceinline__ int swz_b16(int k) { return 2 * ((k & 3) | (((k >> 3) & 1) << 2)); }
+
+template <int NS, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_dma16_kernel(const uint16_t* __restrict__ A,
+                                                                        const uint16_t* __restrict__ B,
+                                                                        uint16_t* __restrict__ C, int M, int N,
+                                                                        int K, int lda, int ldb, int ldc) {
+  using CF = D16Cfg<NS, WM, WN>;
+  constexpr int FM = CF::FM, FN = CF::FN, BK = CF::BK;
+  extern __shared__ __align__(1024) unsigned char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int kg = lane >> 4;  // k-group of the lane's operand and row quad of its result
+
+  // ---- tile -> (tm, tn), grouped for L2 reuse, XCD-aware ----
+  const int tiles_m = (M + CF::BM - 1) / CF::BM, tiles_n = (N + CF::BN - 1) / CF::BN;
+  const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = GROUP_M * tiles_n;
+  const int group = id / per_group;
+  const int first_m = group * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (id % per_group) % gsz;
+  const int tn = (id % per_group) / gsz;
+  const int m0 = tm * CF::BM, n0 = tn * CF::BN;
+  const int nk = K / BK;
+
+  // ---- direct-load lane offsets (bytes from the tile's first element).
+  // Rows past M / columns past N re-read the last valid ones; their
+  // results are never stored. ----
+  const uint32_t lds0 = lds_addr(smem);
+  const bool full_m = m0 + CF::BM <= M, full_n = n0 + CF::BN <= N;
+  uint32_t a_off[CF::A_LPW], b_off[CF::B_LPW];
+#pragma unroll
+  for (int n = 0; n < CF::A_LPW; ++n) {
+    const int row = CF::A_RPL * (wave * CF::A_LPW + n) + lane / CF::A_CH;
+    const int gm = full_m ? m0 + row : min(m0 + row, M - 1);
+    a_off[n] = (uint32_t)(gm - m0) * (uint32_t)lda * 2u + 16u * ((lane % CF::A_CH) ^ swz_a16(row));
+  }
+#pragma unroll
+  for (int n = 0; n < CF::B_LPW; ++n) {
+    const int row = CF::B_RPL * (wave * CF::B_LPW + n) + lane / CF::B_CH;
+    int col = 8 * ((lane % CF::B_CH) ^ swz_b16(row));  // elements
+    if (!full_n) col = min(n0 + col, N - 8) - n0;
+    b_off[n] = (uint32_t)row * (uint32_t)ldb * 2u + 2u * col;
+  }
+  auto issue = [&](int kt, int stage) {
+    const uint32_t st = lds0 + stage * CF::STAGE;
+    const uint16_t* abase = A + (size_t)m0 * lda + (size_t)kt * BK;
+    const uint16_t* bbase = B + (size_t)kt * BK * ldb + n0;
+#pragma unroll
+    for (int n = 0; n < CF::A_LPW; ++n) dma16(abase, a_off[n], st + (wave * CF::A_LPW + n) * 1024);
+#pragma unroll
+    for (int n = 0; n < CF::B_LPW; ++n) dma16(bbase, b_off[n], st + CF::A_B + (wave * CF::B_LPW + n) * 1024);
+  };
+
+  // ---- fragment lane addresses, one base per ring stage (stages lie past
+  // ds_read's 16-bit immediate), fragments at immediates from it ----
+  // A^T (B operand): row am + 16 mf, chunk kg ^ swz(am) (swz is the same
+  // for every mf).
+  const int am = wm * CF::TM + (lane & 15);
+  uint32_t a_col[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    a_col[st] = lds0 + st * CF::STAGE + am * CF::RA + 16 * (kg ^ swz_a16(am));
+    asm volatile("" : "+v"(a_col[st]));  // keep it a base register
+  }
+  // B^T (A operand): lane (kg, j, a) reads k-rows 8kg + 4r + j, columns
+  // wn*TN + 16 nf + 4a .. +3 (8 bytes of a 16-byte chunk).
+  const int b_j = (lane >> 2) & 3, b_a = lane & 3;
+  const int bk = 8 * kg + b_j;  // k-row of the r = 0 read; r = 1 is 4 rows further, same swizzle
+  uint32_t b_col[NS][FN];
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+#pragma unroll
+    for (int nf = 0; nf < FN; ++nf) {
+      const int chunk = (wn * CF::TN + 16 * nf + 4 * b_a) >> 3;
+      b_col[st][nf] = lds0 + st * CF::STAGE + CF::A_B + bk * CF::RB + 16 * (chunk ^ swz_b16(bk)) + 8 * (b_a & 1);
+      asm volatile("" : "+v"(b_col[st][nf]));
+    }
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{};
+
+  u32x4 af[FM];     // A^T fragments of the current tile, refilled in place
+  u32x4 bf[2][FN];  // B^T fragments, double buffered by tile parity
+  auto read_b = [&](int stg, int buf) {
+#pragma unroll
+    for (int nf = 0; nf < FN; ++nf) {
+      const u32x2 lo = lds_read_tr16_at(b_col[stg][nf]);
+      const u32x2 hi = lds_read_tr16_at(b_col[stg][nf] + 4 * CF::RB);
+      bf[buf][nf] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
+  auto read_a = [&](int stg, int mf) { af[mf] = lds_ld128(a_col[stg] + 16 * mf * CF::RA); };
+
+  // One K tile: its fragments are in af and bf[PAR].  Every step issues
+  // exactly one tile of loads (near the end the last tile again, into
+  // stages nobody reads), so the ring accounting is the same in every step.
+  auto step = [&](int kt, auto stg_tag, auto par_tag) {
+    constexpr int STG = decltype(stg_tag)::value;
+    constexpr int PAR = decltype(par_tag)::value;
+    constexpr int NXT = (STG + 1) % NS;
+    // Every wave has read tile kt (during step kt-1) and its own loads of
+    // tile kt+1 have landed (at most the NS-3 tiles issued after it are in
+    // flight): after the barrier tile kt+1 is readable and stage
+    // (kt-1)%NS, last read during step kt-2, takes tile kt+NS-1.
+    wait_vmcnt<(NS - 3) * CF::LPW>();
+    lds_barrier();
+    issue(min(kt + NS - 1, nk - 1), (STG + NS - 1) % NS);
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(NXT, PAR ^ 1);
+#pragma unroll
+    for (int mf = 0; mf < FM; ++mf) {
+#pragma unroll
+      for (int nf = 0; nf < FN; ++nf) acc[mf][nf] = mfma16<BF16>(bf[PAR][nf], af[mf], acc[mf][nf]);
+      read_a(NXT, mf);
+    }
+    interleave_rows16<FM, FN>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  land_args(C);  // C is used only after the K loop
+  // Prologue: tiles 0 .. NS-2 in flight (tiles past the end re-load the
+  // last one), wait for tile 0, read its fragments.
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p) issue(min(p, nk - 1), p);
+  wait_vmcnt<(NS - 2) * CF::LPW>();
+  lds_barrier();
+  read_b(0, 0);
+#pragma unroll
+  for (int mf = 0; mf < FM; ++mf) read_a(0, mf);
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using I4 = std::integral_constant<int, 4>;
+  static_assert(NS == 4 || NS == 5, "unrolled for 4 or 5 stages");
+  int kt = 0;
+  if constexpr (NS == 4) {
+    // stage kt % 4 and parity kt % 2 repeat every 4 tiles
+    for (; kt + 4 <= nk; kt += 4) {
+      step(kt, I0{}, I0{});
+      step(kt + 1, I1{}, I1{});
+      step(kt + 2, I2{}, I0{});
+      step(kt + 3, I3{}, I1{});
+    }
+    if (kt < nk) step(kt, I0{}, I0{});
+    if (kt + 1 < nk) step(kt + 1, I1{}, I1{});
+    if (kt + 2 < nk) step(kt + 2, I2{}, I0{});
+  } else {
+    // stage kt % 5 and parity kt % 2 repeat every 10 tiles
+    for (; kt + 10 <= nk; kt += 10) {
+      step(kt, I0{}, I0{});
+      step(kt + 1, I1{}, I1{});
+      step(kt + 2, I2{}, I0{});
+      step(kt + 3, I3{}, I1{});
+      step(kt + 4, I4{}, I0{});
+      step(kt + 5, I0{}, I1{});
+      step(kt + 6, I1{}, I0{});
+      step(kt + 7, I2{}, I1{});
+      step(kt + 8, I3{}, I0{});
+      step(kt + 9, I4{}, I1{});
+    }
+    if (kt < nk) step(kt, I0{}, I0{});
+    if (kt + 1 < nk) step(kt + 1, I1{}, I1{});
+    if (kt + 2 < nk) step(kt + 2, I2{}, I0{});
+    if (kt + 3 < nk) step(kt + 3, I3{}, I1{});
+    if (kt + 4 < nk) step(kt + 4, I4{}, I0{});
+    if (kt + 5 < nk) step(kt + 5, I0{}, I1{});
+    if (kt + 6 < nk) step(kt + 6, I1{}, I0{});
+    if (kt + 7 < nk) step(kt + 7, I2{}, I1{});
+    if (kt + 8 < nk) step(kt + 8, I3{}, I0{});
+  }
+  wait_vmcnt<0>();  // no DMA may land in LDS after the workgroup ends
+
+  // ---- epilogue: lane holds m = m0 + am + 16 mf, n = n0 + wn*TN + 16 nf + 4 kg + {0..3} ----
+#pragma unroll
+  for (int mf = 0; mf < FM; ++mf) {
+    const int gm = m0 + am + 16 * mf;
+    if (gm >= M) continue;
+    uint16_t* crow = C + (size_t)gm * ldc;
+#pragma unroll
+    for (int nf = 0; nf < FN; ++nf) {
+      const int gn = n0 + wn * CF::TN + 16 * nf + 4 * kg;
+      if (gn < N) {
+        const f32x4& a = acc[mf][nf];
+        st64(crow + gn, u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])});
+      }
+    }
+  }
+}
+
+template <int NS, int WM, int WN>
+static int launch_dma16(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
+                        hipStream_t stream) {
+  using CF = D16Cfg<NS, WM, WN>;
+  const long long tiles = (long long)((M + CF::BM - 1) / CF::BM) * ((N + CF::BN - 1) / CF::BN);
+  if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
+  const int smem = NS * CF::STAGE;
+  constexpr auto kern = gemm_bf16_dma16_kernel<NS, WM, WN>;
+  MX_RETURN_IF_HIP(lds_limit_once<kern>(smem));
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CF::NT), smem, stream, (const uint16_t*)A,
+                     (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
 template <int BM, int BN, int WM, int WN, int KS = 1, int PF = 1>
 static int launch(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
                   hipStream_t stream, int batch = 1, long long sA = 0, long long sB = 0, long long sC = 0) {
@@ -740,8 +1015,13 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   const long long tiles128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
   // At least one 256x256 tile per CU and whole K tiles: the direct-load
   // kernel (its lane offsets are 32-bit: 256 rows of A must span < 4 GiB).
-  if (tiles256 >= 256 && K % MX_BF16_BK == 0 && (long long)lda * 2 * 256 <= 0xffffffffLL)
+  if (tiles256 >= 256 && K % MX_BF16_BK == 0 && (long long)lda * 2 * 256 <= 0xffffffffLL) {
+#if MX_BF16_MFMA16
+    return mx::gemm::launch_dma16<MX_BF16_NS, MX_BF16_WM, MX_BF16_WN>(A, B, C, M, N, K, lda, ldb, ldc, s);
+#else
     return mx::gemm::launch_dma<MX_BF16_BK, MX_BF16_NS, MX_BF16_WM, MX_BF16_WN>(A, B, C, M, N, K, lda, ldb, ldc, s);
+#endif
+  }
   // Otherwise: register-staged kernels, big tiles when they still cover the
   // 256 CUs twice, else smaller tiles for parallelism.
   if (tiles256 >= 512) return mx::gemm::launch<256, 256, 2, 4>(A, B, C, M, N, K, lda, ldb, ldc, s);
