@@ -565,8 +565,9 @@ static int launch_dma(const void* A, const void* B, void* C, int M, int N, int K
 //    reads k-row 8kg + 4r + j, columns 4a..+3, r = 0, 1), A^T fragments are
 //    one 16-byte read of an A row; each lane's D is four consecutive n of
 //    one row of C (an 8-byte store).
-//  * A rows are 64 B: a 16-lane read phase (one k-group) covers 16 rows,
-//    chunk kg ^ ((m >> 2) & 3) puts them on 16 distinct 16-byte slots.  B
+//  * A rows are 64 B and a fragment read covers 16 rows x 4 chunks: chunk
+//    kg ^ ((m >> 1) & 3) is the XOR that measured conflict-free on gfx950
+//    (SQ_LDS_BANK_CONFLICT 0; the (m >> 2) and (m & 3) forms conflict).  B
 //    rows are 512 B (same banks every row): a 32-lane phase of transposing
 //    reads covers 8 k-rows (two k-groups x 4) of 32 bytes each, and chunk
 //    c ^ 2((k & 3) | ((k >> 3) & 1) << 2) gives the 8 rows distinct 32-byte
@@ -594,7 +595,7 @@ struct D16Cfg {
   static_assert((NS - 3) * LPW < 64, "vmcnt range");
   static_assert(A_LPW >= 1 && B_LPW >= 1 && FM >= 1 && FN >= 1, "tile split");
 };
-__device__ __forceinline__ int swz_a16(int m) { return (m >> 2) & 3; }
+__device__ __forceinline__ int swz_a16(int m) { return (m >> 1) & 3; }
 // Schedule of one K tile: per row block FN MFMAs, then LDS reads: the 2FN
 // B^T reads spread over the first half of the row blocks, each A^T read
 // right behind its row block.
