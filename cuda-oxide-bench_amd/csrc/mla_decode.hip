@@ -235,7 +235,8 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
     for (int dt = 0; dt < VTW; ++dt) acc[g][dt] = f32x16{};
   float m_run = -1e30f, l_run = 0.f;
 
-  // ---- S^T of stage si for head group `wave` (36 k-steps, two chains).
+  // ---- S^T of stage si for head group `wave` (36 k-steps, one chain:
+  // back-to-back accumulating MFMAs issue at the full rate).
   // With dma >= 0, this wave's direct loads of stage dma are issued one
   // per 4 k-steps, so they queue behind MFMAs instead of stalling the wave
   // at the address unit all at once. ----
@@ -246,40 +247,43 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
       return ks < 32 ? ld128(lat + koff[ks & 3] + 128 * (ks >> 2)) : ld128(rope + koff[ks & 3]);
     };
     constexpr int KLA = 6;
-    f32x16 sa = f32x16{}, sb = f32x16{};
+    f32x16 sa = f32x16{};
     u32x4 kf[8];
 #pragma unroll
     for (int ks = 0; ks < KLA; ++ks) kf[ks] = kread(ks);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (ks + KLA < KS) kf[(ks + KLA) & 7] = kread(ks + KLA);
-      if (ks & 1)
-        sb = mfma32<BF16>(kf[ks & 7], qf[ks], sb);
-      else
-        sa = mfma32<BF16>(kf[ks & 7], qf[ks], sa);
+      sa = mfma32<BF16>(kf[ks & 7], qf[ks], sa);
       if ((ks & 3) == 2 && ks / 4 < LPW && dma >= 0) issue_p(dma, ks / 4);
       __builtin_amdgcn_sched_barrier(0);
     }
-    return sa + sb;
+    return sa;
   };
 
-  // Softmax pieces of stage si on its scores sc (lane holds head l32,
-  // tokens tb + 8 i + 4 hsel + j for sc[4 i + j]).
-  auto scale_mask = [&](f32x16& sc, int si, int r0, int r1, float& mx) {
+  // Softmax pieces of stage si on its raw scores sc (lane holds head l32,
+  // tokens tb + 8 i + 4 hsel + j for sc[4 i + j]).  The scale (log2 units)
+  // is applied inside the exponent, exp2(s * sl2 - m): the row max of the
+  // raw scores times sl2 > 0 is the max of the scaled ones, so no multiply
+  // per score is needed before it.  Only the last stage of a slice can hold
+  // tokens past its end: they are masked by one wave-uniform branch, not by
+  // a select per score in every stage.
+  auto mask_tail = [&](f32x16& sc, int si) {
     const int tb = t0 + si * BT;
-    const bool need_mask = tb + BT > t1;
+    if (tb + BT > t1) {
 #pragma unroll
-    for (int r = r0; r < r1; ++r) {
-      float x = sc[r] * sl2;
-      if (need_mask && tb + 8 * (r >> 2) + 4 * hsel + (r & 3) >= t1) x = -INFINITY;
-      sc[r] = x;
-      mx = fmaxf(mx, x);
+      for (int r = 0; r < 16; ++r)
+        if (tb + 8 * (r >> 2) + 4 * hsel + (r & 3) >= t1) sc[r] = -INFINITY;
     }
+  };
+  auto row_max = [&](const f32x16& sc, int r0, int r1, float& mx) {
+#pragma unroll
+    for (int r = r0; r < r1; ++r) mx = fmaxf(mx, sc[r]);
   };
   // Lazy running-max update; the rescale flag and factors of stage si go
   // to buffer si&1 for the value waves.
   auto update_max = [&](float mx, int si) {
-    mx = max_xor32(mx);
+    mx = max_xor32(mx) * sl2;  // raw -> log2 units
     int* flags = reinterpret_cast<int*>(smem + F_OFF) + (si & 1) * NWAVES;
     float* corrs = reinterpret_cast<float*>(smem + C_OFF) + ((si & 1) * NWAVES + wave) * 32;
     int flag = 0;
@@ -299,7 +303,7 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
     u32x4* pbuf = reinterpret_cast<u32x4*>(smem + P_OFF + (si & 1) * P_BUF);
     float p[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(sc[8 * k2 + e] - m_run);
+    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(sc[8 * k2 + e], sl2, -m_run));
     const u32x4 pf{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                    pack_bf16x2(p[6], p[7])};
 #pragma unroll
@@ -308,17 +312,18 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
   };
   auto scores_alone = [&](int si, int dma) {
     f32x16 sc = score_mfma(si, dma);
+    mask_tail(sc, si);
     float mx = -INFINITY;
-    scale_mask(sc, si, 0, 16, mx);
+    row_max(sc, 0, 16, mx);
     update_max(mx, si);
     p_chunk(sc, si, 0);
     p_chunk(sc, si, 1);
   };
 
   // ---- values of stage pi: O^T[128 wave + 32 dt .., heads] += V^T . P^T.
-  // With SOFT, the softmax of stage pi+1 (scores sc) runs beside the MFMAs:
-  // scale, mask and max beside the first k half, exp2 / P^T beside the
-  // second. ----
+  // With SOFT, the softmax of stage pi+1 (scores sc, already masked) runs
+  // beside the MFMAs: the row max beside the first k half, exp2 / P^T
+  // beside the second. ----
   auto values = [&](int pi, auto with_soft, f32x16& sc) {
     constexpr bool SOFT = decltype(with_soft)::value;
     // all four flags in one LDS read (one wait instead of four)
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
         for (int dt = 0; dt < VTW; ++dt) acc[g][dt] = mfma32<BF16>(vf[k2][dt], pb[g & 1], acc[g][dt]);
         if constexpr (SOFT) {
           if (k2 == 0)
-            scale_mask(sc, pi + 1, 4 * g, 4 * g + 4, mx);
+            row_max(sc, 4 * g, 4 * g + 4, mx);
           else if (g & 1)
             p_chunk(sc, pi + 1, g >> 1);
         }
@@ -388,6 +393,7 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
   for (int i = 1; i < nblk; ++i) {
     sync(i);
     f32x16 sc = score_mfma(i, i + 2 < nblk ? i + 2 : -1);
+    mask_tail(sc, i);
     values(i - 1, std::true_type{}, sc);
   }
   sync(nblk);
