@@ -48,6 +48,9 @@
 #define MX_BF16_WN 4
 #endif
 // 1: the 16x16x32-MFMA direct-load kernel (BK fixed at 32), 0: the 32x32x16 one
+#ifndef MX_BF16_SDMA
+#define MX_BF16_SDMA 1
+#endif
 #ifndef MX_BF16_MFMA16
 #define MX_BF16_MFMA16 1
 #endif
@@ -550,6 +553,161 @@ static int launch_dma(const void* A, const void* B, void* C, int M, int N, int K
 }
 
 // ---------------------------------------------------------------------------
+// gemm_bf16_sdma_kernel: grids of about one 64x64 tile per CU with a long K
+// (1024^3).  There the time is the latency of streaming each tile's 64 rows
+// of A and 64 columns of B (256 KB per CU at 1024^3), not the MFMAs, so the
+// loads go HBM -> LDS directly through a deep ring:
+//  * 8 waves = 2 K groups x (2 x 2 waves of 32x32); group q takes the K
+//    tiles q*nk .. q*nk + nk - 1, and the two groups' accumulators are
+//    summed through LDS at the end;
+//  * each group has a 5-slot ring of 64-deep K tiles (A: 64 rows x 128 B,
+//    B: 64 k-rows x 128 B; both groups fill the 160 KB of LDS) with four
+//    tiles (64 KB) in flight;
+//  * 16-byte chunks are XOR-swizzled per row, chunk ^ ((m >> 1) & 7) for A
+//    and chunk ^ (((k >> 1) & 1) << 2) for B: LDS serves a 128-bit read in
+//    16-lane groups keyed by lane bit 5 and the parity of lane bits 2..4,
+//    a transposing 64-bit read in 32-lane halves, and both fragment reads
+//    below then touch distinct bank slots within every group.
+// Shapes: M, N multiples of 64, K a multiple of 128.
+// ---------------------------------------------------------------------------
+struct SCfg {
+  static constexpr int BM = 64, BN = 64, BK = 64, NSL = 5, KSG = 2;
+  static constexpr int NW = 8, NWG = NW / KSG, NT = 64 * NW;  // waves, waves per group, threads
+  static constexpr int RA = BK * 2, RB = BN * 2;              // LDS row bytes (128)
+  static constexpr int A_B = BM * RA, B_B = BK * RB;          // 8 KB each
+  static constexpr int STAGE = A_B + B_B;
+  static constexpr int GRP = NSL * STAGE;                     // ring of one group
+  static constexpr int LDS = KSG * GRP;
+  static constexpr int A_LPW = A_B / 1024 / NWG, B_LPW = B_B / 1024 / NWG;  // 1 KB loads per wave per tile
+  static constexpr int LPW = A_LPW + B_LPW;
+  static constexpr int RPL = 1024 / RA;                       // rows per 1 KB load
+  static_assert(LDS <= 160 * 1024 && (NSL - 2) * LPW < 64 && RA == RB, "ring");
+};
+__device__ __forceinline__ int swz_sa(int m) { return (m >> 1) & 7; }
+__device__ __forceinline__ int swz_sb(int k) { return ((k >> 1) & 1) << 2; }
+
+__global__ __launch_bounds__(SCfg::NT, 1) void gemm_bf16_sdma_kernel(const uint16_t* __restrict__ A,
+                                                                    const uint16_t* __restrict__ B,
+                                                                    uint16_t* __restrict__ C, int M, int N, int K,
+                                                                    int lda, int ldb, int ldc) {
+  using CF = SCfg;
+  extern __shared__ __align__(1024) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave / CF::NWG, wg = wave % CF::NWG;  // K group, wave within the group
+  const int wm = wg / 2, wn = wg % 2;
+  const int g = lane >> 5;
+
+  // ---- tile -> (tm, tn), grouped for L2 reuse, XCD-aware ----
+  const int tiles_m = M / CF::BM, tiles_n = N / CF::BN;
+  const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = GROUP_M * tiles_n;
+  const int first_m = (id / per_group) * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  const int m0 = (first_m + (id % per_group) % gsz) * CF::BM;
+  const int n0 = ((id % per_group) / gsz) * CF::BN;
+  const int nk = K / CF::BK / CF::KSG;  // K tiles per group
+  const int kt0 = grp * nk;
+
+  // ---- direct loads: load n of this wave fills rows (k-rows) RPL*(wg*LPW+n)
+  // + lane/8 of the tile, lane taking the chunk stored at position lane%8 ----
+  const uint32_t lds0 = lds_addr(smem) + grp * CF::GRP;
+  uint32_t a_off[CF::A_LPW], b_off[CF::B_LPW];
+#pragma unroll
+  for (int n = 0; n < CF::A_LPW; ++n) {
+    const int row = CF::RPL * (wg * CF::A_LPW + n) + lane / 8;
+    a_off[n] = (uint32_t)row * (uint32_t)lda * 2u + 16u * ((lane % 8) ^ swz_sa(row));
+  }
+#pragma unroll
+  for (int n = 0; n < CF::B_LPW; ++n) {
+    const int row = CF::RPL * (wg * CF::B_LPW + n) + lane / 8;
+    b_off[n] = (uint32_t)row * (uint32_t)ldb * 2u + 16u * ((lane % 8) ^ swz_sb(row));
+  }
+  auto issue = [&](int kt, int slot) {
+    const uint32_t st = lds0 + slot * CF::STAGE;
+    const uint16_t* abase = A + (size_t)m0 * lda + (size_t)(kt0 + kt) * CF::BK;
+    const uint16_t* bbase = B + (size_t)(kt0 + kt) * CF::BK * ldb + n0;
+#pragma unroll
+    for (int n = 0; n < CF::A_LPW; ++n) dma16(abase, a_off[n], st + (wg * CF::A_LPW + n) * 1024);
+#pragma unroll
+    for (int n = 0; n < CF::B_LPW; ++n) dma16(bbase, b_off[n], st + CF::A_B + (wg * CF::B_LPW + n) * 1024);
+  };
+
+  // ---- fragment addresses in slot 0.  A^T (B operand): m = 32 wm +
+  // lane%32, k-chunk 2 ks + g.  B^T (A operand) by transposing reads: lane
+  // (g, sg, 4j+a) reads k-row 16 ks + 8 g + j (+4 for the upper half),
+  // columns 32 wn + 16 sg + 4a .. +3. ----
+  const int am = 32 * wm + (lane & 31);
+  uint32_t a_frag[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) a_frag[ks] = lds0 + am * CF::RA + 16 * ((2 * ks + g) ^ swz_sa(am));
+  const int b_sg = (lane >> 4) & 1, b_j = (lane >> 2) & 3, b_a = lane & 3;
+  const uint32_t b_frag = lds0 + CF::A_B + (8 * g + b_j) * CF::RB +
+                          16 * (((32 * wn + 16 * b_sg + 4 * b_a) >> 3) ^ swz_sb(b_j)) + 8 * (b_a & 1);
+
+  f32x16 acc = f32x16{};
+  auto compute = [&](int slot) {
+    const uint32_t so = slot * CF::STAGE;
+    u32x4 af[4], bf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      af[ks] = lds_ld128(a_frag[ks] + so);
+      const u32x2 lo = lds_read_tr16_at(b_frag + so + 16 * ks * CF::RB);
+      const u32x2 hi = lds_read_tr16_at(b_frag + so + (16 * ks + 4) * CF::RB);
+      bf[ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mfma32<BF16>(bf[ks], af[ks], acc);
+  };
+
+  land_args(C);  // C is used only after the K loop
+  // Tiles 0 .. NSL-2 in flight; every iteration issues one more (past the
+  // end the last tile again, into slots nobody reads), so the wait is the
+  // same in every iteration: tile kt has landed once at most NSL-2 tiles
+  // issued after it are outstanding.
+#pragma unroll
+  for (int p = 0; p < CF::NSL - 1; ++p) issue(min(p, nk - 1), p);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_vmcnt<(CF::NSL - 2) * CF::LPW>();
+    lds_barrier();  // tile kt visible to every wave; slot (kt-1) % NSL free
+    issue(min(kt + CF::NSL - 1, nk - 1), (kt + CF::NSL - 1) % CF::NSL);
+    compute(kt % CF::NSL);
+  }
+  wait_vmcnt<0>();  // no load lands after this point
+  __syncthreads();  // ... and every fragment read is done: the LDS is free
+
+  // ---- sum the two groups' accumulators (group 1 -> LDS -> group 0) ----
+  float* red = reinterpret_cast<float*>(smem);
+  const int tid = threadIdx.x % (64 * CF::NWG);
+  if (grp == 1) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) red[e * 64 * CF::NWG + tid] = acc[e];
+  }
+  __syncthreads();
+  if (grp == 1) return;  // no barrier follows
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] += red[e * 64 * CF::NWG + tid];
+
+  // ---- epilogue: lane holds m = m0 + am, n = n0 + 32 wn + 8 i + 4 g + {0..3} ----
+  uint16_t* crow = C + (size_t)(m0 + am) * ldc + n0 + 32 * wn + 4 * g;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    st64(crow + 8 * i, u32x2{pack_bf16x2(acc[4 * i], acc[4 * i + 1]), pack_bf16x2(acc[4 * i + 2], acc[4 * i + 3])});
+}
+
+static int launch_sdma(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
+                       hipStream_t stream) {
+  const long long tiles = (long long)(M / SCfg::BM) * (N / SCfg::BN);
+  if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
+  constexpr auto kern = gemm_bf16_sdma_kernel;
+  MX_RETURN_IF_HIP(lds_limit_once<kern>(SCfg::LDS));
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(SCfg::NT), SCfg::LDS, stream, (const uint16_t*)A,
+                     (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+// ---------------------------------------------------------------------------
 // gemm_bf16_dma16_kernel: the direct-load design above on 16x16x32 MFMAs.
 // Under a sustained full-chip MFMA load the 16x16x32 shape delivers about
 // 11% more bf16 throughput than 32x32x16 on MI355X (same FLOPs, less
@@ -1030,6 +1188,13 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   // About one 64x64 tile per CU or fewer and a long K (e.g. 1024^3): split
   // K between two wave groups of each workgroup.
   const long long tiles64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
+#if MX_BF16_SDMA
+  // ... with whole 64x64 tiles and 128-deep K chunks: the direct-load ring
+  // (32-bit lane offsets: 64 rows of A and 64 k-rows of B span < 4 GiB).
+  if (tiles64 <= 256 && K >= 512 && M % 64 == 0 && N % 64 == 0 && K % 128 == 0 &&
+      (long long)lda * 2 * 64 <= 0xffffffffLL && (long long)ldb * 2 * 64 <= 0xffffffffLL)
+    return mx::gemm::launch_sdma(A, B, C, M, N, K, lda, ldb, ldc, s);
+#endif
   if (tiles64 <= 256 && K >= 512) return mx::gemm::launch<64, 64, 2, 2, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
   return mx::gemm::launch<64, 64, 2, 2, 1, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
 }

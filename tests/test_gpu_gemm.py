@@ -47,6 +47,25 @@ def test_parity_vs_oracle(ops, mnk):
     assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
 
 
+@pytest.mark.parametrize("mnk,path", [((64, 64, 4096), "direct-load ring, one tile, 32 K tiles per group"),
+                                      ((256, 1024, 2048), "direct-load ring, 64 tiles"),
+                                      ((1024, 1024, 1024), "direct-load ring, 256 tiles (BASELINE configs[0])"),
+                                      ((1024, 1024, 576), "K % 128 != 0: register-staged split-K path"),
+                                      ((960, 1024, 512), "M % 64 == 0, 240 tiles: direct-load ring")])
+def test_small_grid_paths(ops, mnk, path):
+    """Grids of at most one 64x64 tile per CU with K >= 512: whole tiles and
+    128-deep K chunks run the direct-load ring (two K groups per workgroup
+    summed through LDS), other shapes the register-staged split-K kernel."""
+    m, n, k = mnk
+    announce(f"gemm_bf16 {m}x{n}x{k} ({path})")
+    a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
+    c = run(ops, a, b)
+    ref = ogemm.gemm_ref(a, b)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+
+
 def test_reference_distribution_sampled_gate(ops):
     """The reference harness's own check at its smoke size: U[0,1) inputs,
     200 sampled cells, |err| <= 0.2 + 0.05|ref| (cutile-matmul-tc-bf16/main.py:110-135)."""
