@@ -48,6 +48,9 @@
 #define MX_BF16_WN 4
 #endif
 // 1: the 16x16x32-MFMA direct-load kernel (BK fixed at 32), 0: the 32x32x16 one
+#ifndef MX_BF16_SMALLM_SK
+#define MX_BF16_SMALLM_SK 1
+#endif
 #ifndef MX_BF16_SDMA
 #define MX_BF16_SDMA 1
 #endif
@@ -1139,10 +1142,150 @@ __global__ __launch_bounds__(64) void gemm_bf16_smallm_kernel(const uint16_t* __
   }
 }
 
+// Split-K variant for items with a few 64-deep K chunks (4..12, e.g. the
+// 32 x 128 x 512 up-projection of the MLA absorbed step): one workgroup of
+// KW waves per 32 x (32 NF) tile, wave w taking chunks w*nkw .. w*nkw +
+// nkw - 1 and issuing all of them at once into its own LDS region, so a
+// tile needs a single round trip to memory and reads A once per column
+// tile; the partial sums meet in LDS (waves 1..KW-1 each write theirs into
+// their own, consumed region, wave 0 adds and stores).
+template <int NF, int KW>
+__global__ __launch_bounds__(64 * KW) void gemm_bf16_smallm_sk_kernel(const uint16_t* __restrict__ A,
+                                                                     const uint16_t* __restrict__ B,
+                                                                     uint16_t* __restrict__ C, int M, int N, int K,
+                                                                     int lda, int ldb, int ldc, long long sA,
+                                                                     long long sB, long long sC) {
+  constexpr int TN = 32 * NF, RB = TN * 2, B_B = SM_BK * RB, STAGE = SM_A_B + B_B;
+  constexpr int BL = B_B / 1024, BCH = RB / 16, BRPL = 1024 / RB;
+  extern __shared__ __align__(1024) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;
+  const int tiles_n = (N + TN - 1) / TN;
+  const int n0 = (int)(blockIdx.x % tiles_n) * TN;
+  const size_t item = blockIdx.x / tiles_n;
+  A += item * sA;
+  B += item * sB;
+  C += item * sC;
+  const int nkw = K / SM_BK / KW;  // chunks per wave (1..3)
+  const int kc0 = wave * nkw;
+  const uint32_t lds0 = lds_addr(smem) + wave * nkw * STAGE;
+
+  // Direct-load lane offsets as in the kernel above.
+  uint32_t a_off[4], b_off[BL];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int row = 8 * n + (lane >> 3);
+    a_off[n] = (uint32_t)min(row, M - 1) * (uint32_t)lda * 2u + 16u * ((lane & 7) ^ swz_a<64>(row));
+  }
+#pragma unroll
+  for (int n = 0; n < BL; ++n) {
+    const int kr = BRPL * n + lane / BCH;
+    const int col = min(n0 + 8 * ((lane % BCH) ^ sm_swz<NF>(kr)), N - 8);
+    b_off[n] = (uint32_t)kr * (uint32_t)ldb * 2u + 2u * col;
+  }
+  for (int c = 0; c < nkw; ++c) {
+    const uint32_t st = lds0 + c * STAGE;
+    const uint16_t* ab = A + (size_t)(kc0 + c) * SM_BK;
+    const uint16_t* bb = B + (size_t)(kc0 + c) * SM_BK * ldb;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) dma16(ab, a_off[n], st + n * 1024);
+#pragma unroll
+    for (int n = 0; n < BL; ++n) dma16(bb, b_off[n], st + SM_A_B + n * 1024);
+  }
+
+  const int am = lane & 31;
+  const int b_sg = (lane >> 4) & 1, b_j = (lane >> 2) & 3, b_a = lane & 3;
+  const uint32_t a_base = lds0 + am * 128;
+  const int ax = swz_a<64>(am);
+  uint32_t b_base[NF];
+#pragma unroll
+  for (int nf = 0; nf < NF; ++nf) {
+    const int chunk = (32 * nf + 16 * b_sg + 4 * b_a) >> 3;
+    b_base[nf] = lds0 + SM_A_B + (8 * g + b_j) * RB + 16 * (chunk ^ sm_swz<NF>(b_j)) + 8 * (b_a & 1);
+  }
+  f32x16 acc[NF];
+#pragma unroll
+  for (int nf = 0; nf < NF; ++nf) acc[nf] = f32x16{};
+  land_args(C);  // C is used only after the loop
+  for (int c = 0; c < nkw; ++c) {
+    // chunk c landed once at most nkw-1-c later chunks are in flight
+    wait_chunks<4 + BL, 2>(nkw - 1 - c);
+    const uint32_t so = c * STAGE;
+#pragma unroll
+    for (int ks = 0; ks < SM_BK / 16; ++ks) {
+      const u32x4 af = lds_ld128(a_base + so + 16 * ((2 * ks + g) ^ ax));
+#pragma unroll
+      for (int nf = 0; nf < NF; ++nf) {
+        const uint32_t bp = b_base[nf] + so + 16 * ks * RB;
+        const u32x2 lo = lds_read_tr16_at(bp);
+        const u32x2 hi = lds_read_tr16_at(bp + 4 * RB);
+        acc[nf] = mfma32<BF16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, af, acc[nf]);
+      }
+    }
+  }
+
+  // Partial sums: waves 1..KW-1 into their own (consumed) LDS region, laid
+  // out [nf][e][lane] so consecutive lanes hit consecutive banks.
+  float* mine = reinterpret_cast<float*>(smem + wave * nkw * STAGE);
+  if (wave > 0) {
+#pragma unroll
+    for (int nf = 0; nf < NF; ++nf)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mine[(nf * 16 + e) * 64 + lane] = acc[nf][e];
+  }
+  __syncthreads();
+  if (wave > 0) return;  // no barrier follows
+  for (int w = 1; w < KW; ++w) {
+    const float* other = reinterpret_cast<const float*>(smem + w * nkw * STAGE);
+#pragma unroll
+    for (int nf = 0; nf < NF; ++nf)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[nf][e] += other[(nf * 16 + e) * 64 + lane];
+  }
+
+  // lane holds m = lane%32, n = n0 + 32 nf + 8 i + 4 g + {0..3}
+  if (am < M) {
+    uint16_t* crow = C + (size_t)am * ldc;
+#pragma unroll
+    for (int nf = 0; nf < NF; ++nf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int gn = n0 + 32 * nf + 8 * i + 4 * g;
+        const f32x16& a = acc[nf];
+        if (gn < N) st64(crow + gn, u32x2{pack_bf16x2(a[4 * i], a[4 * i + 1]), pack_bf16x2(a[4 * i + 2], a[4 * i + 3])});
+      }
+  }
+}
+
 static int launch_smallm(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda, int ldb,
                          int ldc, long long sA, long long sB, long long sC, hipStream_t stream) {
-  // Widest column tile that still leaves >= 512 workgroups (two per CU).
   auto groups = [&](int tn) { return (long long)batch * ((N + tn - 1) / tn); };
+#if MX_BF16_SMALLM_SK
+  // 4..12 chunks of K, split among 4 waves: one workgroup per 32 x 64 tile
+  // when that still gives >= 256 workgroups (one per CU), else 32 x 32.
+  const int nkc = K / SM_BK;
+  if (nkc % 4 == 0 && nkc >= 4 && nkc <= 12) {
+    const int nfs = groups(64) >= 256 ? 2 : 1;
+    const long long gsk = groups(32 * nfs);
+    if (gsk > 0x7fffffffLL) return MX_ERR_SHAPE;
+    const int smem = nkc * (SM_A_B + SM_BK * 64 * nfs);
+    if (nfs == 2) {
+      constexpr auto kern = gemm_bf16_smallm_sk_kernel<2, 4>;
+      MX_RETURN_IF_HIP(lds_limit_once<kern>(12 * (SM_A_B + SM_BK * 128)));
+      hipLaunchKernelGGL(kern, dim3((unsigned)gsk), dim3(256), smem, stream, (const uint16_t*)A, (const uint16_t*)B,
+                         (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
+    } else {
+      constexpr auto kern = gemm_bf16_smallm_sk_kernel<1, 4>;
+      MX_RETURN_IF_HIP(lds_limit_once<kern>(12 * (SM_A_B + SM_BK * 64)));
+      hipLaunchKernelGGL(kern, dim3((unsigned)gsk), dim3(256), smem, stream, (const uint16_t*)A, (const uint16_t*)B,
+                         (uint16_t*)C, M, N, K, lda, ldb, ldc, sA, sB, sC);
+    }
+    MX_RETURN_IF_HIP(hipGetLastError());
+    return MX_OK;
+  }
+#endif
+  // Widest column tile that still leaves >= 512 workgroups (two per CU).
   const int nf = groups(128) >= 512 ? 4 : (groups(64) >= 512 ? 2 : 1);
   const long long grid = groups(32 * nf);
   if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;

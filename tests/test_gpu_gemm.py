@@ -161,10 +161,14 @@ def test_rejects_bad_arguments(ops):
 
 
 @pytest.mark.parametrize("bmnk", [(1, 64, 64, 64), (7, 100, 136, 72), (128, 32, 512, 128), (128, 32, 128, 512), (16, 5, 40, 192),
-                                  (3, 300, 264, 520), (4, 1024, 1024, 256)])
+                                  (3, 300, 264, 520), (4, 1024, 1024, 256),
+                                  # split-K small-M kernel: 4, 8 and 12 chunks of K, 32 x 64 and 32 x 32
+                                  # tiles, ragged M and N
+                                  (8, 17, 72, 256), (64, 32, 136, 768), (200, 32, 128, 512), (3, 1, 8, 512)])
 def test_batched_vs_oracle(ops, bmnk):
     """Strided-batched GEMM: every item against the fp32 oracle (small-M,
-    64x64 and, at 4 x 1024x1024x256, the 128x128 register-staged kernel)."""
+    its split-K variant for 4..12 chunks of K, 64x64 and, at 4 x
+    1024x1024x256, the 128x128 register-staged kernel)."""
     nb, m, n, k = bmnk
     announce(f"gemm_bf16_batched {nb}x{m}x{n}x{k}")
     g = torch.Generator().manual_seed(nb * 131 + m)
