@@ -23,14 +23,18 @@ torch.cuda.synchronize() calls with one HIP event pair on the launching
 stream.  The headline launches are issued eagerly from Python (each
 ~150 us kernel hides the host cost); the other kernels' K launches are
 captured once into a HIP graph and replayed, so few-microsecond kernels
-are timed on the device, not as Python launch overhead.
+are timed on the device, not as Python launch overhead.  Before each
+case's warm-up (for graph-timed cases, before the untimed replay) the GPU
+runs --settle-ms (default 300) of a plain device GEMM, so the timed steps
+start at load clocks rather than at the clocks of an idle GPU; the JSON
+line reports it under "settle".
 
 CPU baseline (BASELINE.md's plan): this repository's CPU oracle (the
 restatement of the reference's CPU implementation, "port") on the same
 seeded inputs, torch fp32 on the host's cores, 1 warm-up + 3 timed runs,
 median; the GPU output is compared against it on the same sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--settle-ms MS]
        [--only NAME[,NAME...]] [--only-headline] [--calibrate-copy]
 Prints exactly one JSON line on stdout (progress goes to stderr).
 """
@@ -58,12 +62,42 @@ def log(msg: str) -> None:
 
 
 # ---------------------------------------------------------------- timing
+# Device settle.  An MI355X coming out of idle runs at low clocks for a few
+# hundred milliseconds of load (measured: the headline kernel takes 151 us
+# per launch right after idle, 141 us after 100 ms of load and 127 us after
+# 300 ms).  Before each case's warm-up steps the GPU is therefore kept busy
+# for SETTLE_MS with a plain device GEMM (torch.matmul, 8192^2 bf16; not
+# the measured kernel), so that the warm-up and timed steps run at load
+# clocks.  The W warm-up and K timed steps themselves are unchanged.
+SETTLE_MS = 300.0
+_SETTLE: dict = {}
+
+
+def settle() -> None:
+    import torch
+
+    if SETTLE_MS <= 0:
+        return
+    if "a" not in _SETTLE:
+        g = torch.Generator(device="cuda").manual_seed(1)
+        _SETTLE["a"] = torch.randn(8192, 8192, device="cuda", generator=g).to(torch.bfloat16)
+        _SETTLE["c"] = torch.empty_like(_SETTLE["a"])
+    a, c = _SETTLE["a"], _SETTLE["c"]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < SETTLE_MS:
+        for _ in range(8):
+            torch.matmul(a, a, out=c)
+        torch.cuda.synchronize()
+
+
 def time_eager(fn, steps: int, warmup: int):
     """`warmup` calls, then exactly `steps` back-to-back calls bracketed by
     synchronize() and one event pair on the current stream.  Returns (event
     ms per launch, wall ms per step)."""
     import torch
 
+    settle()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -100,6 +134,7 @@ def time_graph(fn, steps: int, warmup: int):
         for _ in range(steps):
             fn()
     torch.cuda.synchronize()
+    settle()
     g.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
@@ -475,16 +510,26 @@ def calibrate_copy(steps: int) -> int:
     return 0
 
 
+def settle_note() -> dict:
+    return {"ms_before_each_case": SETTLE_MS,
+            "work": "torch.matmul 8192x8192 bf16 (a device GEMM, not the measured kernel)",
+            "why": "the GPU leaves idle clocks only after a few hundred ms of load; warm-up and timed steps "
+                   "(exactly --warmup and --steps) then run at load clocks"}
+
+
 def _clean(rec: dict) -> dict:
     return {k: v for k, v in rec.items() if k not in ("shape",)}
 
 
 def main() -> int:
+    global SETTLE_MS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="device GEMM load before each case's warm-up (ms; 0 disables)")
     ap.add_argument("--only-headline", action="store_true", help="run only the headline GQA case")
     ap.add_argument("--only", default="", help=f"comma-separated cases to run (of {', '.join(CASES)})")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -496,6 +541,7 @@ def main() -> int:
               "(every kernel is single-device; sharding is described in DESIGN.md). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
+    SETTLE_MS = max(0.0, args.settle_ms)
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
@@ -531,7 +577,8 @@ def main() -> int:
                           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(first["wall_ms"], 5),
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                           "dtype": "bf16", "data": "synthetic", "config": {"workload": first["workload"]},
-                          "partial_run": names, "others": {n: _clean(r) for n, r in results.items()}},
+                          "partial_run": names, "settle": settle_note(),
+                          "others": {n: _clean(r) for n, r in results.items()}},
                          default=float), flush=True)
         return 0
 
@@ -557,6 +604,7 @@ def main() -> int:
         },
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
+        "settle": settle_note(),
         "tflops_reference_convention": round(head["tflops_reference_convention"], 3),
         "others": {n: _clean(r) for n, r in results.items() if n != "gqa"},
     }
