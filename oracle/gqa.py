@@ -14,11 +14,15 @@ import torch
 
 
 def gqa_naive(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
-              scale: float | None = None, heads: list[int] | None = None) -> torch.Tensor:
+              scale: float | None = None, heads: list[int] | None = None,
+              rows: list[int] | None = None) -> torch.Tensor:
     """q [B,Hq,S,D], k/v [B,Hkv,S,D] (any float dtype) -> fp32 [B,Hq,S,D].
 
     `heads` restricts the computation to those query heads (others stay 0),
-    for bounded CPU timing samples.
+    for bounded CPU timing samples.  `rows` restricts it to those query
+    positions (each keeps its own causal row): the result is then
+    [B,Hq,len(rows),Dv], row i holding query position rows[i].  Long
+    sequences are checked on such samples.
     """
     q = q.detach().cpu().float()
     k = k.detach().cpu().float()
@@ -29,14 +33,15 @@ def gqa_naive(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = 
     G = Hq // Hkv
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    out = torch.zeros((B, Hq, S, v.shape[-1]), dtype=torch.float32)
+    pos = torch.arange(S) if rows is None else torch.tensor(rows, dtype=torch.long)
+    out = torch.zeros((B, Hq, pos.numel(), v.shape[-1]), dtype=torch.float32)
     mask = None
     if causal:
-        mask = torch.ones((S, S), dtype=torch.bool).triu(1)  # True above the diagonal
+        mask = torch.arange(k.shape[2])[None, :] > pos[:, None]  # key t hidden from query s iff t > s
     for b in range(B):
         for h in (heads if heads is not None else range(Hq)):
             kv = h // G  # repeat_interleave(groups, dim=1) maps query head h to kv head h // G
-            scores = (q[b, h] @ k[b, kv].transpose(0, 1)) * scale
+            scores = (q[b, h, pos] @ k[b, kv].transpose(0, 1)) * scale
             if mask is not None:
                 scores = scores.masked_fill(mask, float("-inf"))
             probs = torch.softmax(scores, dim=-1)

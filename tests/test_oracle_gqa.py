@@ -80,3 +80,23 @@ def test_heads_subset_equals_full():
     full = ogqa.gqa_naive(q, k, v, causal=True)
     part = ogqa.gqa_naive(q, k, v, causal=True, heads=[1, 6])
     assert torch.equal(full[:, [1, 6]], part[:, [1, 6]])
+
+
+def test_rows_subset_equals_full_and_sdpa():
+    """Sampled query positions keep their own causal rows: equal to the same
+    rows of the full computation and of the SDPA witness, and blind to keys
+    past each row."""
+    q, k, v = inputs.gqa_inputs(shapes.GQAShape("t", 2, 200, 8, 2, 32, True), dtype=torch.float32)
+    rows = [0, 1, 63, 64, 127, 150, 199]
+    for causal in (False, True):
+        full = ogqa.gqa_naive(q, k, v, causal=causal)
+        part = ogqa.gqa_naive(q, k, v, causal=causal, rows=rows)
+        assert torch.allclose(part, full[:, :, rows], atol=1e-6, rtol=1e-6)
+        sd = ogqa.gqa_sdpa(q, k, v, causal=causal)
+        assert torch.allclose(part, sd[:, :, rows], atol=1e-5, rtol=1e-5)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, 151:] += 3.0
+    v2[:, :, 151:] -= 5.0
+    a = ogqa.gqa_naive(q, k, v, causal=True, rows=[0, 64, 150])
+    b = ogqa.gqa_naive(q, k2, v2, causal=True, rows=[0, 64, 150])
+    assert torch.equal(a, b)
