@@ -16,6 +16,10 @@
 // a 5-stage ring, one barrier per K tile, the next k-step's LDS reads
 // interleaved with the current MFMAs.  Details at the kernel.
 //
+// gemm_bf16_dma16_kernel on 128x128 tiles (at least one per CU, fewer than
+// one 256x256 tile per CU, K % 32 == 0, e.g. 2048^3): the same design with
+// 8 waves of 64x32 and a 6-stage ring of 16 KB stages.
+//
 // gemm_bf16_kernel (everything else: small or ragged-K problems):
 //  * One workgroup computes a BM x BN tile of C with WM x WN waves; each
 //    wave owns a (BM/WM) x (BN/WN) sub-tile of 32x32 fragments.
@@ -56,6 +60,14 @@
 #endif
 #ifndef MX_BF16_MFMA16
 #define MX_BF16_MFMA16 1
+#endif
+// Ring stages and waves across N of the same kernel on 128x128 tiles (16 KB
+// stages; 6 measured best of 4..9 at 2048^3).
+#ifndef MX_BF16_D128_NS
+#define MX_BF16_D128_NS 6
+#endif
+#ifndef MX_BF16_D128_WN
+#define MX_BF16_D128_WN 4
 #endif
 
 namespace mx {
@@ -717,8 +729,9 @@ static int launch_sdma(const void* A, const void* B, void* C, int M, int N, int 
 // operand/accumulator traffic per FLOP, so less power at the same clock
 // cap), which is what sets the large-GEMM rate.
 //
-//  * 256x256 tile, BK = 32 (one 16x16x32 k-step per K tile), WM x WN waves,
-//    each owning (256/WM) x (256/WN) of C as 16x16 fragments.
+//  * BM x BN tile (256x256, or 128x128 for mid-size problems), BK = 32 (one
+//    16x16x32 k-step per K tile), WM x WN waves, each owning (BM/WM) x
+//    (BN/WN) of C as 16x16 fragments.
 //  * Operand layouts (16x16x32): the "A" operand holds 8 consecutive k of
 //    row l%16 at k-group l/16; "B" the same for column l%16; D holds rows
 //    4(l/16)..+3 of column l%16.  Issued as D^T = B^T . A^T: B^T fragments
@@ -729,7 +742,7 @@ static int launch_sdma(const void* A, const void* B, void* C, int M, int N, int 
 //  * A rows are 64 B and a fragment read covers 16 rows x 4 chunks: chunk
 //    kg ^ ((m >> 1) & 3) is the XOR that measured conflict-free on gfx950
 //    (SQ_LDS_BANK_CONFLICT 0; the (m >> 2) and (m & 3) forms conflict).  B
-//    rows are 512 B (same banks every row): a 32-lane phase of transposing
+//    rows are 512 B or 256 B (same banks every row): a 32-lane phase of transposing
 //    reads covers 8 k-rows (two k-groups x 4) of 32 bytes each, and chunk
 //    c ^ 2((k & 3) | ((k >> 3) & 1) << 2) gives the 8 rows distinct 32-byte
 //    slots.  The DMA applies the same XOR on the global side.
@@ -738,9 +751,9 @@ static int launch_sdma(const void* A, const void* B, void* C, int M, int N, int 
 //    parity double buffer at the step's start, each A^T one in place right
 //    after the four MFMAs that consumed the previous tile's.
 // ---------------------------------------------------------------------------
-template <int NS, int WM, int WN>
+template <int NS, int WM, int WN, int BM_ = 256, int BN_ = 256>
 struct D16Cfg {
-  static constexpr int BM = 256, BN = 256, BK = 32;
+  static constexpr int BM = BM_, BN = BN_, BK = 32;
   static constexpr int NW = WM * WN, NT = 64 * NW;
   static constexpr int TM = BM / WM, TN = BN / WN;  // wave block
   static constexpr int FM = TM / 16, FN = TN / 16;  // 16x16 fragments
@@ -752,7 +765,7 @@ struct D16Cfg {
   static constexpr int LPW = A_LPW + B_LPW;
   static constexpr int A_CH = RA / 16, A_RPL = 1024 / RA;  // chunks per A row, A rows per load
   static constexpr int B_CH = RB / 16, B_RPL = 1024 / RB;
-  static_assert(NS >= 3 && NS <= 5 && NS * STAGE <= 160 * 1024, "LDS ring");
+  static_assert(NS >= 4 && NS <= 9 && NS * STAGE <= 160 * 1024, "LDS ring");
   static_assert((NS - 3) * LPW < 64, "vmcnt range");
   static_assert(A_LPW >= 1 && B_LPW >= 1 && FM >= 1 && FN >= 1, "tile split");
 };
@@ -772,12 +785,31 @@ __device__ __forceinline__ void interleave_rows16() {
 }
 __device__ __forceinline__ int swz_b16(int k) { return 2 * ((k & 3) | (((k >> 3) & 1) << 2)); }
 
-template <int NS, int WM, int WN>
+// Steps I .. P-1 of a period of the K loop: stage I % NS, parity I % 2.
+template <int NS, int P, int I = 0, typename Step>
+__device__ __forceinline__ void step_period(Step& step, int kt) {
+  if constexpr (I < P) {
+    step(kt + I, std::integral_constant<int, I % NS>{}, std::integral_constant<int, I % 2>{});
+    step_period<NS, P, I + 1>(step, kt);
+  }
+}
+// The first n (< P) steps of a period, for the tail of the K loop.
+template <int NS, int P, int I = 0, typename Step>
+__device__ __forceinline__ void step_tail(Step& step, int kt, int n) {
+  if constexpr (I < P - 1) {
+    if (I < n) {
+      step(kt + I, std::integral_constant<int, I % NS>{}, std::integral_constant<int, I % 2>{});
+      step_tail<NS, P, I + 1>(step, kt, n);
+    }
+  }
+}
+
+template <int NS, int WM, int WN, int BM_ = 256, int BN_ = 256>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_dma16_kernel(const uint16_t* __restrict__ A,
                                                                         const uint16_t* __restrict__ B,
                                                                         uint16_t* __restrict__ C, int M, int N,
                                                                         int K, int lda, int ldb, int ldc) {
-  using CF = D16Cfg<NS, WM, WN>;
+  using CF = D16Cfg<NS, WM, WN, BM_, BN_>;
   constexpr int FM = CF::FM, FN = CF::FN, BK = CF::BK;
   extern __shared__ __align__(1024) unsigned char smem[];
 
@@ -906,48 +938,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_dma16_kernel(const 
   read_b(0, 0);
 #pragma unroll
   for (int mf = 0; mf < FM; ++mf) read_a(0, mf);
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  using I4 = std::integral_constant<int, 4>;
-  static_assert(NS == 4 || NS == 5, "unrolled for 4 or 5 stages");
+  // stage kt % NS and parity kt % 2 repeat every P tiles
+  constexpr int P = NS % 2 == 0 ? NS : 2 * NS;
   int kt = 0;
-  if constexpr (NS == 4) {
-    // stage kt % 4 and parity kt % 2 repeat every 4 tiles
-    for (; kt + 4 <= nk; kt += 4) {
-      step(kt, I0{}, I0{});
-      step(kt + 1, I1{}, I1{});
-      step(kt + 2, I2{}, I0{});
-      step(kt + 3, I3{}, I1{});
-    }
-    if (kt < nk) step(kt, I0{}, I0{});
-    if (kt + 1 < nk) step(kt + 1, I1{}, I1{});
-    if (kt + 2 < nk) step(kt + 2, I2{}, I0{});
-  } else {
-    // stage kt % 5 and parity kt % 2 repeat every 10 tiles
-    for (; kt + 10 <= nk; kt += 10) {
-      step(kt, I0{}, I0{});
-      step(kt + 1, I1{}, I1{});
-      step(kt + 2, I2{}, I0{});
-      step(kt + 3, I3{}, I1{});
-      step(kt + 4, I4{}, I0{});
-      step(kt + 5, I0{}, I1{});
-      step(kt + 6, I1{}, I0{});
-      step(kt + 7, I2{}, I1{});
-      step(kt + 8, I3{}, I0{});
-      step(kt + 9, I4{}, I1{});
-    }
-    if (kt < nk) step(kt, I0{}, I0{});
-    if (kt + 1 < nk) step(kt + 1, I1{}, I1{});
-    if (kt + 2 < nk) step(kt + 2, I2{}, I0{});
-    if (kt + 3 < nk) step(kt + 3, I3{}, I1{});
-    if (kt + 4 < nk) step(kt + 4, I4{}, I0{});
-    if (kt + 5 < nk) step(kt + 5, I0{}, I1{});
-    if (kt + 6 < nk) step(kt + 6, I1{}, I0{});
-    if (kt + 7 < nk) step(kt + 7, I2{}, I1{});
-    if (kt + 8 < nk) step(kt + 8, I3{}, I0{});
-  }
+  for (; kt + P <= nk; kt += P) step_period<NS, P>(step, kt);
+  step_tail<NS, P>(step, kt, nk - kt);
   wait_vmcnt<0>();  // no DMA may land in LDS after the workgroup ends
 
   // ---- epilogue: lane holds m = m0 + am + 16 mf, n = n0 + wn*TN + 16 nf + 4 kg + {0..3} ----
@@ -967,14 +962,14 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_dma16_kernel(const 
   }
 }
 
-template <int NS, int WM, int WN>
+template <int NS, int WM, int WN, int BM_ = 256, int BN_ = 256>
 static int launch_dma16(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
                         hipStream_t stream) {
-  using CF = D16Cfg<NS, WM, WN>;
+  using CF = D16Cfg<NS, WM, WN, BM_, BN_>;
   const long long tiles = (long long)((M + CF::BM - 1) / CF::BM) * ((N + CF::BN - 1) / CF::BN);
   if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
   const int smem = NS * CF::STAGE;
-  constexpr auto kern = gemm_bf16_dma16_kernel<NS, WM, WN>;
+  constexpr auto kern = gemm_bf16_dma16_kernel<NS, WM, WN, BM_, BN_>;
   MX_RETURN_IF_HIP(lds_limit_once<kern>(smem));
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CF::NT), smem, stream, (const uint16_t*)A,
                      (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
@@ -1327,6 +1322,10 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   // Otherwise: register-staged kernels, big tiles when they still cover the
   // 256 CUs twice, else smaller tiles for parallelism.
   if (tiles256 >= 512) return mx::gemm::launch<256, 256, 2, 4>(A, B, C, M, N, K, lda, ldb, ldc, s);
+  // At least one 128x128 tile per CU and whole K tiles: the direct-load
+  // kernel on 128x128 tiles, whose 16 KB stages allow a deeper ring.
+  if (tiles128 >= 256 && K % MX_BF16_BK == 0 && (long long)lda * 2 * 128 <= 0xffffffffLL)
+    return mx::gemm::launch_dma16<MX_BF16_D128_NS, 2, MX_BF16_D128_WN, 128, 128>(A, B, C, M, N, K, lda, ldb, ldc, s);
   if (tiles128 >= 256) return mx::gemm::launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
   // About one 64x64 tile per CU or fewer and a long K (e.g. 1024^3): split
   // K between two wave groups of each workgroup.

@@ -136,13 +136,34 @@ def test_target_size_sampled(ops):
     assert np.abs(got - ref).max() / scale <= TOL
 
 
-@pytest.mark.parametrize("mnk,path", [((2048, 2048, 2048), "register-staged 128x128 (tiles128 >= 256)"),
+@pytest.mark.parametrize("mnk,path", [((2048, 2048, 2048), "128x128 tiles, 64 K tiles"),
+                                      ((2000, 2040, 2048), "ragged M and N"),
+                                      ((3072, 3072, 1024), "576 tiles: more than one round of workgroups"),
+                                      ((2048, 2048, 32), "one K tile, fewer than the ring's stages"),
+                                      ((2048, 2048, 160), "five K tiles: only the loop tail"),
+                                      ((2048, 4096, 1056), "33 K tiles: five ring periods and a tail of three"),
+                                      ((4080, 2056, 256), "ragged, 544 tiles")])
+def test_direct_load_128_paths(ops, mnk, path):
+    """Mid-size GEMMs (at least one 128x128 tile per CU, fewer than one
+    256x256 tile per CU, K % 32 == 0) run the direct-load 16x16x32 kernel on
+    128x128 tiles with a 6-stage ring.  2048^3 is a size of the reference's
+    mixed-dtype harness sweep (cutile-matmul-tiled-mixed/main.py:60)."""
+    m, n, k = mnk
+    announce(f"gemm_bf16 {m}x{n}x{k} direct-load 128x128 ({path})")
+    a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
+    c = run(ops, a, b)
+    ref = ogemm.gemm_ref(a, b)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+
+
+@pytest.mark.parametrize("mnk,path", [((2048, 2048, 2056), "register-staged 128x128 (tiles128 >= 256, K % 32 != 0)"),
                                       ((4096, 8192, 264), "register-staged 256x256 (tiles256 >= 512, K % 32 != 0)"),
                                       ((2048, 2048, 72), "register-staged 128x128, K tail of 8")])
 def test_register_staged_paths(ops, mnk, path):
-    """Single GEMMs that land on the register-staged 128x128 and 256x256
-    kernels (and their one-stage-ahead load loop): 2048^3 is also a size of
-    the reference's mixed-dtype harness sweep (cutile-matmul-tiled-mixed/main.py:60)."""
+    """Single GEMMs whose K is not a multiple of 32 land on the
+    register-staged 128x128 and 256x256 kernels (zero-filled K tail)."""
     m, n, k = mnk
     announce(f"gemm_bf16 {m}x{n}x{k} {path}")
     a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
