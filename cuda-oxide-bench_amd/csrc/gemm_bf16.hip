@@ -25,8 +25,10 @@
 //    wave owns a (BM/WM) x (BN/WN) sub-tile of 32x32 fragments.
 //  * K advances in 64-deep tiles staged through LDS via registers, double
 //    buffered: the next tile's global loads are in flight while MFMAs
-//    consume the current one; one barrier per K tile.  Ragged K is
-//    zero-filled.
+//    consume the current one; one barrier per K tile.  The loads are
+//    buffer loads: chunks past M, N or K get an out-of-range offset and
+//    read as zero, so edge tiles and the K tail run the same branch-free
+//    code as interior ones.
 //  * A is stored k-contiguous ([BM][64]); B is stored exactly as it sits in
 //    memory ([64][BN], n contiguous) and its k-contiguous MFMA operand is
 //    read with gfx950's transposing LDS read (ds_read_b64_tr_b16), so no
@@ -102,6 +104,23 @@ struct Cfg {
 // (not the MFMAs) sets the time, it runs KS loads in flight per CU.
 // PF = 2 stages the global loads two K tiles ahead in two register sets
 // (the LDS double buffer is unchanged), for the same latency-bound case.
+// Buffer resource over [base, base + 2^31 - 16) for loads whose offsets
+// stay below 2^31; an offset of kOobOffset is out of range and reads zero.
+constexpr uint32_t kOobOffset = 0x7ffffff0u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)kOobOffset, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_ld128(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0);
+}
+// The register-staged kernel's in-range offsets (BM rows of A, BK k-rows of
+// B from a tile's base) stay below that range: leading dimensions up to
+// 4M (A, BM = 256) and 16M (B) elements.
+template <int BM>
+inline bool staged_strides_ok(int lda, int ldb) {
+  return (long long)lda * 2 * BM < (long long)kOobOffset && (long long)ldb * 2 * BK < (long long)kOobOffset;
+}
+
 template <int BM, int BN, int WM, int WN, int KS = 1, int PF = 1>
 __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C, int M,
@@ -132,7 +151,6 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
   const int tm = first_m + (id % per_group) % gsz;
   const int tn = (id % per_group) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
-  const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
 
   // ---- global -> register staging.  A: chunk q -> row q/8, chunk q%8.
   //      B: chunk q -> k row q/(BN/8), column chunk q%(BN/8). ----
@@ -140,32 +158,27 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
   u32x4 ra[PF][CF::A_CHUNKS], rb[PF][CF::B_CHUNKS];
   constexpr int BCH = BN / 8;
 
+  // Loads go through buffer resources based at the K tile: a chunk past M,
+  // N or K gets an offset past the resource's range and reads as zero, so
+  // every tile, edge or interior, K tail or not, runs the same branch-free
+  // code (the host keeps lda * 2 * BM and ldb * 2 * BK below 2^31).
   auto load_tile = [&](int k0, auto set_tag) {
     constexpr int SET = decltype(set_tag)::value;
-    const bool full = interior && (k0 + BK <= K);  // uniform
+    const __amdgpu_buffer_rsrc_t rs_a = tile_rsrc(A + (size_t)m0 * lda + k0);
+    const __amdgpu_buffer_rsrc_t rs_b = tile_rsrc(B + (size_t)k0 * ldb + n0);
 #pragma unroll
     for (int i = 0; i < CF::A_CHUNKS; ++i) {
       const int q = tid + i * NT;
-      const int gm = m0 + (q >> 3), gk = k0 + (q & 7) * 8;
-      if (full) {
-        ra[SET][i] = ld128(A + (size_t)gm * lda + gk);
-      } else {
-        const bool ok = gm < M && gk < K;
-        const u32x4 x = ld128(A + (size_t)min(gm, M - 1) * lda + min(gk, K - 8));
-        ra[SET][i] = ok ? x : u32x4{0, 0, 0, 0};
-      }
+      const int r = q >> 3, c = (q & 7) * 8;
+      const bool ok = m0 + r < M && k0 + c < K;
+      ra[SET][i] = buffer_ld128(rs_a, ok ? (uint32_t)r * (uint32_t)lda * 2u + 2u * c : kOobOffset);
     }
 #pragma unroll
     for (int i = 0; i < CF::B_CHUNKS; ++i) {
       const int q = tid + i * NT;
-      const int gk = k0 + q / BCH, gn = n0 + (q % BCH) * 8;
-      if (full) {
-        rb[SET][i] = ld128(B + (size_t)gk * ldb + gn);
-      } else {
-        const bool ok = gk < K && gn < N;
-        const u32x4 x = ld128(B + (size_t)min(gk, K - 1) * ldb + min(gn, N - 8));
-        rb[SET][i] = ok ? x : u32x4{0, 0, 0, 0};
-      }
+      const int r = q / BCH, c = (q % BCH) * 8;
+      const bool ok = k0 + r < K && n0 + c < N;
+      rb[SET][i] = buffer_ld128(rs_b, ok ? (uint32_t)r * (uint32_t)ldb * 2u + 2u * c : kOobOffset);
     }
   };
 
@@ -983,6 +996,7 @@ static int launch(const void* A, const void* B, void* C, int M, int N, int K, in
   using CF = Cfg<BM, BN, WM, WN>;
   const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7fffffffLL || batch > 65535) return MX_ERR_SHAPE;
+  if (!staged_strides_ok<BM>(lda, ldb)) return MX_ERR_SHAPE;
   const size_t smem = (size_t)KS * 2 * CF::LDS_STAGE;
   static_assert(KS * 2 * CF::LDS_STAGE <= 160 * 1024, "double buffers fit in the LDS");
   constexpr auto kern = gemm_bf16_kernel<BM, BN, WM, WN, KS, PF>;
@@ -1373,8 +1387,14 @@ int batched_check(const void* A, const void* B, void* C, int batch, int M, int N
   long long grid = 0;
   switch (batched_path(batch, M, N, K, lda, ldb)) {
     case BatchedPath::SmallM: grid = (long long)batch * ((N + 31) / 32); break;  // widest grid of the three widths
-    case BatchedPath::T128: grid = (long long)((M + 127) / 128) * ((N + 127) / 128); break;
-    case BatchedPath::T64: grid = (long long)((M + 63) / 64) * ((N + 63) / 64); break;
+    case BatchedPath::T128:
+      grid = (long long)((M + 127) / 128) * ((N + 127) / 128);
+      if (!staged_strides_ok<128>(lda, ldb)) return MX_ERR_SHAPE;
+      break;
+    case BatchedPath::T64:
+      grid = (long long)((M + 63) / 64) * ((N + 63) / 64);
+      if (!staged_strides_ok<64>(lda, ldb)) return MX_ERR_SHAPE;
+      break;
   }
   return grid > 0x7fffffffLL ? MX_ERR_SHAPE : MX_OK;
 }

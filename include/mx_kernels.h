@@ -56,6 +56,9 @@ const char* mx_version(void);
  * ldc >= N (in elements).  fp32 accumulation, C rounded to bf16 (RNE).
  * Requires K % 8 == 0, N % 8 == 0, lda/ldb/ldc % 8 == 0 and 16-byte aligned
  * pointers; M, N, K otherwise arbitrary (ragged edges are zero-padded).
+ * Shapes that run the register-staged kernel (K % 32 != 0, or small grids)
+ * take lda < 2^30 / BM (BM = 256, 128 or 64 rows per tile, so at least 4M
+ * elements) and ldb < 16M elements; larger strides return MX_ERR_SHAPE.
  * Replaces: cutile-matmul-tc-bf16/main.py:117-118 (ct.launch of the
  * `matmul_bf16` kernel defined at :59-78) and the bf16 row of
  * cutile-matmul-tiled-mixed/main.py:121-130.

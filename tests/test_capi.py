@@ -58,6 +58,8 @@ P = ctypes.c_void_p(0x10000)  # never dereferenced: every call below fails valid
     ((P, P, P, 64, 64, 60, 60, 64, 64, None), _lib.MX_ERR_ALIGN),
     ((P, P, P, 64, 64, 64, 32, 64, 64, None), _lib.MX_ERR_SHAPE),
     ((ctypes.c_void_p(0x10008), P, P, 64, 64, 64, 64, 64, 64, None), _lib.MX_ERR_ALIGN),
+    # register-staged kernel: 64 rows of A at this stride pass its 2^31-byte buffer range
+    ((P, P, P, 64, 64, 64, 20971520, 64, 64, None), _lib.MX_ERR_SHAPE),
 ])
 def test_gemm_bf16_validation(args, code):
     assert _lib.load().mx_gemm_bf16(*args) == code
@@ -139,6 +141,7 @@ def test_gemm_batched_validation():
     assert f(P, P, P, 70000, 64, 64, 64, 64, 64, 64, 0, 0, 0, None) == _lib.MX_ERR_SHAPE
     assert f(P, P, P, 2, 64, 64, 64, 64, 64, 64, -8, 0, 0, None) == _lib.MX_ERR_SHAPE
     assert f(P, P, P, 2, 64, 64, 64, 64, 64, 64, 4, 0, 0, None) == _lib.MX_ERR_ALIGN
+    assert f(P, P, P, 2, 64, 64, 64, 64, 20971520, 64, 0, 0, 0, None) == _lib.MX_ERR_SHAPE  # ldb past the buffer range
 
 
 def test_mla_absorbed_validation():
