@@ -1324,9 +1324,16 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   hipStream_t s = (hipStream_t)stream;
   const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
   const long long tiles128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
-  // At least one 256x256 tile per CU and whole K tiles: the direct-load
-  // kernel (its lane offsets are 32-bit: 256 rows of A must span < 4 GiB).
-  if (tiles256 >= 256 && K % MX_BF16_BK == 0 && (long long)lda * 2 * 256 <= 0xffffffffLL) {
+  // Rounds of 256 workgroups: a round of 256x256 tiles of the direct-load
+  // kernel takes ~2.6 times a round of its 128x128 tiles at the same K
+  // (measured 2.2-3.0 at 2048-4096), so 256x256 also wins below one tile
+  // per CU when 128x128 tiles would need more than 2.6 times the rounds
+  // (3072^3: 69 vs 78 us; 2560^3 stays on 128x128: 48 vs 59 us).
+  const long long r256 = (tiles256 + 255) / 256, r128 = (tiles128 + 255) / 256;
+  const bool big = tiles256 >= 256 || 13 * r256 < 5 * r128;
+  // Whole K tiles: the direct-load kernel (its lane offsets are 32-bit: 256
+  // rows of A must span < 4 GiB).
+  if (big && K % MX_BF16_BK == 0 && (long long)lda * 2 * 256 <= 0xffffffffLL) {
 #if MX_BF16_MFMA16
     return mx::gemm::launch_dma16<MX_BF16_NS, MX_BF16_WM, MX_BF16_WN>(A, B, C, M, N, K, lda, ldb, ldc, s);
 #else

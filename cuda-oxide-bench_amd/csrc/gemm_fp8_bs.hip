@@ -383,6 +383,13 @@ extern "C" int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, con
   if (((uintptr_t)sA | (uintptr_t)sB) & 3) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
   const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
-  if (tiles256 >= 256) return mx::gemm8::launch<256, 256>(A, sA, B, sB, C, M, N, K, s);
+  const long long tiles128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
+  // Rounds of 256 workgroups: a round of 256x256 tiles takes ~2.4 times a
+  // round of 128x128 ones at the same K (measured 1.95-2.55 at 2048-3072),
+  // so the big tile wins unless the small one needs fewer than 2.4 times
+  // its rounds (3072^3: 1 round against 3, 57 vs 72 us; 2560^3: 1 against
+  // 2, 44 vs 38 us).
+  const long long r256 = (tiles256 + 255) / 256, r128 = (tiles128 + 255) / 256;
+  if (tiles256 >= 256 || 12 * r256 < 5 * r128) return mx::gemm8::launch<256, 256>(A, sA, B, sB, C, M, N, K, s);
   return mx::gemm8::launch<128, 128>(A, sA, B, sB, C, M, N, K, s);
 }

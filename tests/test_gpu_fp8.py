@@ -51,12 +51,14 @@ def test_parity_vs_oracle(ops, mnk):
     assert err <= TOL, f"normwise rel err {err:.3e}"
 
 
-@pytest.mark.parametrize("mnk", [(4096, 4096, 128), (4096, 4096, 384), (4000, 4352, 640), (4096, 4112, 256)])
+@pytest.mark.parametrize("mnk", [(4096, 4096, 128), (4096, 4096, 384), (4000, 4352, 640), (4096, 4112, 256),
+                                 (3072, 3072, 1024), (3000, 3056, 640)])
 def test_large_tile_path(ops, mnk):
-    """Shapes on the 256x256 kernel (>= 256 such tiles): one scale block
-    (fewer stages than the ring holds), an odd block count, ragged M and N
-    (N = 4352 and 4112: a partial last column tile, and a last 128-column
-    scale block only 16 wide)."""
+    """Shapes on the 256x256 kernel: >= 256 such tiles, or fewer when 128x128
+    tiles would need more than 2.4 times the rounds of workgroups (3072^3:
+    144 tiles against 576).  One scale block (fewer stages than the ring
+    holds), an odd block count, ragged M and N (N = 4352 and 4112: a partial
+    last column tile, and a last 128-column scale block only 16 wide)."""
     m, n, k = mnk
     announce(f"fp8 256-tile {m}x{n}x{k}")
     a8, sa, b8, sb = inputs.fp8_gemm_inputs(shapes.FP8GemmShape("t", m, n, k))

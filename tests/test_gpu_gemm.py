@@ -138,7 +138,7 @@ def test_target_size_sampled(ops):
 
 @pytest.mark.parametrize("mnk,path", [((2048, 2048, 2048), "128x128 tiles, 64 K tiles"),
                                       ((2000, 2040, 2048), "ragged M and N"),
-                                      ((3072, 3072, 1024), "576 tiles: more than one round of workgroups"),
+                                      ((2560, 2560, 1024), "400 tiles: two rounds of workgroups"),
                                       ((2048, 2048, 32), "one K tile, fewer than the ring's stages"),
                                       ((2048, 2048, 160), "five K tiles: only the loop tail"),
                                       ((2048, 4096, 1056), "33 K tiles: five ring periods and a tail of three"),
@@ -150,6 +150,23 @@ def test_direct_load_128_paths(ops, mnk, path):
     mixed-dtype harness sweep (cutile-matmul-tiled-mixed/main.py:60)."""
     m, n, k = mnk
     announce(f"gemm_bf16 {m}x{n}x{k} direct-load 128x128 ({path})")
+    a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
+    c = run(ops, a, b)
+    ref = ogemm.gemm_ref(a, b)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+
+
+@pytest.mark.parametrize("mnk,path", [((3072, 3072, 1024), "144 tiles of 256x256 against 576 of 128x128"),
+                                      ((3000, 3064, 512), "ragged, 144 tiles"),
+                                      ((3584, 3584, 2048), "196 tiles against 784")])
+def test_direct_load_256_below_one_tile_per_cu(ops, mnk, path):
+    """Fewer than one 256x256 tile per CU still runs the 256x256 direct-load
+    kernel when 128x128 tiles would need more than 2.6 times the rounds of
+    workgroups."""
+    m, n, k = mnk
+    announce(f"gemm_bf16 {m}x{n}x{k} direct-load 256x256 ({path})")
     a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
     c = run(ops, a, b)
     ref = ogemm.gemm_ref(a, b)
