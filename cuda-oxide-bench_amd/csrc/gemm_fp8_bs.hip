@@ -368,6 +368,226 @@ static int launch(const void* A, const float* sA, const void* B, const float* sB
   return MX_OK;
 }
 
+
+// ---------------------------------------------------------------------------
+// Small M (decode batches, M <= 32 MF): the product is a stream of the
+// weights B, and 128x128 tiles would leave most CUs idle (N/128 workgroups).
+//  * A workgroup owns 32 columns of C for all M rows, NW waves; wave w takes
+//    the scale blocks kb = w, w + NW, ... of K, so the workgroups are N/32
+//    and each streams its 32 columns of B once.  Neighbouring column blocks
+//    run on one XCD, where they share B's 128-byte lines in L2.
+//  * Each wave has a private ring of NSL slots, one scale block per slot:
+//    A (32 MF rows x 128 B), B (128 k-rows x 32 B) and the block's scales
+//    (one activation scale per row, the weight scale) by direct loads, so
+//    one vmcnt wait lands all of them and no register is written behind
+//    the compiler's back.  Slots are private, so the block loop has no
+//    barrier; the wave issues block i+NSL-1 before it waits for block i.
+//  * C^T = B^T . A^T on 32x32x64 fp8 MFMAs as in the main kernel: B^T
+//    fragments by ds_read_b64_tr_b8 from 32-byte rows (eight rows fill the
+//    256 banks' width, so a 32-lane phase is conflict free unswizzled), A^T
+//    fragments by two ds_read_b128 from 128-byte rows whose chunk c sits at
+//    c ^ ((m >> 1) & 7).  Two MFMAs build the block's partial, promoted with
+//    one FMA per element: acc += (sA sB) * partial.
+//  * The waves' accumulators meet in LDS at the end; wave i sums the four
+//    result registers of every wave that hold n = 8i + 4(l/32) + {0..3}
+//    and stores them (with 4 waves every register is summed once).
+// ---------------------------------------------------------------------------
+template <int MF, int NW, int NSL>
+struct SmallCfg {
+  static constexpr int A_B = 32 * MF * 128;   // A rows of one scale block
+  static constexpr int B_B = 128 * 32;         // B k-rows of one scale block
+  static constexpr int SA_OFF = A_B + B_B, SB_OFF = SA_OFF + 256;  // 64 row scales, 64 copies of sB
+  static constexpr int SLOT = SB_OFF + 256;
+  static constexpr int A_L = A_B / 1024, B_L = B_B / 1024;
+  static constexpr int VM = A_L + B_L + 2;  // direct loads per block
+  static constexpr int LDS = NW * NSL * SLOT;
+  static_assert(NW == 4 || NW == 8, "waves");
+  static_assert(LDS <= 160 * 1024, "LDS");
+  static_assert((NSL - 1) * VM < 64, "vmcnt range");
+  static_assert(NW * MF * 64 * 16 * 4 <= LDS, "reduction area");
+};
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, in order.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void unroll_n(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    unroll_n<N, I + 1>(f);
+  }
+}
+
+__device__ __forceinline__ int swz_sa(int m) { return (m >> 1) & 7; }
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// As dma16 for 4 bytes per lane: lane i's dword lands at lds_addr + 4 i.
+__device__ __forceinline__ void dma4(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, %0" ::"s"(sbase), "v"(voff), "s"(lds_addr)
+               : "memory", "m0");
+}
+// s_waitcnt vmcnt(N) that also orders memory: no LDS read of the data it
+// waits for is scheduled above it (this kernel has no barrier after it).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_mem() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+#pragma clang diagnostic pop
+
+template <int MF, int NW, int NSL>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_fp8_bs_smallm_kernel(const uint8_t* __restrict__ A,
+                                                                      const float* __restrict__ sA,
+                                                                      const uint8_t* __restrict__ B,
+                                                                      const float* __restrict__ sB,
+                                                                      uint16_t* __restrict__ C, int M, int N,
+                                                                      int K) {
+  using CF = SmallCfg<MF, NW, NSL>;
+  extern __shared__ __align__(1024) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Consecutive 32-column blocks share 128-byte lines of B: keep them on one
+  // XCD (one L2), so each line comes from HBM once.
+  const int n0 = xcd_remap(blockIdx.x, (N + 31) / 32) * 32;
+  const int kblocks = K / SBK;
+  const int nblocks_n = (N + 127) / 128;
+  const int cnt = kblocks > wave ? (kblocks - wave + NW - 1) / NW : 0;  // this wave's blocks
+  const uint32_t ring = lds_addr(smem) + wave * NSL * CF::SLOT;
+
+  // Direct-load lane offsets.  A load n: rows 8n + l/8, LDS chunk l%8 taking
+  // global chunk (l%8) ^ swz(row); B load n: k-rows 32n + l/2, chunk l%2
+  // (columns past N re-read the last 16 valid ones; never stored).
+  uint32_t a_off[CF::A_L], b_off[CF::B_L];
+#pragma unroll
+  for (int n = 0; n < CF::A_L; ++n) {
+    const int row = 8 * n + (lane >> 3);
+    a_off[n] = (uint32_t)min(row, M - 1) * (uint32_t)K + 16u * ((lane & 7) ^ swz_sa(row));
+  }
+#pragma unroll
+  for (int n = 0; n < CF::B_L; ++n) {
+    const int col = min(n0 + 16 * (lane & 1), N - 16) - n0;
+    b_off[n] = (uint32_t)(32 * n + (lane >> 1)) * (uint32_t)N + col;
+  }
+  // scales: lane l loads the activation scale of row l (rows past M re-read
+  // row M-1) and every lane the one weight scale of this column block
+  const uint32_t sa_off = (uint32_t)min(lane, M - 1) * (uint32_t)kblocks * 4u;
+  const uint32_t sb_off = (uint32_t)(n0 / 128) * 4u;
+  // block i of this wave (kb = wave + NW i; past its last block, the last
+  // one again, or block 0 for a wave without blocks) into slot I = i % NSL
+  auto issue = [&](int i, auto slot_tag) {
+    constexpr int I = decltype(slot_tag)::value;
+    const int kb = cnt > 0 ? wave + NW * min(i, cnt - 1) : 0;
+    const uint32_t st = ring + I * CF::SLOT;
+#pragma unroll
+    for (int n = 0; n < CF::A_L; ++n) dma16(A + (size_t)kb * SBK, a_off[n], st + n * 1024);
+#pragma unroll
+    for (int n = 0; n < CF::B_L; ++n) dma16(B + (size_t)kb * SBK * N + n0, b_off[n], st + CF::A_B + n * 1024);
+    dma4(sA + kb, sa_off, st + CF::SA_OFF);
+    dma4(sB + (size_t)kb * nblocks_n, sb_off, st + CF::SB_OFF);
+  };
+
+  // fragment lane addresses within a slot
+  const int am = lane & 31, ah = lane >> 5;
+  uint32_t a_col[2][2];  // [k step][16-byte half]
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) a_col[st][e] = am * 128 + 16 * ((4 * st + 2 * ah + e) ^ swz_sa(am));
+  const int q = lane >> 4, jj = (lane & 15) >> 1, hh = lane & 1;
+  const uint32_t b_col = CF::A_B + (32 * (q >> 1) + jj) * 32 + 16 * (q & 1) + 8 * hh;
+
+  f32x16 acc[MF];
+#pragma unroll
+  for (int f = 0; f < MF; ++f) acc[f] = f32x16{};
+
+  auto compute = [&](auto slot_tag) {
+    constexpr int I = decltype(slot_tag)::value;
+    const uint32_t st = ring + I * CF::SLOT;
+    i32x8 bt[2], at[2][MF];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      u32x2 v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = lds_read_tr8_at(st + b_col + 64 * s2 * 32 + 8 * r * 32);
+      bt[s2] = i32x8{(int)v[0][0], (int)v[0][1], (int)v[1][0], (int)v[1][1],
+                     (int)v[2][0], (int)v[2][1], (int)v[3][0], (int)v[3][1]};
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const uint32_t r = st + 32 * f * 128;
+        const u32x4 lo = lds_ld128(r + a_col[s2][0]);
+        const u32x4 hi = lds_ld128(r + a_col[s2][1]);
+        at[s2][f] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+    }
+    const float sbv = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+        (uintptr_t)(st + CF::SB_OFF));
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+      const float sav = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+          (uintptr_t)(st + CF::SA_OFF + 4 * (32 * f + am)));
+      f32x16 p = mfma32_fp8(bt[0], at[0][f], f32x16{});
+      p = mfma32_fp8(bt[1], at[1][f], p);
+      acc[f] += (sav * sbv) * p;
+    }
+  };
+
+  land_args(C);
+  // prologue: blocks 0 .. NSL-2 in flight
+  unroll_n<NSL - 1>([&](auto i_tag) { issue(decltype(i_tag)::value, i_tag); });
+
+  // block i: issue block i + NSL - 1 into the slot block i - 1 used, then
+  // wait for block i (the NSL - 1 blocks after it may be in flight)
+  auto step = [&](int i, auto slot_tag) {
+    constexpr int I = decltype(slot_tag)::value;
+    // the previous block's fragment reads have completed before its slot
+    // takes new data
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue(i + NSL - 1, std::integral_constant<int, (I + NSL - 1) % NSL>{});
+    wait_vmcnt_mem<(NSL - 1) * CF::VM>();
+    compute(slot_tag);
+  };
+  int i = 0;
+  for (; i + NSL <= cnt; i += NSL) unroll_n<NSL>([&](auto s_tag) { step(i + decltype(s_tag)::value, s_tag); });
+  unroll_n<NSL - 1>([&](auto s_tag) {
+    if (i + decltype(s_tag)::value < cnt) step(i + decltype(s_tag)::value, s_tag);
+  });
+  wait_vmcnt<0>();  // no DMA may land in the ring once it is reused below
+
+  // ---- accumulators meet in LDS: [wave][f][e][lane] floats ----
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int f = 0; f < MF; ++f)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) red[((wave * MF + f) * 16 + e) * 64 + lane] = acc[f][e];
+  __syncthreads();
+  if (wave < 4) {
+    const int gn = n0 + 8 * wave + 4 * ah;
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] += red[((w * MF + f) * 16 + 4 * wave + j) * 64 + lane];
+      const int gm = 32 * f + am;
+      if (gm < M && gn < N)
+        st64(C + (size_t)gm * N + gn, u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])});
+    }
+  }
+}
+
+template <int MF, int NW, int NSL>
+static int launch_smallm(const void* A, const float* sA, const void* B, const float* sB, void* C, int M, int N, int K,
+                         hipStream_t stream) {
+  using CF = SmallCfg<MF, NW, NSL>;
+  constexpr auto kern = gemm_fp8_bs_smallm_kernel<MF, NW, NSL>;
+  MX_RETURN_IF_HIP(lds_limit_once<kern>(CF::LDS));
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 31) / 32)), dim3(64 * NW), CF::LDS, stream, (const uint8_t*)A, sA,
+                     (const uint8_t*)B, sB, (uint16_t*)C, M, N, K);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
 }  // namespace gemm8
 }  // namespace mx
 
@@ -389,6 +609,12 @@ extern "C" int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, con
   // so the big tile wins unless the small one needs fewer than 2.4 times
   // its rounds (3072^3: 1 round against 3, 57 vs 72 us; 2560^3: 1 against
   // 2, 44 vs 38 us).
+#ifndef MX_FP8_SMALLM_NW
+#define MX_FP8_SMALLM_NW 4
+#endif
+  // Decode-sized M: stream the weights with 32-column workgroups.
+  if (M <= 32) return mx::gemm8::launch_smallm<1, MX_FP8_SMALLM_NW, 4>(A, sA, B, sB, C, M, N, K, s);
+  if (M <= 64) return mx::gemm8::launch_smallm<2, MX_FP8_SMALLM_NW, 3>(A, sA, B, sB, C, M, N, K, s);
   const long long r256 = (tiles256 + 255) / 256, r128 = (tiles128 + 255) / 256;
   if (tiles256 >= 256 || 12 * r256 < 5 * r128) return mx::gemm8::launch<256, 256>(A, sA, B, sB, C, M, N, K, s);
   return mx::gemm8::launch<128, 128>(A, sA, B, sB, C, M, N, K, s);

@@ -51,6 +51,23 @@ def test_parity_vs_oracle(ops, mnk):
     assert err <= TOL, f"normwise rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("mnk", [(1, 7168, 4096), (16, 16, 128), (32, 4096, 7168), (5, 2064, 1152), (33, 512, 1024),
+                                 (64, 2048, 7168), (48, 272, 640), (20, 4112, 2944)])
+def test_small_m_path(ops, mnk):
+    """M <= 64 (decode batches) runs the weight-streaming kernel: 32-column
+    workgroups, scale blocks split over the waves.  Single rows, N not a
+    multiple of 32 (a last block 16 wide), fewer scale blocks than waves
+    (K = 128), block counts that do not divide by the wave count, and both
+    the one- and two-fragment (M > 32) variants."""
+    m, n, k = mnk
+    announce(f"fp8 small-M {m}x{n}x{k}")
+    a8, sa, b8, sb = inputs.fp8_gemm_inputs(shapes.FP8GemmShape("t", m, n, k))
+    c = run(ops, a8, sa, b8, sb)
+    ref = ofp8.gemm_fp8_bs_ref_torch(a8, sa, b8, sb)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+
+
 @pytest.mark.parametrize("mnk", [(4096, 4096, 128), (4096, 4096, 384), (4000, 4352, 640), (4096, 4112, 256),
                                  (3072, 3072, 1024), (3000, 3056, 640)])
 def test_large_tile_path(ops, mnk):
