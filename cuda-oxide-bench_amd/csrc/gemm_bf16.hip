@@ -20,6 +20,9 @@
 // one 256x256 tile per CU, K % 32 == 0, e.g. 2048^3): the same design with
 // 8 waves of 64x32 and a 6-stage ring of 16 KB stages.
 //
+// gemm_bf16_stream_kernel (M <= 64, N >= 256, K % 64 == 0): decode-sized
+// products stream B through 32-column workgroups whose waves split K.
+//
 // gemm_bf16_kernel (everything else: small or ragged-K problems):
 //  * One workgroup computes a BM x BN tile of C with WM x WN waves; each
 //    wave owns a (BM/WM) x (BN/WN) sub-tile of 32x32 fragments.
@@ -1311,6 +1314,164 @@ static int launch_smallm(const void* A, const void* B, void* C, int batch, int M
   return MX_OK;
 }
 
+
+// ---------------------------------------------------------------------------
+// gemm_bf16_stream_kernel: single products with small M (decode batches,
+// M <= 32 MF) stream the weights B.  Tiles of 64 or more rows would leave
+// most CUs idle or re-read B per row block.
+//  * A workgroup owns 32 columns of C for all M rows, NW waves; wave w takes
+//    the 64-deep K blocks kb = w, w + NW, ..., so the workgroups are N/32
+//    and each streams its 32 columns of B once.  Neighbouring column blocks
+//    run on one XCD, where they share B's 128-byte lines in L2.
+//  * Each wave has a private ring of NSL slots, one K block per slot (A: 32 MF
+//    rows x 128 B, chunk c at c ^ ((m >> 1) & 7); B: 64 k-rows x 64 B), by
+//    direct loads; slots are private, so the block loop has no barrier.
+//  * C^T = B^T . A^T on 32x32x16 MFMAs: B^T fragments by transposing reads
+//    from the 64-byte B rows (a 32-lane phase covers 4 rows x 64 B, conflict
+//    free unswizzled), A^T fragments by ds_read_b128.
+//  * The waves' accumulators meet in LDS at the end; wave i sums and stores
+//    the four result registers holding n = 8i + 4(l/32) + {0..3}.
+// ---------------------------------------------------------------------------
+template <int MF, int NW, int NSL>
+struct StreamCfg {
+  static constexpr int A_B = 32 * MF * 128;  // 64 k of 32 MF rows
+  static constexpr int B_B = 64 * 64;         // 64 k-rows of 32 columns
+  static constexpr int SLOT = A_B + B_B;
+  static constexpr int A_L = A_B / 1024, B_L = B_B / 1024;
+  static constexpr int VM = A_L + B_L;
+  static constexpr int LDS = NW * NSL * SLOT;
+  static_assert(NW == 4, "one reducing wave per result register quad");
+  static_assert(LDS <= 160 * 1024, "LDS");
+  static_assert((NSL - 1) * VM < 64, "vmcnt range");
+  static_assert(NW * MF * 64 * 16 * 4 <= LDS, "reduction area");
+};
+__device__ __forceinline__ int swz_s(int m) { return (m >> 1) & 7; }
+// f(integral_constant<int, I>) for I = 0 .. N-1, in order.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void unroll_n(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    unroll_n<N, I + 1>(f);
+  }
+}
+
+template <int MF, int NW, int NSL>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_bf16_stream_kernel(const uint16_t* __restrict__ A,
+                                                                    const uint16_t* __restrict__ B,
+                                                                    uint16_t* __restrict__ C, int M, int N, int K,
+                                                                    int lda, int ldb, int ldc) {
+  using CF = StreamCfg<MF, NW, NSL>;
+  extern __shared__ __align__(1024) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = xcd_remap(blockIdx.x, (N + 31) / 32) * 32;
+  const int kblocks = K / 64;
+  const int cnt = kblocks > wave ? (kblocks - wave + NW - 1) / NW : 0;
+  const uint32_t ring = lds_addr(smem) + wave * NSL * CF::SLOT;
+
+  // A load n: rows 8n + l/8, LDS chunk l%8 taking global chunk (l%8) ^
+  // swz(row) (rows past M re-read row M-1); B load n: k-rows 16n + l/4,
+  // chunk l%4 (columns past N re-read the last 8 valid ones; never stored).
+  uint32_t a_off[CF::A_L], b_off[CF::B_L];
+#pragma unroll
+  for (int n = 0; n < CF::A_L; ++n) {
+    const int row = 8 * n + (lane >> 3);
+    a_off[n] = (uint32_t)min(row, M - 1) * (uint32_t)lda * 2u + 16u * ((lane & 7) ^ swz_s(row));
+  }
+#pragma unroll
+  for (int n = 0; n < CF::B_L; ++n) {
+    const int col = min(n0 + 8 * (lane & 3), N - 8) - n0;
+    b_off[n] = (uint32_t)(16 * n + (lane >> 2)) * (uint32_t)ldb * 2u + 2u * col;
+  }
+  auto issue = [&](int i, auto slot_tag) {
+    constexpr int I = decltype(slot_tag)::value;
+    const int kb = cnt > 0 ? wave + NW * min(i, cnt - 1) : 0;
+    const uint32_t st = ring + I * CF::SLOT;
+#pragma unroll
+    for (int n = 0; n < CF::A_L; ++n) dma16(A + (size_t)kb * 64, a_off[n], st + n * 1024);
+#pragma unroll
+    for (int n = 0; n < CF::B_L; ++n) dma16(B + (size_t)kb * 64 * ldb + n0, b_off[n], st + CF::A_B + n * 1024);
+  };
+
+  // fragment lane addresses within a slot.  A^T (B operand): row am, chunk
+  // 2 ks + g.  B^T (A operand): lane 16G + 4j + a reads k-row 8 (G>>1) +
+  // 4 r + j (+16 ks), columns 16 (G&1) + 4a .. +3.
+  const int am = lane & 31, g = lane >> 5;
+  uint32_t a_col[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) a_col[ks] = am * 128 + 16 * ((2 * ks + g) ^ swz_s(am));
+  const int G = lane >> 4, bj = (lane >> 2) & 3, ba = lane & 3;
+  const uint32_t b_col = CF::A_B + (8 * (G >> 1) + bj) * 64 + 32 * (G & 1) + 8 * ba;
+
+  f32x16 acc[MF];
+#pragma unroll
+  for (int f = 0; f < MF; ++f) acc[f] = f32x16{};
+
+  auto compute = [&](auto slot_tag) {
+    constexpr int I = decltype(slot_tag)::value;
+    const uint32_t st = ring + I * CF::SLOT;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x2 lo = lds_read_tr16_at(st + b_col + 16 * ks * 64);
+      const u32x2 hi = lds_read_tr16_at(st + b_col + 16 * ks * 64 + 4 * 64);
+      const u32x4 bt{lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+      for (int f = 0; f < MF; ++f) acc[f] = mfma32<BF16>(bt, lds_ld128(st + 32 * f * 128 + a_col[ks]), acc[f]);
+    }
+  };
+
+  land_args(C);
+  unroll_n<NSL - 1>([&](auto i_tag) { issue(decltype(i_tag)::value, i_tag); });
+  // block i: issue block i + NSL - 1 into the slot block i - 1 used (its
+  // reads completed), then wait for block i
+  auto step = [&](int i, auto slot_tag) {
+    constexpr int I = decltype(slot_tag)::value;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue(i + NSL - 1, std::integral_constant<int, (I + NSL - 1) % NSL>{});
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NSL - 1) * CF::VM) : "memory");
+    compute(slot_tag);
+  };
+  int i = 0;
+  for (; i + NSL <= cnt; i += NSL) unroll_n<NSL>([&](auto s_tag) { step(i + decltype(s_tag)::value, s_tag); });
+  unroll_n<NSL - 1>([&](auto s_tag) {
+    if (i + decltype(s_tag)::value < cnt) step(i + decltype(s_tag)::value, s_tag);
+  });
+  wait_vmcnt<0>();  // no DMA may land in the ring once it is reused below
+
+  // ---- accumulators meet in LDS: [wave][f][e][lane] floats ----
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int f = 0; f < MF; ++f)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) red[((wave * MF + f) * 16 + e) * 64 + lane] = acc[f][e];
+  __syncthreads();
+  const int gn = n0 + 8 * wave + 4 * g;
+#pragma unroll
+  for (int f = 0; f < MF; ++f) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] += red[((w * MF + f) * 16 + 4 * wave + j) * 64 + lane];
+    const int gm = 32 * f + am;
+    if (gm < M && gn < N)
+      st64(C + (size_t)gm * ldc + gn, u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])});
+  }
+}
+
+template <int MF, int NSL>
+static int launch_stream(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
+                         hipStream_t stream) {
+  using CF = StreamCfg<MF, 4, NSL>;
+  constexpr auto kern = gemm_bf16_stream_kernel<MF, 4, NSL>;
+  MX_RETURN_IF_HIP(lds_limit_once<kern>(CF::LDS));
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 31) / 32)), dim3(256), CF::LDS, stream, (const uint16_t*)A,
+                     (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
 }  // namespace gemm
 }  // namespace mx
 
@@ -1322,6 +1483,18 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   if ((K % 8) || (N % 8) || (lda % 8) || (ldb % 8) || (ldc % 8)) return MX_ERR_ALIGN;
   if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
+#ifndef MX_BF16_STREAM
+#define MX_BF16_STREAM 1
+#endif
+#if MX_BF16_STREAM
+  // Decode-sized M against at least 256 columns, whole 64-deep K blocks:
+  // stream the weights (32-bit lane offsets: 64 rows of A and 64 k-rows of
+  // B span < 4 GiB).
+  if (M <= 64 && N >= 256 && K % 64 == 0 && (long long)lda * 2 * 64 <= 0xffffffffLL &&
+      (long long)ldb * 2 * 64 <= 0xffffffffLL)
+    return M <= 32 ? mx::gemm::launch_stream<1, 4>(A, B, C, M, N, K, lda, ldb, ldc, s)
+                   : mx::gemm::launch_stream<2, 3>(A, B, C, M, N, K, lda, ldb, ldc, s);
+#endif
   const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
   const long long tiles128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
   // Rounds of 256 workgroups: a round of 256x256 tiles of the direct-load

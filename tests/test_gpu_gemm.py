@@ -158,6 +158,23 @@ def test_direct_load_128_paths(ops, mnk, path):
     assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
 
 
+@pytest.mark.parametrize("mnk", [(1, 7168, 4096), (16, 4096, 7168), (32, 256, 64), (33, 1000, 192), (64, 2048, 7168),
+                                 (7, 296, 640), (48, 3000, 1344)])
+def test_weight_streaming_small_m(ops, mnk):
+    """M <= 64 against at least 256 columns with whole 64-deep K blocks runs
+    the weight-streaming kernel: single rows, one K block (fewer than the
+    waves), the two-fragment variant (M > 32), a last column block 8 or 24
+    wide, block counts that do not divide by the wave count."""
+    m, n, k = mnk
+    announce(f"gemm_bf16 {m}x{n}x{k} weight streaming")
+    a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
+    c = run(ops, a, b)
+    ref = ogemm.gemm_ref(a, b)
+    err = normwise_rel_err(c, ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+
+
 @pytest.mark.parametrize("mnk,path", [((3072, 3072, 1024), "144 tiles of 256x256 against 576 of 128x128"),
                                       ((3000, 3064, 512), "ragged, 144 tiles"),
                                       ((3584, 3584, 2048), "196 tiles against 784")])
