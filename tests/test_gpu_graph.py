@@ -58,7 +58,7 @@ def _cuda(*ts):
     return [t.cuda() for t in ts]
 
 
-@pytest.mark.parametrize("mnk", [(1024, 1024, 1024), (200, 264, 520), (2048, 2048, 256)])
+@pytest.mark.parametrize("mnk", [(1024, 1024, 1024), (200, 264, 520), (2048, 2048, 256), (16, 4096, 1024), (3072, 3072, 256)])
 def test_gemm_bf16(ops, mnk):
     m, n, k = mnk
     announce(f"graph gemm_bf16 {m}x{n}x{k}")
@@ -78,10 +78,12 @@ def test_gemm_bf16_batched(ops, bmnk):
     check_graph("gemm_bf16_batched", lambda: ops.gemm_bf16_batched(a, b, out=c), [c])
 
 
-def test_gemm_fp8(ops):
-    announce("graph gemm_fp8_bs 512x512x1024")
-    a8, sa, b8, sb = _cuda(*inputs.fp8_gemm_inputs(shapes.FP8GemmShape("t", 512, 512, 1024)))
-    c = torch.empty((512, 512), dtype=torch.bfloat16, device="cuda")
+@pytest.mark.parametrize("mnk", [(512, 512, 1024), (32, 2048, 1024)])
+def test_gemm_fp8(ops, mnk):
+    m, n, k = mnk
+    announce(f"graph gemm_fp8_bs {m}x{n}x{k}")
+    a8, sa, b8, sb = _cuda(*inputs.fp8_gemm_inputs(shapes.FP8GemmShape("t", m, n, k)))
+    c = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
     check_graph("gemm_fp8_bs", lambda: ops.gemm_fp8_bs(a8, sa, b8, sb, out=c), [c])
 
 
