@@ -20,8 +20,10 @@
 // one 256x256 tile per CU, K % 32 == 0, e.g. 2048^3): the same design with
 // 8 waves of 64x32 and a 6-stage ring of 16 KB stages.
 //
-// gemm_bf16_stream_kernel (M <= 64, N >= 256, K % 64 == 0): decode-sized
-// products stream B through 32-column workgroups whose waves split K.
+// gemm_bf16_stream_kernel (K % 64 == 0; M <= 64 and N >= 256, or at most 64
+// tiles of 64x64 and K >= 512): products too small to fill the CUs with
+// tiles stream B through workgroups of 32 columns x 32 or 64 rows whose
+// waves split K.
 //
 // gemm_bf16_kernel (everything else: small or ragged-K problems):
 //  * One workgroup computes a BM x BN tile of C with WM x WN waves; each
@@ -1316,13 +1318,14 @@ static int launch_smallm(const void* A, const void* B, void* C, int batch, int M
 
 
 // ---------------------------------------------------------------------------
-// gemm_bf16_stream_kernel: single products with small M (decode batches,
-// M <= 32 MF) stream the weights B.  Tiles of 64 or more rows would leave
-// most CUs idle or re-read B per row block.
-//  * A workgroup owns 32 columns of C for all M rows, NW waves; wave w takes
-//    the 64-deep K blocks kb = w, w + NW, ..., so the workgroups are N/32
-//    and each streams its 32 columns of B once.  Neighbouring column blocks
-//    run on one XCD, where they share B's 128-byte lines in L2.
+// gemm_bf16_stream_kernel: products with few tiles (decode batches, small
+// M or N with a long K) stream the weights B.  Tiles of 64 or more rows
+// would leave most CUs idle.
+//  * A workgroup owns 32 columns x 32 MF rows of C, NW waves; wave w takes
+//    the 64-deep K blocks kb = w, w + NW, ..., so every workgroup streams its
+//    32 columns of B once.  The row chunks of a column block and the
+//    neighbouring column blocks run on one XCD, where they share B's
+//    128-byte lines in L2.
 //  * Each wave has a private ring of NSL slots, one K block per slot (A: 32 MF
 //    rows x 128 B, chunk c at c ^ ((m >> 1) & 7); B: 64 k-rows x 64 B), by
 //    direct loads; slots are private, so the block loop has no barrier.
@@ -1364,7 +1367,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_bf16_stream_kernel(const uint
   extern __shared__ __align__(1024) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = xcd_remap(blockIdx.x, (N + 31) / 32) * 32;
+  // Workgroup -> (32-column block, chunk of 32 MF rows), the row chunks of a
+  // column block adjacent, so one XCD holds whole column blocks and their
+  // neighbours (which share B's lines in L2).
+  const int nmc = (M + 32 * MF - 1) / (32 * MF);
+  const int wid = xcd_remap(blockIdx.x, (int)gridDim.x);
+  const int n0 = (wid / nmc) * 32, m0 = (wid % nmc) * 32 * MF;
+  A += (size_t)m0 * lda;
+  C += (size_t)m0 * ldc;
+  M -= m0;  // rows of this chunk (more than 32 MF only past the last row read)
   const int kblocks = K / 64;
   const int cnt = kblocks > wave ? (kblocks - wave + NW - 1) / NW : 0;
   const uint32_t ring = lds_addr(smem) + wave * NSL * CF::SLOT;
@@ -1466,7 +1477,9 @@ static int launch_stream(const void* A, const void* B, void* C, int M, int N, in
   using CF = StreamCfg<MF, 4, NSL>;
   constexpr auto kern = gemm_bf16_stream_kernel<MF, 4, NSL>;
   MX_RETURN_IF_HIP(lds_limit_once<kern>(CF::LDS));
-  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 31) / 32)), dim3(256), CF::LDS, stream, (const uint16_t*)A,
+  const long long grid = (long long)((N + 31) / 32) * ((M + 32 * MF - 1) / (32 * MF));
+  if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), CF::LDS, stream, (const uint16_t*)A,
                      (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
@@ -1487,11 +1500,15 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
 #define MX_BF16_STREAM 1
 #endif
 #if MX_BF16_STREAM
-  // Decode-sized M against at least 256 columns, whole 64-deep K blocks:
-  // stream the weights (32-bit lane offsets: 64 rows of A and 64 k-rows of
-  // B span < 4 GiB).
-  if (M <= 64 && N >= 256 && K % 64 == 0 && (long long)lda * 2 * 64 <= 0xffffffffLL &&
-      (long long)ldb * 2 * 64 <= 0xffffffffLL)
+  // Stream the weights with whole 64-deep K blocks (32-bit lane offsets: 64
+  // rows of A and 64 k-rows of B span < 4 GiB) for decode-sized M against
+  // at least 256 columns, and for any product with at most 64 tiles of
+  // 64x64 and K >= 512, which the tiled kernels cannot spread over the CUs
+  // (graph-replayed: 256x512x4096 17.6 -> 9.4 us, 96x512x8192 44.9 -> 14.4
+  // us; 1024^3, 256 such tiles, stays tiled: 8.3 against 10.6 us).
+  const long long tiles64s = (long long)((M + 63) / 64) * ((N + 63) / 64);
+  if (((M <= 64 && N >= 256) || (tiles64s <= 64 && K >= 512)) && K % 64 == 0 &&
+      (long long)lda * 2 * 64 <= 0xffffffffLL && (long long)ldb * 2 * 64 <= 0xffffffffLL)
     return M <= 32 ? mx::gemm::launch_stream<1, 4>(A, B, C, M, N, K, lda, ldb, ldc, s)
                    : mx::gemm::launch_stream<2, 3>(A, B, C, M, N, K, lda, ldb, ldc, s);
 #endif

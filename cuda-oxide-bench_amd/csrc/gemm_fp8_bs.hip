@@ -370,12 +370,13 @@ static int launch(const void* A, const float* sA, const void* B, const float* sB
 
 
 // ---------------------------------------------------------------------------
-// Small M (decode batches, M <= 32 MF): the product is a stream of the
-// weights B, and 128x128 tiles would leave most CUs idle (N/128 workgroups).
-//  * A workgroup owns 32 columns of C for all M rows, NW waves; wave w takes
-//    the scale blocks kb = w, w + NW, ... of K, so the workgroups are N/32
-//    and each streams its 32 columns of B once.  Neighbouring column blocks
-//    run on one XCD, where they share B's 128-byte lines in L2.
+// Small M (decode batches) or few tiles: the product is a stream of the
+// weights B, and 128x128 tiles would leave most CUs idle.
+//  * A workgroup owns 32 columns x 32 MF rows of C, NW waves; wave w takes
+//    the scale blocks kb = w, w + NW, ... of K, so every workgroup streams
+//    its 32 columns of B once.  The row chunks of a column block and the
+//    neighbouring column blocks run on one XCD, where they share B's
+//    128-byte lines in L2.
 //  * Each wave has a private ring of NSL slots, one scale block per slot:
 //    A (32 MF rows x 128 B), B (128 k-rows x 32 B) and the block's scales
 //    (one activation scale per row, the weight scale) by direct loads, so
@@ -445,10 +446,17 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_fp8_bs_smallm_kernel(const ui
   extern __shared__ __align__(1024) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // Consecutive 32-column blocks share 128-byte lines of B: keep them on one
-  // XCD (one L2), so each line comes from HBM once.
-  const int n0 = xcd_remap(blockIdx.x, (N + 31) / 32) * 32;
+  // Workgroup -> (32-column block, chunk of 32 MF rows), the row chunks of a
+  // column block adjacent: consecutive column blocks share 128-byte lines
+  // of B, and one XCD (one L2) then fetches each line from HBM once.
   const int kblocks = K / SBK;
+  const int nmc = (M + 32 * MF - 1) / (32 * MF);
+  const int wid = xcd_remap(blockIdx.x, (int)gridDim.x);
+  const int n0 = (wid / nmc) * 32, m0 = (wid % nmc) * 32 * MF;
+  A += (size_t)m0 * K;
+  sA += (size_t)m0 * kblocks;
+  C += (size_t)m0 * N;
+  M -= m0;  // rows of this chunk (more than 32 MF only past the last row read)
   const int nblocks_n = (N + 127) / 128;
   const int cnt = kblocks > wave ? (kblocks - wave + NW - 1) / NW : 0;  // this wave's blocks
   const uint32_t ring = lds_addr(smem) + wave * NSL * CF::SLOT;
@@ -582,7 +590,9 @@ static int launch_smallm(const void* A, const float* sA, const void* B, const fl
   using CF = SmallCfg<MF, NW, NSL>;
   constexpr auto kern = gemm_fp8_bs_smallm_kernel<MF, NW, NSL>;
   MX_RETURN_IF_HIP(lds_limit_once<kern>(CF::LDS));
-  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 31) / 32)), dim3(64 * NW), CF::LDS, stream, (const uint8_t*)A, sA,
+  const long long grid = (long long)((N + 31) / 32) * ((M + 32 * MF - 1) / (32 * MF));
+  if (grid > 0x7fffffffLL) return MX_ERR_SHAPE;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NW), CF::LDS, stream, (const uint8_t*)A, sA,
                      (const uint8_t*)B, sB, (uint16_t*)C, M, N, K);
   MX_RETURN_IF_HIP(hipGetLastError());
   return MX_OK;
@@ -612,9 +622,14 @@ extern "C" int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, con
 #ifndef MX_FP8_SMALLM_NW
 #define MX_FP8_SMALLM_NW 4
 #endif
-  // Decode-sized M: stream the weights with 32-column workgroups.
+  // Decode-sized M, or at most 64 tiles of 128x128 with M <= 512: stream
+  // the weights with 32-column workgroups (graph-replayed: 256x4096x4096
+  // 27.5 -> 22.5 us, 512x1024x4096 27.4 -> 12.3 us; 1024^3 stays tiled,
+  // 10.6 against 11.8 us).
   if (M <= 32) return mx::gemm8::launch_smallm<1, MX_FP8_SMALLM_NW, 4>(A, sA, B, sB, C, M, N, K, s);
-  if (M <= 64) return mx::gemm8::launch_smallm<2, MX_FP8_SMALLM_NW, 3>(A, sA, B, sB, C, M, N, K, s);
+  const long long tiles128s = (long long)((M + 127) / 128) * ((N + 127) / 128);
+  if (M <= 64 || (tiles128s <= 64 && M <= 512))
+    return mx::gemm8::launch_smallm<2, MX_FP8_SMALLM_NW, 3>(A, sA, B, sB, C, M, N, K, s);
   const long long r256 = (tiles256 + 255) / 256, r128 = (tiles128 + 255) / 256;
   if (tiles256 >= 256 || 12 * r256 < 5 * r128) return mx::gemm8::launch<256, 256>(A, sA, B, sB, C, M, N, K, s);
   return mx::gemm8::launch<128, 128>(A, sA, B, sB, C, M, N, K, s);

@@ -52,10 +52,12 @@ def test_parity_vs_oracle(ops, mnk):
 
 
 @pytest.mark.parametrize("mnk", [(1, 7168, 4096), (16, 16, 128), (32, 4096, 7168), (5, 2064, 1152), (33, 512, 1024),
-                                 (64, 2048, 7168), (48, 272, 640), (20, 4112, 2944)])
+                                 (64, 2048, 7168), (48, 272, 640), (20, 4112, 2944), (256, 512, 4096), (130, 1024, 2048),
+                                 (500, 1008, 1024), (512, 1024, 384)])
 def test_small_m_path(ops, mnk):
-    """M <= 64 (decode batches) runs the weight-streaming kernel: 32-column
-    workgroups, scale blocks split over the waves.  Single rows, N not a
+    """M <= 64 (decode batches), or at most 64 tiles of 128x128 with
+    M <= 512, runs the weight-streaming kernel: workgroups of 32 columns x
+    32 or 64 rows, scale blocks split over the waves.  Single rows, N not a
     multiple of 32 (a last block 16 wide), fewer scale blocks than waves
     (K = 128), block counts that do not divide by the wave count, and both
     the one- and two-fragment (M > 32) variants."""

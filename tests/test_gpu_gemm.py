@@ -47,15 +47,16 @@ def test_parity_vs_oracle(ops, mnk):
     assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
 
 
-@pytest.mark.parametrize("mnk,path", [((64, 64, 4096), "direct-load ring, one tile, 32 K tiles per group"),
-                                      ((256, 1024, 2048), "direct-load ring, 64 tiles"),
+@pytest.mark.parametrize("mnk,path", [((64, 64, 4096), "one tile: weight streaming"),
+                                      ((256, 1024, 2048), "64 tiles: weight streaming"),
                                       ((1024, 1024, 1024), "direct-load ring, 256 tiles (BASELINE configs[0])"),
                                       ((1024, 1024, 576), "K % 128 != 0: register-staged split-K path"),
                                       ((960, 1024, 512), "M % 64 == 0, 240 tiles: direct-load ring")])
 def test_small_grid_paths(ops, mnk, path):
-    """Grids of at most one 64x64 tile per CU with K >= 512: whole tiles and
-    128-deep K chunks run the direct-load ring (two K groups per workgroup
-    summed through LDS), other shapes the register-staged split-K kernel."""
+    """Grids of at most one 64x64 tile per CU with K >= 512: at most 64
+    tiles stream the weights; more, with whole tiles and 128-deep K chunks,
+    run the direct-load ring (two K groups per workgroup summed through
+    LDS), other shapes the register-staged split-K kernel."""
     m, n, k = mnk
     announce(f"gemm_bf16 {m}x{n}x{k} ({path})")
     a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
@@ -159,12 +160,15 @@ def test_direct_load_128_paths(ops, mnk, path):
 
 
 @pytest.mark.parametrize("mnk", [(1, 7168, 4096), (16, 4096, 7168), (32, 256, 64), (33, 1000, 192), (64, 2048, 7168),
-                                 (7, 296, 640), (48, 3000, 1344)])
+                                 (7, 296, 640), (48, 3000, 1344), (256, 512, 4096), (130, 1024, 2048),
+                                 (1000, 96, 1024), (2048, 128, 4096), (96, 512, 8192)])
 def test_weight_streaming_small_m(ops, mnk):
-    """M <= 64 against at least 256 columns with whole 64-deep K blocks runs
-    the weight-streaming kernel: single rows, one K block (fewer than the
-    waves), the two-fragment variant (M > 32), a last column block 8 or 24
-    wide, block counts that do not divide by the wave count."""
+    """M <= 64 against at least 256 columns, or at most 64 tiles of 64x64
+    with K >= 512, with whole 64-deep K blocks runs the weight-streaming
+    kernel: single rows, one K block (fewer than the waves), the
+    two-fragment variant (M > 32) and its chunks of 64 rows (a last chunk of
+    2 or 40 rows), a last column block 8 or 24 wide, block counts that do
+    not divide by the wave count."""
     m, n, k = mnk
     announce(f"gemm_bf16 {m}x{n}x{k} weight streaming")
     a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
