@@ -12,6 +12,8 @@ product (no padding) and `d_v` is 512.  --smoke checks the committed
 golden oracle output (H16, T40) with the bf16 normwise bound 2e-2;
 --bench times B32 H128 T4096 (DeepSeek-V3 shape) with 2 warm-up + 10
 timed launches.  GB/s counts the latent cache read once plus Q and O.
+--batch / --ctx (not in the reference CLI) replace B and T of the bench
+shape, e.g. B1 T32768 for a long-context single sequence.
 
 --mode prefill runs the reference cell's own kernel instead: pre-projected
 multi-head attention over q/k of qk_head_dim and v of d_v
@@ -60,13 +62,17 @@ def run_smoke() -> bool:
     return ok
 
 
-def run_bench(csv_path: str, iters: int) -> None:
+def run_bench(csv_path: str, iters: int, batch: int | None = None, ctx: int | None = None) -> None:
+    import dataclasses
+
     import torch
 
     pkg = H.package()
     ops = pkg.load_ops()
     F = pkg.flops
     s = pkg.shapes.MLA_BASELINE
+    if batch is not None or ctx is not None:
+        s = dataclasses.replace(s, name="custom", batch=batch or s.batch, ctx=ctx or s.ctx)
     print(f"[bench] shape={s.name} B={s.batch} H={s.n_h} T={s.ctx} d_qk={s.d_qk} d_v={s.d_latent}")
     q, kv = (t.cuda() for t in pkg.inputs.mla_inputs(s))
     out = torch.empty((s.batch, s.n_h, s.d_latent), dtype=torch.bfloat16, device="cuda")
@@ -169,6 +175,8 @@ def main() -> int:
     ap.add_argument("--inputs-dir", default=None,
                     help="prefill: replay a fixture set written in the reference's inputs/ layout")
     ap.add_argument("--fixture", default="correctness_mla", help="prefill fixture shape name (mla_<fixture>_*.npy)")
+    ap.add_argument("--batch", type=int, default=None, help="decode --bench: batch size (default 32)")
+    ap.add_argument("--ctx", type=int, default=None, help="decode --bench: context length T (default 4096)")
     args = ap.parse_args()
     if not (args.smoke or args.bench or args.export_cubin):
         args.smoke = True
@@ -185,7 +193,7 @@ def main() -> int:
         if args.mode == "prefill":
             run_prefill_bench(args.csv_out, iters, args.causal, args.dtype)
         else:
-            run_bench(args.csv_out, iters)
+            run_bench(args.csv_out, iters, args.batch, args.ctx)
         print()
     if args.export_cubin:
         lib = importlib.import_module("cuda-oxide-bench_amd._lib")

@@ -449,45 +449,79 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 }
 
 // Merge the per-split softmax states:  o = sum_s w_s o_s / sum_s w_s,
-// w_s = l_s 2^(m_s - max_s m_s), o_s the normalised split output.  One
-// thread per 16 bytes of a (b, 32-head group) partial tile: the adjacent
-// lanes 2p, 2p+1 of one slot, i.e. 4 latent columns of two heads (2048
-// threads, 8 workgroups of 256 per tile), so the merge spreads over the
-// whole GPU with 128-bit loads; the split loop is batched for memory
-// parallelism.
+// w_s = l_s 2^(m_s - max_s m_s), o_s the normalised split output.  An
+// element-thread owns 16 bytes of a (b, 32-head group) partial tile: the
+// adjacent lanes 2p, 2p+1 of one slot, i.e. 4 latent columns of two heads
+// (2048 element-threads per tile), so the merge spreads over the whole GPU
+// with 128-bit loads.  With many splits (small batches) SG threads share an
+// element, each summing one of SG slices of the splits, and their sums meet
+// in LDS: the serial chain of loads per thread stays near nsplit / SG.
 constexpr int CMB_WG = 256;
-constexpr int CMB_PER = VT * 4 * 32 / CMB_WG;  // workgroups per (b, 32-head group) = 8
-constexpr int CMB_MAXS = 64;                    // splits whose (m, l) are staged in LDS (16 KB)
+constexpr int CMB_ET = VT * 4 * 32;  // element-threads per (b, 32-head group) tile = 2048
 
+template <int SG>
+struct CmbCfg {
+  static constexpr int ET = CMB_WG / SG;     // element-threads per workgroup
+  static constexpr int PER = CMB_ET / ET;    // workgroups per tile
+  static constexpr int MAXS = SG == 1 ? 32 : 256;  // most splits; their (m, l) are staged in LDS (8 or 64 KB)
+};
+
+template <int SG>
 __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __restrict__ ws_o,
                                                             const float* __restrict__ ws_ml,
                                                             uint16_t* __restrict__ O, int H, int nsplit) {
+  using CF = CmbCfg<SG>;
   const int HW = (H + HPW - 1) / HPW;
-  const int gi = blockIdx.x / CMB_PER;          // b * HW + hw
-  const int part = blockIdx.x % CMB_PER;
+  const int gi = blockIdx.x / CF::PER;          // b * HW + hw
+  const int part = blockIdx.x % CF::PER;
   const int b = gi / HW, hw = gi % HW;
-  const int idx = part * CMB_WG + threadIdx.x;  // slot * 32 + lane pair
+  const int sg = (int)threadIdx.x / CF::ET;     // split slice
+  const int idx = part * CF::ET + (int)threadIdx.x % CF::ET;  // slot * 32 + lane pair
   const int lp = idx & 31, slot = idx >> 5;
   const int lane0 = 2 * lp;                     // lanes lane0, lane0 + 1
   const int l32 = lane0 & 31, hsel = lane0 >> 5;
   const size_t g0 = (size_t)b * nsplit * HW + hw;  // tile of split 0; split stride HW
   // The (m, l) pairs of the tile's 32 heads for every split (256 B per
-  // split) are read once per workgroup into LDS, not once per thread.
-  __shared__ f32x4 ml_lds[CMB_MAXS * 16];
-  const int nst = min(nsplit, CMB_MAXS);
-  for (int i = threadIdx.x; i < nst * 16; i += CMB_WG)
-    ml_lds[i] = *reinterpret_cast<const f32x4*>(ws_ml + (g0 + (size_t)(i >> 4) * HW) * 64 + 4 * (i & 15));
-  __syncthreads();
-  auto mlv_of = [&](int s) {  // (m, l) of heads l32, l32 + 1 in split s
-    return s < CMB_MAXS ? ml_lds[s * 16 + (l32 >> 1)]
-                        : *reinterpret_cast<const f32x4*>(ws_ml + (g0 + (size_t)s * HW) * 64 + 2 * l32);
-  };
-  float2 mmax{-1e30f, -1e30f};
-  for (int s = 0; s < nsplit; ++s) {
-    const f32x4 x = mlv_of(s);
-    mmax.x = fmaxf(mmax.x, x[0]);
-    mmax.y = fmaxf(mmax.y, x[2]);
+  // split) are read once per workgroup into LDS, eight loads in flight per
+  // thread; the host keeps nsplit <= MAXS.
+  __shared__ f32x4 ml_lds[CF::MAXS * 16];
+  __shared__ float2 mx_part[16][16];  // [split residue mod 16][head pair]: partial maxima
+  const int n4 = nsplit * 16;
+  for (int base = 0; base < n4; base += 8 * CMB_WG) {
+    f32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * CMB_WG + (int)threadIdx.x;
+      if (i < n4) v[u] = *reinterpret_cast<const f32x4*>(ws_ml + (g0 + (size_t)(i >> 4) * HW) * 64 + 4 * (i & 15));
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * CMB_WG + (int)threadIdx.x;
+      if (i < n4) ml_lds[i] = v[u];
+    }
   }
+  __syncthreads();
+  {  // per-head maxima over the splits: 16 threads per head pair
+    const int hp = threadIdx.x & 15, j = threadIdx.x >> 4;
+    float2 m{-1e30f, -1e30f};
+    for (int t = j; t < nsplit; t += 16) {
+      const f32x4 x = ml_lds[t * 16 + hp];
+      m.x = fmaxf(m.x, x[0]);
+      m.y = fmaxf(m.y, x[2]);
+    }
+    mx_part[j][hp] = m;
+  }
+  __syncthreads();
+  auto mlv_of = [&](int t) { return ml_lds[t * 16 + (l32 >> 1)]; };  // (m, l) of heads l32, l32 + 1 in split t
+  float2 mmax{-1e30f, -1e30f};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float2 x = mx_part[j][l32 >> 1];
+    mmax.x = fmaxf(mmax.x, x.x);
+    mmax.y = fmaxf(mmax.y, x.y);
+  }
+  // this thread's slice of the splits
+  const int s0 = (int)(((long long)nsplit * sg) / SG), s1 = (int)(((long long)nsplit * (sg + 1)) / SG);
   f32x4 o0{0.f, 0.f, 0.f, 0.f}, o1{0.f, 0.f, 0.f, 0.f};
   float l0 = 0.f, l1 = 0.f;
   const uint32_t* po = ws_o + g0 * PT_U32 + ((size_t)slot * 64 + lane0) * 2;
@@ -503,8 +537,8 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
                      bf16_bits_to_f32(p[3] & 0xffffu), bf16_bits_to_f32(p[3] >> 16)};
   };
   // Eight splits per batch of loads: all independent, issued together.
-  int s = 0;
-  for (; s + 8 <= nsplit; s += 8) {
+  int s = s0;
+  for (; s + 8 <= s1; s += 8) {
     u32x4 p[8];
     f32x4 mlv[8];
 #pragma unroll
@@ -515,7 +549,29 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc1(p[u], mlv[u]);
   }
-  for (; s < nsplit; ++s) acc1(ld128(po + (size_t)s * sstride), mlv_of(s));
+  for (; s < s1; ++s) acc1(ld128(po + (size_t)s * sstride), mlv_of(s));
+  if constexpr (SG > 1) {
+    // the slices' sums meet in LDS (reusing the (m, l) staging area)
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(ml_lds);  // [sg][10][ET]
+    const int e = (int)threadIdx.x % CF::ET;
+    const float v[10] = {o0[0], o0[1], o0[2], o0[3], o1[0], o1[1], o1[2], o1[3], l0, l1};
+#pragma unroll
+    for (int j = 0; j < 10; ++j) red[(sg * 10 + j) * CF::ET + e] = v[j];
+    __syncthreads();
+    if (sg != 0) return;
+    float t[10];
+#pragma unroll
+    for (int j = 0; j < 10; ++j) {
+      t[j] = 0.f;
+#pragma unroll
+      for (int g = 0; g < SG; ++g) t[j] += red[(g * 10 + j) * CF::ET + e];
+    }
+    o0 = f32x4{t[0], t[1], t[2], t[3]};
+    o1 = f32x4{t[4], t[5], t[6], t[7]};
+    l0 = t[8];
+    l1 = t[9];
+  }
   const int vt = slot >> 2, i = slot & 3;
   const int head0 = hw * HPW + l32;
   const float inv0 = l0 > 0.f ? 1.f / l0 : 0.f, inv1 = l1 > 0.f ? 1.f / l1 : 0.f;
@@ -524,6 +580,13 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
     st64(orow, u32x2{pack_bf16x2(o0[0] * inv0, o0[1] * inv0), pack_bf16x2(o0[2] * inv0, o0[3] * inv0)});
   if (head0 + 1 < H)
     st64(orow + DV, u32x2{pack_bf16x2(o1[0] * inv1, o1[1] * inv1), pack_bf16x2(o1[2] * inv1, o1[3] * inv1)});
+}
+
+// Split slices per merge element: about 32 splits per thread at most.
+inline int combine_sg(int nsplit) { return nsplit >= 128 ? 8 : nsplit >= 64 ? 4 : nsplit >= 32 ? 2 : 1; }
+inline int combine_max_splits(int nsplit) { return combine_sg(nsplit) == 1 ? CmbCfg<1>::MAXS : CmbCfg<8>::MAXS; }
+inline long long combine_grid(int B, int HW, int nsplit) {
+  return (long long)B * HW * (CMB_ET / (CMB_WG / combine_sg(nsplit)));
 }
 
 inline size_t workspace_bytes(int B, int H, int T) {
@@ -539,7 +602,8 @@ static int check_grid(int B, int H, int T) {
   const long long HGB = (H + HPG - 1) / HPG;
   const long long HW = (H + HPW - 1) / HPW;
   const long long grid = (long long)B * HGB * sp.nsplit;
-  if (grid > 0x7fffffffLL || (long long)B * HW * CMB_PER > 0x7fffffffLL) return MX_ERR_SHAPE;
+  if (grid > 0x7fffffffLL || combine_grid(B, (int)HW, sp.nsplit) > 0x7fffffffLL) return MX_ERR_SHAPE;
+  if (sp.nsplit > combine_max_splits(sp.nsplit)) return MX_ERR_SHAPE;  // pick_split keeps nsplit <= 256
   return MX_OK;
 }
 
@@ -559,8 +623,13 @@ static int launch_decode(const void* Q, const void* Qr, int q_ld, int qr_ld, con
                      sp.nsplit, sp.tps, q_ld, qr_ld);
   MX_RETURN_IF_HIP(hipGetLastError());
   if (sp.nsplit > 1) {
-    hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)(B * HW * CMB_PER)), dim3(CMB_WG), 0, s, ws_o, ws_ml,
-                       (uint16_t*)O, H, sp.nsplit);
+    const dim3 cg((unsigned)combine_grid(B, (int)HW, sp.nsplit));
+    switch (combine_sg(sp.nsplit)) {
+      case 1: hipLaunchKernelGGL(mla_combine_kernel<1>, cg, dim3(CMB_WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
+      case 2: hipLaunchKernelGGL(mla_combine_kernel<2>, cg, dim3(CMB_WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
+      case 4: hipLaunchKernelGGL(mla_combine_kernel<4>, cg, dim3(CMB_WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
+      default: hipLaunchKernelGGL(mla_combine_kernel<8>, cg, dim3(CMB_WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
+    }
     MX_RETURN_IF_HIP(hipGetLastError());
   }
   return MX_OK;

@@ -57,6 +57,7 @@ def read_csv(path):
     ("hip-attn-gqa", ["--bench"], GQA, "gpu_ms", 2),
     ("hip-attn-gqa", ["--bench", "--shape", "baseline", "--block-m", "64", "--block-n", "64"], GQA, "gpu_ms", 2),
     ("hip-attn-mla", ["--bench"], MLA, "gpu_ms", 2),
+    ("hip-attn-mla", ["--bench", "--batch", "1", "--ctx", "32768"], MLA, "gpu_ms", 2),
     ("hip-attn-mla", ["--bench", "--mode", "prefill"], MLA, "gpu_ms", 2),
     ("hip-attn-gdn", ["--bench"], GDN, "gpu_us", 2),
     ("hip-attn-gdn", ["--bench", "--shape", "wide"], GDN, "gpu_us", 2),

@@ -67,10 +67,11 @@ def test_mla_prefill_long(ops):
     assert normwise_rel_err(o.cpu()[:, :, rows], ref) <= TOL
 
 
-@pytest.mark.parametrize("bht", [(1, 128, 16384), (2, 16, 65536)])
+@pytest.mark.parametrize("bht", [(1, 128, 16384), (2, 16, 65536), (1, 128, 20000)])
 def test_mla_decode_long(ops, bht):
-    """More than 64 T splits: the merge reads the (m, l) pairs past the 64
-    it stages in LDS from global memory."""
+    """More than 64 T splits (256, 128, 209): the merge gives each output
+    element 4 or 8 threads, each summing one slice of the splits, whose sums
+    meet in LDS; 209 splits make slices of unequal length."""
     B, H, T = bht
     announce(f"long mla_decode B{B} H{H} T{T}")
     nsplit = ops.mla_decode_splits(B, H, T)
