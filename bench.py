@@ -13,8 +13,9 @@ Every other BASELINE config is measured the same way and reported under
   gemm_fp8_8192    fp8 1x128/128x128 block-scaled GEMM 8192^3
   mla_decode       MLA absorbed decode B32 H128 T4096 576/512
   gdn_decode       GDN decode B64 Hk16 Hv32 d128
-and the widened rows (absorbed MLA step, KDA decode, fp8 activation
-quantiser, MLA prefill) without a CPU leg, plus hipblaslt_8192: the
+and the widened rows with theirs (absorbed MLA step, KDA decode, fp8
+activation quantiser on its first 256 rows for the CPU, MLA prefill on 16
+of 128 heads for the CPU), plus hipblaslt_8192: the
 vendor library's bf16 and per-tensor fp8 GEMMs at 8192^3 on the same GPU,
 a labelled reference line.
 
@@ -417,7 +418,8 @@ def case_mla_absorbed(c: Ctx) -> dict:
     shape = c.S.MLA_BASELINE
     q, kv = c.I.mla_inputs(shape)
     kvd = kv.cuda()
-    x = {n: t.cuda() for n, t in c.I.mla_projection_inputs(shape).items()}
+    xh = c.I.mla_projection_inputs(shape)
+    x = {n: t.cuda() for n, t in xh.items()}
     od = torch.empty((shape.batch, shape.n_h, 128), dtype=torch.bfloat16, device="cuda")
     wsa = torch.empty(c.ops.mla_decode_absorbed_workspace_bytes(shape.batch, shape.n_h, shape.ctx) + 256,
                       dtype=torch.uint8, device="cuda")
@@ -426,51 +428,115 @@ def case_mla_absorbed(c: Ctx) -> dict:
                           c.steps, c.warmup)
     # cache + both weights + q_nope/q_rope read once, O written once
     nb = kv.numel() * 2 + sum(x[n].numel() * 2 for n in ("w_uk", "w_uv", "q_nope", "q_rope")) + od.numel() * 2
-    return {"workload": f"mla_decode_absorbed step B{shape.batch} H{shape.n_h} T{shape.ctx} d_nope128 d_v128",
-            "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
-            "note": "one mx_mla_decode_absorbed call: q_nope W_UK, latent decode + combine, o_lat W_UV; "
-                    "bytes: cache, weights, q_nope/q_rope in, O out"}
+    wl = f"mla_decode_absorbed step B{shape.batch} H{shape.n_h} T{shape.ctx} d_nope128 d_v128"
+    rec = {"workload": wl, "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
+           "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl,
+                                "mla_decode_kernel (+ two batched bf16 GEMMs and mla_combine_kernel, one call)"),
+           "note": "one mx_mla_decode_absorbed call: q_nope W_UK, latent decode + combine, o_lat W_UV; "
+                   "bytes: cache, weights, q_nope/q_rope in, O out"}
+    if c.cpu:
+        from oracle import mla as omla
+
+        got = od.cpu()
+        rec["cpu_baseline"] = cpu_leg(lambda: omla.mla_absorbed_ref(xh["q_nope"], xh["q_rope"], kv, xh["w_uk"],
+                                                                    xh["w_uv"], shape.scale), nb, "GB/s",
+                                      f"the whole workload ({shape.batch} sequences x {shape.n_h} heads, "
+                                      f"T={shape.ctx}, both projections)", got=got)
+    del kvd, x, od, wsa
+    return rec
 
 
 def case_kda_decode(c: Ctx) -> dict:
     import torch
 
     shape = c.S.KDA_LARGE
-    x = {n: t.cuda() for n, t in c.I.kda_inputs(shape).items()}
+    xh = c.I.kda_inputs(shape)
+    x = {n: t.cuda() for n, t in xh.items()}
     so = torch.empty_like(x["S_in"])
     od = torch.empty((shape.batch, shape.n_heads, shape.d_v), dtype=torch.float16, device="cuda")
     ms, wall = time_graph(lambda: c.ops.kda_decode(x["q"], x["k"], x["v"], x["g"], x["beta"], x["S_in"],
                                                    S_out=so, o=od), c.steps, c.warmup)
     nb = c.F.kda_decode_bytes(shape)
-    return {"workload": f"kda_decode B{shape.batch} H{shape.n_heads} d{shape.d_k} f16", "unit": "GB/s",
-            "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
-            "frac_hbm_peak": c.F.gbps(nb, ms) / c.F.PEAK_HBM_GBPS}
+    wl = f"kda_decode B{shape.batch} H{shape.n_heads} d{shape.d_k} f16"
+    rec = {"workload": wl, "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
+           "frac_hbm_peak": c.F.gbps(nb, ms) / c.F.PEAK_HBM_GBPS,
+           "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl, "gdn_decode_kernel (KDA gate)")}
+    if c.cpu:
+        from oracle import kda as okda
+        from oracle.metrics import normwise_rel_err
+
+        o_gpu, s_gpu = od.cpu(), so.cpu()
+        leg = cpu_leg(lambda: okda.kda_decode_ref(**xh), nb, "GB/s",
+                      f"the whole workload ({shape.batch}x{shape.n_heads} heads, {shape.d_k}x{shape.d_v} state; "
+                      f"float64 numpy oracle)", got=o_gpu, ref_of=lambda r: r[0])
+        leg["sample"] = leg["sample"].replace("fp32 torch CPU oracle", "float64 numpy CPU oracle")
+        leg["parity_normwise_state_on_sample"] = normwise_rel_err(s_gpu, okda.kda_decode_ref(**xh)[1])
+        rec["cpu_baseline"] = leg
+    del x, so, od
+    return rec
+
+
+QUANT_CPU_ROWS = 256  # rows of the 8192-wide activation the CPU leg quantises
 
 
 def case_quant_fp8_act(c: Ctx) -> dict:
+    import numpy as np
     import torch
 
     m = k = 8192
-    xa = torch.randn((m, k), generator=torch.Generator().manual_seed(c.I.SEED)).to(torch.bfloat16).cuda()
+    xh = torch.randn((m, k), generator=torch.Generator().manual_seed(c.I.SEED)).to(torch.bfloat16)
+    xa = xh.cuda()
     qa = torch.empty((m, k), dtype=torch.float8_e4m3fn, device="cuda")
     sa = torch.empty((m, k // 128), dtype=torch.float32, device="cuda")
     ms, wall = time_graph(lambda: c.ops.quant_fp8_act(xa, q=qa, scales=sa), c.steps, c.warmup)
     nb = c.F.quant_fp8_act_bytes(m, k)
-    return {"workload": f"quant_fp8_act {m}x{k} bf16 -> e4m3 + 1x128 scales", "unit": "GB/s", "mean_ms": ms,
-            "wall_ms": wall, "value": c.F.gbps(nb, ms), "frac_hbm_peak": c.F.gbps(nb, ms) / c.F.PEAK_HBM_GBPS}
+    wl = f"quant_fp8_act {m}x{k} bf16 -> e4m3 + 1x128 scales"
+    rec = {"workload": wl, "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
+           "frac_hbm_peak": c.F.gbps(nb, ms) / c.F.PEAK_HBM_GBPS,
+           "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl, "quant_fp8_act_kernel<BF16>")}
+    if c.cpu:
+        from oracle import fp8 as ofp8
+
+        r = QUANT_CPU_ROWS
+        xs = xh[:r].float().numpy()
+        leg = cpu_leg(lambda: ofp8.quantize_blockwise(xs, (1, 128)), c.F.quant_fp8_act_bytes(r, k), "GB/s",
+                      f"the first {r} of {m} rows ({r}x{k}); numpy oracle")
+        leg["sample"] = leg["sample"].replace("fp32 torch CPU oracle", "numpy CPU oracle")
+        codes, scales = ofp8.quantize_blockwise(xs, (1, 128))
+        leg["codes_bit_exact_on_sample"] = bool(np.array_equal(ofp8.fp8_tensor_codes(qa[:r].cpu()), codes))
+        leg["scales_bit_exact_on_sample"] = bool(np.array_equal(sa[:r].cpu().numpy(), scales))
+        rec["cpu_baseline"] = leg
+    del xa, qa, sa
+    return rec
+
+
+MLA_PREFILL_CPU_HEADS = 16  # heads of 128 the CPU leg computes
 
 
 def case_mla_prefill(c: Ctx) -> dict:
     import torch
 
     shape = c.S.MLA_PREFILL_BENCH
-    q, k, v = (t.cuda() for t in c.I.mla_prefill_inputs(shape, dtype=torch.bfloat16))
+    qh, kh, vh = c.I.mla_prefill_inputs(shape, dtype=torch.bfloat16)
+    q, k, v = qh.cuda(), kh.cuda(), vh.cuda()
     o = torch.empty((shape.batch, shape.n_h, shape.seq, shape.d_v), dtype=torch.bfloat16, device="cuda")
     ms, wall = time_graph(lambda: c.ops.mla_prefill_fwd(q, k, v, out=o), c.steps, c.warmup)
     fl = c.F.mla_attention_flops(shape)
-    return {"workload": f"mla_prefill B{shape.batch} S{shape.seq} H{shape.n_h} qk{shape.qk_head_dim} "
-                        f"v{shape.d_v} bf16 non-causal", "unit": "TFLOPS", "mean_ms": ms, "wall_ms": wall,
-            "value": c.F.tflops(fl, ms), "frac_mfma_peak": c.F.tflops(fl, ms) / c.F.PEAK_BF16_TFLOPS}
+    wl = f"mla_prefill B{shape.batch} S{shape.seq} H{shape.n_h} qk{shape.qk_head_dim} v{shape.d_v} bf16 non-causal"
+    rec = {"workload": wl, "unit": "TFLOPS", "mean_ms": ms, "wall_ms": wall,
+           "value": c.F.tflops(fl, ms), "frac_mfma_peak": c.F.tflops(fl, ms) / c.F.PEAK_BF16_TFLOPS,
+           "roofline": roofline("mfma", fl, ms, c.F.PEAK_BF16_TFLOPS, "TFLOP/s", wl,
+                                "gqa_fwd_kernel<192, 128, BF16, false, 1, 8>")}
+    if c.cpu:
+        from oracle import mla as omla
+
+        hs = list(range(MLA_PREFILL_CPU_HEADS))
+        got = o[:, :len(hs)].cpu()
+        rec["cpu_baseline"] = cpu_leg(lambda: omla.mla_prefill_ref(qh, kh, vh, heads=hs)[:, :len(hs)],
+                                      fl * len(hs) // shape.n_h, "TFLOPS",
+                                      f"{len(hs)} of {shape.n_h} heads (S={shape.seq}, full S x S)", got=got)
+    del q, k, v, o
+    return rec
 
 
 CASES = {
@@ -486,7 +552,8 @@ CASES = {
     "mla_prefill": case_mla_prefill,
     "hipblaslt_8192": case_hipblaslt_8192,
 }
-# the BASELINE.json configs, which carry a roofline block and a CPU leg
+# the BASELINE.json configs; these and the absorbed step, KDA, the
+# quantiser and the prefill carry a roofline block and a CPU leg
 BASELINE_CASES = ("gqa", "gemm_bf16_1024", "gemm_bf16_8192", "gemm_fp8_8192", "mla_decode", "gdn_decode")
 
 
