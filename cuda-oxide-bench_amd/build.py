@@ -90,22 +90,23 @@ def clangxx() -> str:
     return str(Path(hipcc()).resolve().parent.parent / "llvm" / "bin" / "clang++")
 
 
-def build_host_asan(verbose: bool = False) -> Path:
+def build_host_asan(verbose: bool = False, out_dir: Path | None = None) -> Path:
     """Debug variant for host-side checking: every source compiled at -O1
     with AddressSanitizer on the host code only (the gfx950 device code is
-    built as usual, uninstrumented), linked into ``_build_asan/
-    libmxkernels_asan.so`` together with the C-ABI validation driver
-    ``tests/asan/capi_validation.cpp``.  Returns the driver's path; run it
+    built as usual, uninstrumented), linked into ``libmxkernels_asan.so`` in
+    ``out_dir`` (default ``_build_asan/``) together with the C-ABI validation
+    driver ``tests/asan/capi_validation.cpp``.  Returns the driver's path; run it
     with ASAN_OPTIONS=detect_leaks=0 (the HIP runtime keeps allocations
     until exit).  Not the product library: ``build()`` makes that."""
-    ASAN_DIR.mkdir(exist_ok=True)
+    out = Path(out_dir) if out_dir is not None else ASAN_DIR
+    out.mkdir(parents=True, exist_ok=True)
     flags = [f"--offload-arch={ARCH}", "-O1", "-fPIC", "-std=c++17",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer",
              f"-I{INCLUDE}", f"-I{CSRC}", "-Wno-unused-command-line-argument"]
 
     def one(src: Path) -> Path:
-        obj = ASAN_DIR / (src.stem + ".o")
+        obj = out / (src.stem + ".o")
         cmd = [hipcc(), *(["-x", "hip"] if src.suffix == ".cpp" else []), *flags, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
@@ -117,14 +118,14 @@ def build_host_asan(verbose: bool = False) -> Path:
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(len(srcs), max(1, min(8, os.cpu_count() or 1)))) as ex:
         objs = list(ex.map(one, srcs))
-    lib = ASAN_DIR / "libmxkernels_asan.so"
+    lib = out / "libmxkernels_asan.so"
     rocm_lib = Path(hipcc()).resolve().parent.parent / "lib"
-    driver = ASAN_DIR / "capi_validation"
+    driver = out / "capi_validation"
     for cmd in ([clangxx(), "-shared", "-fsanitize=address", "-o", str(lib), *map(str, objs), f"-L{rocm_lib}",
                  "-lamdhip64", f"-Wl,-rpath,{rocm_lib}"],
                 [clangxx(), "-std=c++17", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
-                 f"-I{INCLUDE}", str(ASAN_DRIVER_SRC), "-o", str(driver), f"-L{ASAN_DIR}", "-lmxkernels_asan",
-                 f"-Wl,-rpath,{ASAN_DIR}"]):
+                 f"-I{INCLUDE}", str(ASAN_DRIVER_SRC), "-o", str(driver), f"-L{out}", "-lmxkernels_asan",
+                 f"-Wl,-rpath,{out}"]):
         if verbose:
             print(" ".join(cmd), flush=True)
         proc = subprocess.run(cmd, capture_output=True, text=True)

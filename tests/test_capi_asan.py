@@ -17,7 +17,7 @@ import pytest
 from conftest import import_submodule
 
 
-def test_capi_validation_under_asan():
+def test_capi_validation_under_asan(tmp_path):
     build = import_submodule("build")
     try:
         build.hipcc()
@@ -25,7 +25,7 @@ def test_capi_validation_under_asan():
         pytest.skip("hipcc not available")
     if not os.path.exists(build.clangxx()) and not shutil.which("clang++"):
         pytest.skip("clang++ not available")
-    driver = build.build_host_asan()
+    driver = build.build_host_asan(out_dir=tmp_path)
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0:exitcode=23")
     proc = subprocess.run([str(driver)], capture_output=True, text=True, timeout=120, env=env)
     assert proc.returncode == 0, proc.stdout + proc.stderr
