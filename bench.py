@@ -329,7 +329,8 @@ def case_gemm_fp8_8192(c: Ctx) -> dict:
 
 def case_hipblaslt_8192(c: Ctx) -> dict:
     """The vendor library beside this repo's GEMMs, same box and run: torch.matmul
-    (hipBLASLt) on the bf16 8192^3 inputs of gemm_bf16_8192, and
+    (hipBLASLt) on the bf16 8192^3 inputs of gemm_bf16_8192 and on the
+    1024^3 ones of gemm_bf16_1024, and
     torch._scaled_mm (hipBLASLt fp8, one per-tensor scale each, column-major
     B) at 8192^3.  A reference line, not this repository's kernels: the
     library has no 1x128/128x128 block-scaled fp8 GEMM to compare against."""
@@ -341,6 +342,12 @@ def case_hipblaslt_8192(c: Ctx) -> dict:
     out = torch.empty((shape.m, shape.n), dtype=torch.bfloat16, device="cuda")
     ms_bf16, _ = time_graph(lambda: torch.matmul(ad, bd, out=out), c.steps, c.warmup)
     del ad, bd
+    # the same at configs[0] (1024^3), beside gemm_bf16_1024
+    s0 = c.S.GEMM_PARITY
+    a0, b0 = (t.cuda() for t in c.I.gemm_inputs(s0))
+    out0 = torch.empty((s0.m, s0.n), dtype=torch.bfloat16, device="cuda")
+    ms_1024, _ = time_graph(lambda: torch.matmul(a0, b0, out=out0), c.steps, c.warmup)
+    del a0, b0, out0
     g = torch.Generator().manual_seed(c.I.SEED)
     a8 = torch.randn((shape.m, shape.k), generator=g).to(torch.float8_e4m3fn).cuda()
     b8 = torch.randn((shape.n, shape.k), generator=g).to(torch.float8_e4m3fn).cuda().t()  # column-major [K, N]
@@ -352,6 +359,7 @@ def case_hipblaslt_8192(c: Ctx) -> dict:
             "unit": "TFLOPS", "mean_ms": ms_bf16, "wall_ms": ms_bf16, "value": c.F.tflops(fl, ms_bf16),
             "bf16_tflops": c.F.tflops(fl, ms_bf16), "fp8_per_tensor_tflops": c.F.tflops(fl, ms_fp8),
             "fp8_per_tensor_mean_ms": ms_fp8,
+            "bf16_1024_tflops": c.F.tflops(c.F.gemm_flops(s0), ms_1024), "bf16_1024_mean_ms": ms_1024,
             "note": "vendor library on the same GPU for comparison; not part of this repository's path"}
 
 
