@@ -31,8 +31,10 @@ def test_golden(ops):
     assert normwise_rel_err(o, g["o"]) <= TOL
 
 
+# (1, 20, 8000): 63 splits, merged by 2 thread slices per element, 20 of a
+# 32-head tile; (2, 36, 12000): 125 splits, 4 slices, a second head tile of 4.
 @pytest.mark.parametrize("bht", [(2, 16, 200), (1, 128, 1), (1, 128, 33), (3, 20, 500), (4, 128, 1024),
-                                 (1, 128, 4096), (2, 64, 4100)])
+                                 (1, 128, 4096), (2, 64, 4100), (1, 20, 8000), (2, 36, 12000)])
 def test_parity_vs_oracle(ops, bht):
     B, H, T = bht
     announce(f"mla B{B} H{H} T{T}")
