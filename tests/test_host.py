@@ -59,3 +59,22 @@ def test_inputs_deterministic():
     a2, b2 = inputs.gemm_inputs(shapes.GemmShape("t", 8, 16, 8))
     assert torch.equal(a1, a2) and torch.equal(b1, b2)
     assert a1.float().abs().max() <= 1.0 and a1.float().min() < 0
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """With the kernel library absent the package raises at load time; there
+    is no CPU fallback to route to."""
+    import os
+    import subprocess
+    import sys
+
+    from conftest import REPO_ROOT
+
+    code = ("import importlib, sys; sys.path.insert(0, %r)\n"
+            "pkg = importlib.import_module('cuda-oxide-bench_amd')\n"
+            "try:\n    pkg.load_ops()\nexcept ImportError as e:\n    print('ImportError:', e); sys.exit(3)\n"
+            "sys.exit(0)\n") % str(REPO_ROOT)
+    env = dict(os.environ, MX_KERNELS_LIB=str(tmp_path / "libmxkernels.so"))
+    proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert proc.returncode == 3, proc.stdout + proc.stderr
+    assert "not found" in proc.stdout
