@@ -456,18 +456,25 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 // with 128-bit loads.  With many splits (small batches) SG threads share an
 // element, each summing one of SG slices of the splits, and their sums meet
 // in LDS: the serial chain of loads per thread stays near nsplit / SG.
-constexpr int CMB_WG = 256;
+#ifndef MX_MLA_CMB_WG_MANY
+#define MX_MLA_CMB_WG_MANY 512
+#endif
 constexpr int CMB_ET = VT * 4 * 32;  // element-threads per (b, 32-head group) tile = 2048
 
 template <int SG>
 struct CmbCfg {
-  static constexpr int ET = CMB_WG / SG;     // element-threads per workgroup
+  // Threads per workgroup: with split slices, larger workgroups cover more
+  // output elements each, so fewer of them stage the same (m, l) pairs.
+  static constexpr int WG = SG == 1 ? 256 : MX_MLA_CMB_WG_MANY;
+  static constexpr int ET = WG / SG;         // element-threads per workgroup
   static constexpr int PER = CMB_ET / ET;    // workgroups per tile
   static constexpr int MAXS = SG == 1 ? 32 : 256;  // most splits; their (m, l) are staged in LDS (8 or 64 KB)
+  static constexpr int MXS = WG / 16;        // slices of the splits in the per-head max
+  static_assert(WG % 256 == 0 && WG <= 1024 && CMB_ET % ET == 0, "merge workgroup size");
 };
 
 template <int SG>
-__global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __restrict__ ws_o,
+__global__ __launch_bounds__(CmbCfg<SG>::WG) void mla_combine_kernel(const uint32_t* __restrict__ ws_o,
                                                             const float* __restrict__ ws_ml,
                                                             uint16_t* __restrict__ O, int H, int nsplit) {
   using CF = CmbCfg<SG>;
@@ -485,26 +492,26 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
   // split) are read once per workgroup into LDS, eight loads in flight per
   // thread; the host keeps nsplit <= MAXS.
   __shared__ f32x4 ml_lds[CF::MAXS * 16];
-  __shared__ float2 mx_part[16][16];  // [split residue mod 16][head pair]: partial maxima
+  __shared__ float2 mx_part[CF::MXS][16];  // [split residue mod MXS][head pair]: partial maxima
   const int n4 = nsplit * 16;
-  for (int base = 0; base < n4; base += 8 * CMB_WG) {
+  for (int base = 0; base < n4; base += 8 * CF::WG) {
     f32x4 v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int i = base + u * CMB_WG + (int)threadIdx.x;
+      const int i = base + u * CF::WG + (int)threadIdx.x;
       if (i < n4) v[u] = *reinterpret_cast<const f32x4*>(ws_ml + (g0 + (size_t)(i >> 4) * HW) * 64 + 4 * (i & 15));
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int i = base + u * CMB_WG + (int)threadIdx.x;
+      const int i = base + u * CF::WG + (int)threadIdx.x;
       if (i < n4) ml_lds[i] = v[u];
     }
   }
   __syncthreads();
-  {  // per-head maxima over the splits: 16 threads per head pair
+  {  // per-head maxima over the splits: MXS threads per head pair
     const int hp = threadIdx.x & 15, j = threadIdx.x >> 4;
     float2 m{-1e30f, -1e30f};
-    for (int t = j; t < nsplit; t += 16) {
+    for (int t = j; t < nsplit; t += CF::MXS) {
       const f32x4 x = ml_lds[t * 16 + hp];
       m.x = fmaxf(m.x, x[0]);
       m.y = fmaxf(m.y, x[2]);
@@ -515,7 +522,7 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
   auto mlv_of = [&](int t) { return ml_lds[t * 16 + (l32 >> 1)]; };  // (m, l) of heads l32, l32 + 1 in split t
   float2 mmax{-1e30f, -1e30f};
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < CF::MXS; ++j) {
     const float2 x = mx_part[j][l32 >> 1];
     mmax.x = fmaxf(mmax.x, x.x);
     mmax.y = fmaxf(mmax.y, x.y);
@@ -585,8 +592,11 @@ __global__ __launch_bounds__(CMB_WG) void mla_combine_kernel(const uint32_t* __r
 // Split slices per merge element: about 32 splits per thread at most.
 inline int combine_sg(int nsplit) { return nsplit >= 128 ? 8 : nsplit >= 64 ? 4 : nsplit >= 32 ? 2 : 1; }
 inline int combine_max_splits(int nsplit) { return combine_sg(nsplit) == 1 ? CmbCfg<1>::MAXS : CmbCfg<8>::MAXS; }
+inline int combine_per(int sg) {  // workgroups per (b, 32-head) tile
+  return sg == 1 ? CmbCfg<1>::PER : sg == 2 ? CmbCfg<2>::PER : sg == 4 ? CmbCfg<4>::PER : CmbCfg<8>::PER;
+}
 inline long long combine_grid(int B, int HW, int nsplit) {
-  return (long long)B * HW * (CMB_ET / (CMB_WG / combine_sg(nsplit)));
+  return (long long)B * HW * combine_per(combine_sg(nsplit));
 }
 
 inline size_t workspace_bytes(int B, int H, int T) {
@@ -625,10 +635,10 @@ static int launch_decode(const void* Q, const void* Qr, int q_ld, int qr_ld, con
   if (sp.nsplit > 1) {
     const dim3 cg((unsigned)combine_grid(B, (int)HW, sp.nsplit));
     switch (combine_sg(sp.nsplit)) {
-      case 1: hipLaunchKernelGGL(mla_combine_kernel<1>, cg, dim3(CMB_WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
-      case 2: hipLaunchKernelGGL(mla_combine_kernel<2>, cg, dim3(CMB_WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
-      case 4: hipLaunchKernelGGL(mla_combine_kernel<4>, cg, dim3(CMB_WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
-      default: hipLaunchKernelGGL(mla_combine_kernel<8>, cg, dim3(CMB_WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
+      case 1: hipLaunchKernelGGL(mla_combine_kernel<1>, cg, dim3(CmbCfg<1>::WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
+      case 2: hipLaunchKernelGGL(mla_combine_kernel<2>, cg, dim3(CmbCfg<2>::WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
+      case 4: hipLaunchKernelGGL(mla_combine_kernel<4>, cg, dim3(CmbCfg<4>::WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
+      default: hipLaunchKernelGGL(mla_combine_kernel<8>, cg, dim3(CmbCfg<8>::WG), 0, s, ws_o, ws_ml, (uint16_t*)O, H, sp.nsplit); break;
     }
     MX_RETURN_IF_HIP(hipGetLastError());
   }
