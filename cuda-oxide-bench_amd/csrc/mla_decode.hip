@@ -459,13 +459,16 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 #ifndef MX_MLA_CMB_WG_MANY
 #define MX_MLA_CMB_WG_MANY 512
 #endif
+#ifndef MX_MLA_CMB_WG_ONE
+#define MX_MLA_CMB_WG_ONE 256
+#endif
 constexpr int CMB_ET = VT * 4 * 32;  // element-threads per (b, 32-head group) tile = 2048
 
 template <int SG>
 struct CmbCfg {
   // Threads per workgroup: with split slices, larger workgroups cover more
   // output elements each, so fewer of them stage the same (m, l) pairs.
-  static constexpr int WG = SG == 1 ? 256 : MX_MLA_CMB_WG_MANY;
+  static constexpr int WG = SG == 1 ? MX_MLA_CMB_WG_ONE : MX_MLA_CMB_WG_MANY;
   static constexpr int ET = WG / SG;         // element-threads per workgroup
   static constexpr int PER = CMB_ET / ET;    // workgroups per tile
   static constexpr int MAXS = SG == 1 ? 32 : 256;  // most splits; their (m, l) are staged in LDS (8 or 64 KB)
