@@ -133,19 +133,28 @@ def kda_inputs(s: KDAShape, dtype: torch.dtype = torch.float16, seed: int = KDA_
     """The reference's KDA recipe (cutile-attn-kda/main.py:282-305), restated
     draw for draw on numpy's default_rng: q, k ~ N(0,1)/sqrt(d_k), v ~ N(0,1),
     g = -|N(0,1)|/2 (decay exp(g) in (~0.6, 1]), beta ~ U(0.1, 0.9),
-    S_in ~ 0.1 N(0,1) fp32; the 16-bit inputs are rounded from float32 the
-    way the reference's astype(np.float16) does (round to nearest even).
+    S_in ~ 0.1 N(0,1) fp32.  The draws stay float64 until the one cast to the
+    input type, as the reference's astype(np.float16) does (numpy rounds
+    float64 straight to half, round to nearest even); rounding through
+    float32 first would change a few values per shape.
     Returns dict q, k, g [B,H,dk]; v [B,H,dv]; beta [B,H] in `dtype`; S_in fp32."""
     rng = np.random.default_rng(seed)
     B, Hh, dk, dv = s.batch, s.n_heads, s.d_k, s.d_v
     scale_k = 1.0 / np.sqrt(dk)
-    q = (rng.standard_normal((B, Hh, dk)) * scale_k).astype(np.float32)
-    k = (rng.standard_normal((B, Hh, dk)) * scale_k).astype(np.float32)
-    v = rng.standard_normal((B, Hh, dv)).astype(np.float32)
-    gg = (-np.abs(rng.standard_normal((B, Hh, dk))) * 0.5).astype(np.float32)
-    beta = rng.uniform(0.1, 0.9, size=(B, Hh)).astype(np.float32)
+    q = rng.standard_normal((B, Hh, dk)) * scale_k
+    k = rng.standard_normal((B, Hh, dk)) * scale_k
+    v = rng.standard_normal((B, Hh, dv))
+    gg = -np.abs(rng.standard_normal((B, Hh, dk))) * 0.5
+    beta = rng.uniform(0.1, 0.9, size=(B, Hh))
     S = (rng.standard_normal((B, Hh, dk, dv)) * 0.1).astype(np.float32)
-    t = lambda x: torch.from_numpy(x).to(dtype)  # noqa: E731
+
+    def t(x):
+        if dtype == torch.float16:
+            return torch.from_numpy(x.astype(np.float16))
+        if dtype == torch.float64:
+            return torch.from_numpy(x)
+        return torch.from_numpy(x.astype(np.float32)).to(dtype)
+
     return {"q": t(q), "k": t(k), "v": t(v), "g": t(gg), "beta": t(beta), "S_in": torch.from_numpy(S).contiguous()}
 
 
