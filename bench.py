@@ -30,6 +30,25 @@ runs --settle-ms (default 300) of a plain device GEMM, so the timed steps
 start at load clocks rather than at the clocks of an idle GPU; the JSON
 line reports it under "settle".
 
+Rotated inputs (the HBM-bound cases mla_decode, gdn_decode, kda_decode,
+quant_fp8_act, mla_absorbed): MI355X has a 256 MB Infinity Cache (MALL)
+in front of HBM, and these working sets (67-270 MB) fit in it or sit at
+its edge, so replaying one input set measures partly cache bandwidth.
+Each such case is therefore also timed with R copies of its inputs (and
+outputs), step j of the graph using copy j % R, so that between two
+touches of one copy more than 256 MB of other copies stream through.
+The case's `value` and `roofline` are the rotated figures; the same-buffer
+figure is kept as `hot`.
+
+Parity gate (the reference's rule: a kernel that fails its correctness
+check reports no numbers, analysis/wave15-attention-architecture/reference/
+README.md:47-58): every case's GPU output is compared against the CPU
+oracle, on the whole workload in the CPU leg, or with --no-cpu-baseline on
+a bounded sample (listed under `parity.check`).  Bounds: normwise
+max|got-ref|/max|ref| <= 2e-2 for bf16/fp8 outputs, <= 1e-3 for the fp32
+GDN/KDA state, codes and scales bit-exact for the fp8 quantiser.  If any
+case misses its bound, no JSON line is printed and the exit status is 3.
+
 CPU baseline (BASELINE.md's plan): this repository's CPU oracle (the
 restatement of the reference's CPU implementation, "port") on the same
 seeded inputs, torch fp32 on the host's cores, 1 warm-up + 3 timed runs,
@@ -151,6 +170,121 @@ def time_graph(fn, steps: int, warmup: int):
     return ms, wall_ms
 
 
+def time_graph_rotated(fns, steps: int, warmup: int):
+    """As time_graph, with step j of the captured graph calling fns[j % R]
+    (R input/output copies), so each copy is touched once every R steps."""
+    import torch
+
+    r = len(fns)
+    for j in range(max(warmup, r)):
+        fns[j % r]()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for j in range(steps):
+            fns[j % r]()
+    torch.cuda.synchronize()
+    settle()
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ms = start.elapsed_time(end) / steps
+    del g
+    return ms, wall_ms
+
+
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def rotation_count(bytes_per_set: int) -> int:
+    """Copies R such that the other R-1 copies streamed between two touches
+    of one copy exceed the Infinity Cache at least 1.5 times over."""
+    r = 2
+    while (r - 1) * bytes_per_set < 1.5 * MALL_BYTES:
+        r += 1
+    return r
+
+
+def rotate(rec: dict, fns, set_bytes: int, work: float, c, wl: str, kernel: str) -> None:
+    """Time the case again over rotated copies; the rotated figure becomes the
+    case's value and roofline, the same-buffer one moves to rec["hot"]."""
+    ms, wall = time_graph_rotated(fns, c.steps, c.warmup)
+    rec["hot"] = {"value": rec["value"], "mean_ms": rec["mean_ms"], "wall_ms": rec["wall_ms"],
+                  "roofline": rec["roofline"],
+                  "note": "one input/output set replayed every step (working set can sit in the 256 MB MALL)"}
+    rec["value"] = c.F.gbps(work, ms)
+    rec["mean_ms"], rec["wall_ms"] = ms, wall
+    rec["roofline"] = roofline("hbm", work, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl, kernel)
+    rec["rotated"] = {"sets": len(fns), "bytes_per_set": set_bytes,
+                      "bytes_between_reuse": (len(fns) - 1) * set_bytes,
+                      "note": f"step j reads and writes copy j % {len(fns)}; value and roofline are this figure"}
+
+
+# ---------------------------------------------------------------- parity gate
+OUT_BOUND = 2e-2     # normwise, bf16/fp8 outputs
+STATE_BOUND = 1e-3   # normwise, fp32 GDN/KDA state
+
+
+def parity_record(c, rec: dict, sample_check) -> None:
+    """rec["parity"]: the CPU leg's whole-workload comparison when it ran,
+    else `sample_check()` -> dict of measured errors on a bounded sample."""
+    leg = rec.get("cpu_baseline")
+    if leg is not None:
+        par = {"check": "cpu_baseline sample: " + leg["sample"].split(";")[0]}
+        if "parity_normwise_on_sample" in leg:
+            par["output_normwise"] = leg["parity_normwise_on_sample"]
+        if "parity_normwise_state_on_sample" in leg:
+            par["state_normwise"] = leg["parity_normwise_state_on_sample"]
+        if "codes_bit_exact_on_sample" in leg:
+            par["bit_exact"] = bool(leg["codes_bit_exact_on_sample"] and leg["scales_bit_exact_on_sample"])
+    else:
+        par = sample_check()
+    par["bounds"] = {"output_normwise": OUT_BOUND, "state_normwise": STATE_BOUND}
+    rec["parity"] = par
+
+
+def parity_failures(results: dict) -> list[str]:
+    """Cases whose GPU output misses its bound (or was never checked)."""
+    bad = []
+    for name, rec in results.items():
+        par = rec.get("parity")
+        if par is None:
+            if name != "hipblaslt_8192":  # the vendor reference line computes nothing of this path
+                bad.append(f"{name}: no parity check")
+            continue
+        e = par.get("output_normwise")
+        if e is not None and not e <= OUT_BOUND:
+            bad.append(f"{name}: output normwise {e:.3e} > {OUT_BOUND}")
+        e = par.get("state_normwise")
+        if e is not None and not e <= STATE_BOUND:
+            bad.append(f"{name}: state normwise {e:.3e} > {STATE_BOUND}")
+        if par.get("bit_exact") is False:
+            bad.append(f"{name}: quantised codes/scales not bit-exact")
+        if all(par.get(k) is None for k in ("output_normwise", "state_normwise", "bit_exact")):
+            bad.append(f"{name}: parity check measured nothing")
+    return bad
+
+
+def _nw(got, ref) -> float:
+    from oracle.metrics import normwise_rel_err
+
+    return float(normwise_rel_err(got, ref))
+
+
 # ---------------------------------------------------------------- CPU leg
 def cpu_info() -> str:
     try:
@@ -270,6 +404,15 @@ def case_gqa(c: Ctx) -> dict:
         rec["cpu_baseline"] = cpu_leg(lambda: ogqa.gqa_naive(q, k, v, causal=True), flops, "TFLOPS",
                                       f"the whole workload (all {shape.n_q} query heads, causal S={shape.seq})",
                                       got=got)
+
+    def sample():
+        from oracle import gqa as ogqa
+
+        hs = [0, 13, shape.n_q - 1]
+        return {"check": f"query heads {hs} of {shape.n_q}, full causal S={shape.seq}",
+                "output_normwise": _nw(out.cpu()[:, hs], ogqa.gqa_naive(q, k, v, causal=True, heads=hs)[:, hs])}
+
+    parity_record(c, rec, sample)
     return rec
 
 
@@ -292,6 +435,15 @@ def _gemm_bf16(c: Ctx, shape, name: str) -> dict:
         got = out.cpu()
         rec["cpu_baseline"] = cpu_leg(lambda: ogemm.gemm_ref(a, b), flops, "TFLOPS",
                                       f"the whole {shape.m}x{shape.n}x{shape.k} product", got=got)
+
+    def sample():
+        from oracle import gemm as ogemm
+
+        rows = sorted(set(list(range(32)) + list(range(shape.m - 32, shape.m))))
+        return {"check": f"rows {{0..31, {shape.m - 32}..{shape.m - 1}}} of C, every column",
+                "output_normwise": _nw(out.cpu()[rows], ogemm.gemm_ref(a[rows], b))}
+
+    parity_record(c, rec, sample)
     del ad, bd, out
     return rec
 
@@ -323,6 +475,15 @@ def case_gemm_fp8_8192(c: Ctx) -> dict:
         got = out.cpu()
         rec["cpu_baseline"] = cpu_leg(lambda: ofp8.gemm_fp8_bs_ref_torch(a8, sa, b8, sb), flops, "TFLOPS",
                                       f"the whole {shape.m}^3 product of the dequantised operands", got=got)
+
+    def sample():
+        from oracle import fp8 as ofp8
+
+        rows = list(range(32)) + list(range(shape.m - 32, shape.m))
+        return {"check": f"rows {{0..31, {shape.m - 32}..{shape.m - 1}}} of C, every column",
+                "output_normwise": _nw(out.cpu()[rows], ofp8.gemm_fp8_bs_ref_torch(a8[rows], sa[rows], b8, sb))}
+
+    parity_record(c, rec, sample)
     del a8d, sad, b8d, sbd, out
     return rec
 
@@ -375,10 +536,18 @@ def case_mla_decode(c: Ctx) -> dict:
     ms, wall = time_graph(lambda: c.ops.mla_decode(qd, kvd, shape.scale, out=o, workspace=ws), c.steps, c.warmup)
     nb, fl = c.F.mla_decode_bytes(shape), c.F.mla_decode_flops(shape)
     wl = f"mla_decode absorbed B{shape.batch} H{shape.n_h} T{shape.ctx} 576/512 bf16"
+    kern = "mla_decode_kernel + mla_combine_kernel (one call)"
     rec = {"workload": wl, "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
            "tflops": c.F.tflops(fl, ms), "flops": fl,
-           "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl,
-                                "mla_decode_kernel + mla_combine_kernel (one call)")}
+           "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl, kern)}
+    set_b = (kvd.numel() + qd.numel() + o.numel()) * 2
+    sets = [(qd, kvd, o)] + [(qd.clone(), kvd.clone(), torch.empty_like(o))
+                             for _ in range(rotation_count(set_b) - 1)]
+    rotate(rec, [lambda t=t: c.ops.mla_decode(t[0], t[1], shape.scale, out=t[2], workspace=ws) for t in sets],
+           set_b, nb, c, wl, kern)
+    rec["tflops"] = c.F.tflops(fl, rec["mean_ms"])
+    o = sets[(c.steps - 1) % len(sets)][2]  # the last step's output
+    del sets
     if c.cpu:
         from oracle import mla as omla
 
@@ -386,6 +555,15 @@ def case_mla_decode(c: Ctx) -> dict:
         rec["cpu_baseline"] = cpu_leg(lambda: omla.mla_decode_ref(q, kv, shape.scale), nb, "GB/s",
                                       f"the whole workload ({shape.batch} sequences x {shape.n_h} heads, "
                                       f"T={shape.ctx})", got=got)
+
+    def sample():
+        from oracle import mla as omla
+
+        bs = [0, shape.batch - 1]
+        return {"check": f"sequences {bs} of {shape.batch}, all heads, T={shape.ctx}",
+                "output_normwise": _nw(o.cpu()[bs], omla.mla_decode_ref(q, kv, shape.scale, batches=bs)[bs])}
+
+    parity_record(c, rec, sample)
     del qd, kvd, o, ws
     return rec
 
@@ -405,6 +583,13 @@ def case_gdn_decode(c: Ctx) -> dict:
           f"bf16 q/k/v, fp32 state")
     rec = {"workload": wl, "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
            "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl, "gdn_decode_kernel")}
+    sets = [(xd, so, od)] + [({n: t.clone() for n, t in xd.items()}, torch.empty_like(so), torch.empty_like(od))
+                             for _ in range(rotation_count(nb) - 1)]
+    rotate(rec, [lambda t=t: c.ops.gdn_decode(t[0]["q"], t[0]["k"], t[0]["v"], t[0]["alpha"], t[0]["beta"],
+                                              t[0]["S_in"], S_out=t[1], o=t[2]) for t in sets],
+           nb, nb, c, wl, "gdn_decode_kernel")
+    _, so, od = sets[(c.steps - 1) % len(sets)]
+    del sets
     if c.cpu:
         from oracle import gdn as ogdn
         from oracle.metrics import normwise_rel_err
@@ -416,6 +601,15 @@ def case_gdn_decode(c: Ctx) -> dict:
         ro, rs = ogdn.gdn_decode_ref(**x)
         leg["parity_normwise_state_on_sample"] = normwise_rel_err(s_gpu, rs)
         rec["cpu_baseline"] = leg
+
+    def sample():
+        from oracle import gdn as ogdn
+
+        ro, rs = ogdn.gdn_decode_ref(**x)
+        return {"check": "the whole workload (output and state)", "output_normwise": _nw(od.cpu(), ro),
+                "state_normwise": _nw(so.cpu(), rs)}
+
+    parity_record(c, rec, sample)
     del xd, so, od
     return rec
 
@@ -437,11 +631,18 @@ def case_mla_absorbed(c: Ctx) -> dict:
     # cache + both weights + q_nope/q_rope read once, O written once
     nb = kv.numel() * 2 + sum(x[n].numel() * 2 for n in ("w_uk", "w_uv", "q_nope", "q_rope")) + od.numel() * 2
     wl = f"mla_decode_absorbed step B{shape.batch} H{shape.n_h} T{shape.ctx} d_nope128 d_v128"
+    kern = "mla_decode_kernel (+ two batched bf16 GEMMs and mla_combine_kernel, one call)"
     rec = {"workload": wl, "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
-           "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl,
-                                "mla_decode_kernel (+ two batched bf16 GEMMs and mla_combine_kernel, one call)"),
+           "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl, kern),
            "note": "one mx_mla_decode_absorbed call: q_nope W_UK, latent decode + combine, o_lat W_UV; "
                    "bytes: cache, weights, q_nope/q_rope in, O out"}
+    sets = [(x, kvd, od)] + [({n: t.clone() for n, t in x.items()}, kvd.clone(), torch.empty_like(od))
+                             for _ in range(rotation_count(nb) - 1)]
+    rotate(rec, [lambda t=t: c.ops.mla_decode_absorbed(t[0]["q_nope"], t[0]["q_rope"], t[1], t[0]["w_uk"],
+                                                       t[0]["w_uv"], shape.scale, out=t[2], workspace=wsa)
+                 for t in sets], nb, nb, c, wl, kern)
+    od = sets[(c.steps - 1) % len(sets)][2]
+    del sets
     if c.cpu:
         from oracle import mla as omla
 
@@ -450,6 +651,15 @@ def case_mla_absorbed(c: Ctx) -> dict:
                                                                     xh["w_uv"], shape.scale), nb, "GB/s",
                                       f"the whole workload ({shape.batch} sequences x {shape.n_h} heads, "
                                       f"T={shape.ctx}, both projections)", got=got)
+
+    def sample():
+        from oracle import mla as omla
+
+        r = omla.mla_absorbed_ref(xh["q_nope"][:2], xh["q_rope"][:2], kv[:2], xh["w_uk"], xh["w_uv"], shape.scale)
+        return {"check": f"sequences [0, 1] of {shape.batch}, all heads, both projections",
+                "output_normwise": _nw(od.cpu()[:2], r)}
+
+    parity_record(c, rec, sample)
     del kvd, x, od, wsa
     return rec
 
@@ -467,8 +677,15 @@ def case_kda_decode(c: Ctx) -> dict:
     nb = c.F.kda_decode_bytes(shape)
     wl = f"kda_decode B{shape.batch} H{shape.n_heads} d{shape.d_k} f16"
     rec = {"workload": wl, "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
-           "frac_hbm_peak": c.F.gbps(nb, ms) / c.F.PEAK_HBM_GBPS,
            "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl, "gdn_decode_kernel (KDA gate)")}
+    sets = [(x, so, od)] + [({n: t.clone() for n, t in x.items()}, torch.empty_like(so), torch.empty_like(od))
+                            for _ in range(rotation_count(nb) - 1)]
+    rotate(rec, [lambda t=t: c.ops.kda_decode(t[0]["q"], t[0]["k"], t[0]["v"], t[0]["g"], t[0]["beta"],
+                                              t[0]["S_in"], S_out=t[1], o=t[2]) for t in sets],
+           nb, nb, c, wl, "gdn_decode_kernel (KDA gate)")
+    rec["frac_hbm_peak"] = rec["value"] / c.F.PEAK_HBM_GBPS
+    _, so, od = sets[(c.steps - 1) % len(sets)]
+    del sets
     if c.cpu:
         from oracle import kda as okda
         from oracle.metrics import normwise_rel_err
@@ -480,6 +697,18 @@ def case_kda_decode(c: Ctx) -> dict:
         leg["sample"] = leg["sample"].replace("fp32 torch CPU oracle", "float64 numpy CPU oracle")
         leg["parity_normwise_state_on_sample"] = normwise_rel_err(s_gpu, okda.kda_decode_ref(**xh)[1])
         rec["cpu_baseline"] = leg
+
+    def sample():
+        import torch as _t
+
+        from oracle import kda as okda
+
+        ro, rs = okda.kda_decode_ref(**xh)
+        return {"check": "the whole workload (output and state), float64 numpy oracle",
+                "output_normwise": _nw(od.float().cpu(), _t.from_numpy(ro).float()),
+                "state_normwise": _nw(so.cpu(), _t.from_numpy(rs).float())}
+
+    parity_record(c, rec, sample)
     del x, so, od
     return rec
 
@@ -500,8 +729,14 @@ def case_quant_fp8_act(c: Ctx) -> dict:
     nb = c.F.quant_fp8_act_bytes(m, k)
     wl = f"quant_fp8_act {m}x{k} bf16 -> e4m3 + 1x128 scales"
     rec = {"workload": wl, "unit": "GB/s", "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(nb, ms),
-           "frac_hbm_peak": c.F.gbps(nb, ms) / c.F.PEAK_HBM_GBPS,
            "roofline": roofline("hbm", nb, ms, c.F.PEAK_HBM_GBPS, "GB/s", wl, "quant_fp8_act_kernel<BF16>")}
+    sets = [(xa, qa, sa)] + [(xa.clone(), torch.empty_like(qa), torch.empty_like(sa))
+                             for _ in range(rotation_count(nb) - 1)]
+    rotate(rec, [lambda t=t: c.ops.quant_fp8_act(t[0], q=t[1], scales=t[2]) for t in sets], nb, nb, c, wl,
+           "quant_fp8_act_kernel<BF16>")
+    rec["frac_hbm_peak"] = rec["value"] / c.F.PEAK_HBM_GBPS
+    _, qa, sa = sets[(c.steps - 1) % len(sets)]
+    del sets
     if c.cpu:
         from oracle import fp8 as ofp8
 
@@ -514,6 +749,17 @@ def case_quant_fp8_act(c: Ctx) -> dict:
         leg["codes_bit_exact_on_sample"] = bool(np.array_equal(ofp8.fp8_tensor_codes(qa[:r].cpu()), codes))
         leg["scales_bit_exact_on_sample"] = bool(np.array_equal(sa[:r].cpu().numpy(), scales))
         rec["cpu_baseline"] = leg
+
+    def sample():
+        from oracle import fp8 as ofp8
+
+        r = QUANT_CPU_ROWS
+        codes, scales = ofp8.quantize_blockwise(xh[:r].float().numpy(), (1, 128))
+        exact = (np.array_equal(ofp8.fp8_tensor_codes(qa[:r].cpu()), codes)
+                 and np.array_equal(sa[:r].cpu().numpy(), scales))
+        return {"check": f"the first {r} of {m} rows, codes and scales", "bit_exact": bool(exact)}
+
+    parity_record(c, rec, sample)
     del xa, qa, sa
     return rec
 
@@ -543,6 +789,15 @@ def case_mla_prefill(c: Ctx) -> dict:
         rec["cpu_baseline"] = cpu_leg(lambda: omla.mla_prefill_ref(qh, kh, vh, heads=hs)[:, :len(hs)],
                                       fl * len(hs) // shape.n_h, "TFLOPS",
                                       f"{len(hs)} of {shape.n_h} heads (S={shape.seq}, full S x S)", got=got)
+
+    def sample():
+        from oracle import mla as omla
+
+        hs = [0, 1]
+        return {"check": f"heads {hs} of {shape.n_h} (S={shape.seq}, full S x S)",
+                "output_normwise": _nw(o[:, hs].cpu(), omla.mla_prefill_ref(qh, kh, vh, heads=hs)[:, hs])}
+
+    parity_record(c, rec, sample)
     del q, k, v, o
     return rec
 
@@ -645,11 +900,22 @@ def main() -> int:
         log(f"case {name}: {rec['value']:.1f} {rec['unit']} (event mean {rec['mean_ms'] * 1e3:.2f} us){extra}")
         results[name] = rec
 
+    return emit(results, names, args.steps, args.warmup, pkg.flops.tflops)
+
+
+def emit(results: dict, names: list, steps: int, warmup: int, tflops) -> int:
+    """Print the one JSON line, or nothing and status 3 when a case failed its parity check."""
+    bad = parity_failures(results)
+    if bad:
+        for b in bad:
+            log(f"PARITY FAILURE {b}")
+        log("no numbers reported: a kernel that fails its correctness check is not published")
+        return 3
     head = results.get("gqa")
     if head is None:  # a profiling run of other cases: report the first one as the line's value
         first = results[names[0]]
         print(json.dumps({"metric": METRIC, "value": round(first["value"], 3), "unit": first["unit"], "n_gpus": 1,
-                          "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(first["wall_ms"], 5),
+                          "steps": steps, "warmup": warmup, "ms_per_step": round(first["wall_ms"], 5),
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                           "dtype": "bf16", "data": "synthetic", "config": {"workload": first["workload"]},
                           "partial_run": names, "settle": settle_note(),
@@ -660,11 +926,11 @@ def main() -> int:
     shape = head["shape"]
     line = {
         "metric": METRIC,
-        "value": round(pkg.flops.tflops(head["flops"], head["wall_ms"]), 3),
+        "value": round(tflops(head["flops"], head["wall_ms"]), 3),
         "unit": "TFLOPS",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(head["wall_ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -679,6 +945,7 @@ def main() -> int:
         },
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
+        "parity": head.get("parity"),
         "settle": settle_note(),
         "tflops_reference_convention": round(head["tflops_reference_convention"], 3),
         "others": {n: _clean(r) for n, r in results.items() if n != "gqa"},

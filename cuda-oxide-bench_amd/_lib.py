@@ -39,6 +39,10 @@ SIGNATURES: dict[str, tuple] = {
     "mx_gemm_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "mx_gemm_fp8_bs": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mx_gqa_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _i, _vp]),
+    "mx_gqa_fwd_tile": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _i, _i, _i, _i, _vp]),
+    "mx_gqa_fwd_tile_check": (_i, [_i, _i, _i, _i, _i, _i]),
+    "mx_gqa_fwd_default_block_m": (_i, [_i, _i, _i]),
+    "mx_gqa_fwd_tile_info": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "mx_mla_decode": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "mx_mla_prefill_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _i, _vp]),
     "mx_mla_decode_workspace": (_sz, [_i, _i, _i, _i]),

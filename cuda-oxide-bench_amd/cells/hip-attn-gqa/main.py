@@ -17,14 +17,20 @@ convention (4*B*Hq*S^2*D, flops.py:31-47); tflops_causal the causal
 algorithmic count 2*B*Hq*D*S*(S+1).
 
 Tile overrides keep the reference's pick_blocks semantics
-(cutile-attn-gqa/main.py:202-230): --block-m (default 64) and --block-n
-(default: --block-m) must divide the sequence, checked by assertion, and
-must name the tile the gfx950 kernel runs for the shape — BLOCK_N = 64 keys
-per LDS stage and BLOCK_M = 256/hpw queries of a head per workgroup, where
-the workgroup's 8 waves of 32 queries cover hpw = 4, 2 or 1 heads of a KV
-group (G % 4 == 0, G % 2 == 0, else): 64 at the bench shape's G = 4, 128 at
-the correctness shape's G = 2.  Any other pair fails the same way the
-reference's assertion does.  The tile in use is what results.csv reports.
+(cutile-attn-gqa/main.py:202-230): --block-m and --block-n must divide the
+sequence (checked by assertion) and select the tile the gfx950 kernel runs
+(mx_gqa_fwd_tile): BLOCK_M query rows of each head per workgroup, BLOCK_N
+keys per LDS stage.  BLOCK_N is the kernels' 64-key stage; an unset
+--block-n takes 64 (the reference defaults it to BLOCK_M, and its own
+BLOCK_M sweep holds it at 64, sweep_block_m.py).  BLOCK_M sets how many
+heads of a KV group a workgroup covers (hpw = workgroup rows / BLOCK_M):
+64, 128 and 256 at the bench shape's G = 4, 64 (4-wave kernel), 128 and 256
+at the correctness shape's G = 2.  --wave-m (added) picks the queries per
+wave: 32 (two waves per SIMD, default) or 64 (one wave per SIMD).  A tile no
+kernel has fails the pick_blocks assertion, as an untileable shape does in
+the reference.  Without overrides the default tile runs at any seq (ragged
+tiles are masked).  The tile in use is what results.csv reports;
+sweep_block_m.py in this directory runs the reference's BLOCK_M sweep.
 """
 from __future__ import annotations
 
@@ -42,36 +48,36 @@ ITERS = 10
 BLOCK_N = 64  # keys per LDS stage
 
 
-def kernel_tile(n_q: int, n_kv: int) -> tuple[int, int]:
-    """(BLOCK_M, BLOCK_N) the kernel runs: 8 waves of 32 queries cover hpw
-    heads of a KV group, so a workgroup holds 256/hpw queries of each head."""
-    g = n_q // n_kv
-    hpw = 4 if g % 4 == 0 else (2 if g % 2 == 0 else 1)
-    return 256 // hpw, BLOCK_N
+def kernel_tile(n_q: int, n_kv: int, d_head: int = 128) -> tuple[int, int]:
+    """(BLOCK_M, BLOCK_N) of the default tile: 8 waves of 32 queries over
+    hpw = 4, 2 or 1 heads of a KV group (mx_gqa_fwd_default_block_m)."""
+    ops = H.package().load_ops()
+    return ops.gqa_default_block_m(n_q, n_kv, d_head), BLOCK_N
 
 
 def pick_blocks(seq: int, n_q: int, n_kv: int, block_m_override: int | None = None,
-                block_n_override: int | None = None):
+                block_n_override: int | None = None, d_head: int = 128, wave_m: int = 32):
     """(BLOCK_M, BLOCK_N) for a sequence length, with the reference's override
-    semantics (cutile-attn-gqa/main.py:202-230): an override defaults the
-    other side (BLOCK_N to BLOCK_M, BLOCK_M to 64) and must divide seq.
-    Without overrides the kernel's own tile runs at any seq (ragged tiles
-    are masked)."""
-    tile = kernel_tile(n_q, n_kv)
-    if block_m_override is not None or block_n_override is not None:
+    semantics (cutile-attn-gqa/main.py:202-230): an override must divide seq
+    (an unset BLOCK_M is 64; an unset BLOCK_N is the kernels' 64-key stage)
+    and must be a tile the library has a kernel for at this head grouping.
+    Without overrides the default tile runs at any seq."""
+    if block_m_override is not None or block_n_override is not None or wave_m != 32:
         bm = block_m_override if block_m_override is not None else 64
-        bn = block_n_override if block_n_override is not None else bm
+        bn = block_n_override if block_n_override is not None else BLOCK_N
         assert seq % bm == 0, f"BLOCK_M={bm} does not divide seq={seq}"
         assert seq % bn == 0, f"BLOCK_N={bn} does not divide seq={seq}"
-        assert (bm, bn) == tile, (
-            f"BLOCK_M={bm} BLOCK_N={bn} is not the gfx950 kernel's tile for n_q={n_q} n_kv={n_kv}: "
-            f"{tile} (BLOCK_M queries of a head per workgroup, BLOCK_N keys per LDS stage)")
+        ops = H.package().load_ops()
+        assert ops.gqa_tile_supported(n_q, n_kv, d_head, bm, bn, wave_m), (
+            f"no gfx950 GQA kernel has BLOCK_M={bm} BLOCK_N={bn} wave_m={wave_m} at n_q={n_q} n_kv={n_kv} "
+            f"d={d_head} (BLOCK_N is the 64-key stage; a workgroup's rows must cover a whole number of heads "
+            f"dividing the group size)")
         return bm, bn
-    return tile
+    return kernel_tile(n_q, n_kv, d_head)
 
 
 def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness", block_m: int | None = None,
-              block_n: int | None = None) -> bool:
+              block_n: int | None = None, wave_m: int = 32) -> bool:
     """The correctness check: the committed golden set, or with inputs_dir a
     fixture set in the reference's inputs/ layout (gqa_<fixture>_*.npy,
     f16 inputs, f32 expected output; cutile-attn-gqa/main.py:177-183)."""
@@ -92,9 +98,9 @@ def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness", block
         g = H.load_golden("gqa_correctness_f16")
         q, k, v = (H.from_bits(g[x], torch.float16).cuda() for x in "qkv")
         expected = g["o"]
-    bm, bn = pick_blocks(q.shape[2], q.shape[1], k.shape[1], block_m, block_n)
-    print(f"[smoke] BLOCK_M={bm} BLOCK_N={bn}")
-    o = ops.gqa_fwd(q, k, v, causal=False)
+    bm, bn = pick_blocks(q.shape[2], q.shape[1], k.shape[1], block_m, block_n, q.shape[3], wave_m)
+    print(f"[smoke] BLOCK_M={bm} BLOCK_N={bn} wave_m={wave_m}")
+    o = ops.gqa_fwd(q, k, v, causal=False, block_m=bm, block_n=bn, wave_m=wave_m)
     torch.cuda.synchronize()
     o32 = o.float().cpu().numpy()
     tol = pkg.tolerances.get("f16")
@@ -110,7 +116,7 @@ def run_smoke(inputs_dir: str | None = None, fixture: str = "correctness", block
 
 
 def run_bench(shape, dtype, dist, csv_path: str, iters: int, block_m: int | None = None,
-              block_n: int | None = None) -> None:
+              block_n: int | None = None, wave_m: int = 32) -> None:
     import torch
 
     pkg = H.package()
@@ -118,11 +124,12 @@ def run_bench(shape, dtype, dist, csv_path: str, iters: int, block_m: int | None
     F = pkg.flops
     print(f"[bench] shape={shape.name} B={shape.batch} S={shape.seq} n_q={shape.n_q} n_kv={shape.n_kv} "
           f"d={shape.d_head} causal={shape.causal} dtype={dtype}")
-    bm, bn = pick_blocks(shape.seq, shape.n_q, shape.n_kv, block_m, block_n)
-    print(f"[bench] BLOCK_M={bm} BLOCK_N={bn}")
+    bm, bn = pick_blocks(shape.seq, shape.n_q, shape.n_kv, block_m, block_n, shape.d_head, wave_m)
+    print(f"[bench] BLOCK_M={bm} BLOCK_N={bn} wave_m={wave_m}")
     q, k, v = (t.cuda() for t in pkg.inputs.gqa_inputs(shape, dtype=dtype, dist=dist))
     out = torch.empty_like(q)
-    ms = H.time_iters(lambda: ops.gqa_fwd(q, k, v, causal=shape.causal, out=out), WARMUP, iters)
+    ms = H.time_iters(lambda: ops.gqa_fwd(q, k, v, causal=shape.causal, out=out, block_m=bm, block_n=bn,
+                                          wave_m=wave_m), WARMUP, iters)
     conv = F.gqa_attention_flops(shape)
     alg = F.gqa_algorithmic_flops(shape)
     dname = "bf16" if dtype == torch.bfloat16 else "f16"
@@ -131,14 +138,15 @@ def run_bench(shape, dtype, dist, csv_path: str, iters: int, block_m: int | None
         print(f"[bench] iter={i} gpu_ms={m:.3f} tflops={F.tflops(conv, m):.3f}")
         rows.append(["hip", "gqa_fwd_fused", shape.batch, shape.seq, shape.n_q, shape.n_kv, shape.d_head, bm,
                      bn, i, f"{m:.6f}", f"{F.tflops(conv, m):.6f}", int(shape.causal), dname,
-                     f"{F.tflops(alg, m):.6f}"])
+                     f"{F.tflops(alg, m):.6f}", wave_m])
     H.write_csv(csv_path, ["impl", "kernel", "batch", "seq", "n_q", "n_kv", "d_head", "block_m", "block_n", "iter",
-                           "gpu_ms", "tflops", "causal", "dtype", "tflops_causal"], rows)
+                           "gpu_ms", "tflops", "causal", "dtype", "tflops_causal", "wave_m"], rows)
     st = H.summarize_ms(ms)
     H.print_summary(f"{shape.name} (algorithmic {'causal' if shape.causal else 'full'} FLOPs)", st,
                     F.tflops(alg, st["best_ms"]), F.tflops(alg, st["median_ms"]), "TFLOPS", F.PEAK_BF16_TFLOPS)
     H.write_sidecar(csv_path, {"kernel": "gqa_fwd_fused", "shape": shape.name, "causal": shape.causal,
-                               "dtype": dname, **st, "flops_algorithmic": alg, "flops_reference_convention": conv,
+                               "dtype": dname, "block_m": bm, "block_n": bn, "wave_m": wave_m,
+                               **st, "flops_algorithmic": alg, "flops_reference_convention": conv,
                                "tflops_algorithmic_median": F.tflops(alg, st["median_ms"]),
                                "peak_tflops": F.PEAK_BF16_TFLOPS,
                                "frac_mfma_peak_median": F.tflops(alg, st["median_ms"]) / F.PEAK_BF16_TFLOPS,
@@ -155,6 +163,8 @@ def main() -> int:
     ap.add_argument("--block-m", type=int, default=None)
     ap.add_argument("--block-n", type=int, default=None)
     ap.add_argument("--iters", type=int, default=None)
+    ap.add_argument("--wave-m", type=int, choices=[32, 64], default=32,
+                    help="query rows per wave: 32 (two waves per SIMD) or 64 (one wave per SIMD)")
     ap.add_argument("--shape", choices=["llama3_8b", "baseline"], default="llama3_8b")
     ap.add_argument("--causal", action="store_true", default=None)
     ap.add_argument("--dtype", choices=["f16", "bf16"], default=None)
@@ -170,12 +180,12 @@ def main() -> int:
     import torch
 
     H.banner()
-    if args.block_m is not None or args.block_n is not None:
-        print(f"[tile] override: BLOCK_M={args.block_m} BLOCK_N={args.block_n}")
+    if args.block_m is not None or args.block_n is not None or args.wave_m != 32:
+        print(f"[tile] override: BLOCK_M={args.block_m} BLOCK_N={args.block_n} wave_m={args.wave_m}")
     print()
     rc = H.EXIT_OK
     if args.smoke:
-        if not run_smoke(args.inputs_dir, args.fixture, args.block_m, args.block_n):
+        if not run_smoke(args.inputs_dir, args.fixture, args.block_m, args.block_n, args.wave_m):
             rc = H.EXIT_SMOKE_FAIL
         print()
     if args.bench:
@@ -189,7 +199,7 @@ def main() -> int:
         if args.dtype is not None:
             dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
         run_bench(shape, dtype, dist, args.csv_out, args.iters if args.iters is not None else ITERS, args.block_m,
-                  args.block_n)
+                  args.block_n, args.wave_m)
         print()
     if args.export_cubin:
         lib = importlib.import_module("cuda-oxide-bench_amd._lib")

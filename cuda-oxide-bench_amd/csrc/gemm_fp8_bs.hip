@@ -609,6 +609,8 @@ extern "C" int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, con
   if (N % 16) return MX_ERR_ALIGN;
   if ((long long)M * K > (1LL << 40) || (long long)K * N > (1LL << 40)) return MX_ERR_SHAPE;
   if ((long long)N * 256 > 0xffffffffLL || (long long)K * 256 > 0xffffffffLL) return MX_ERR_SHAPE;
+  // the activation-scale row offsets (row * K/128 * 4 bytes) are 32-bit
+  if ((long long)M * (K / 128) * 4 > 0xffffffffLL) return MX_ERR_SHAPE;
   if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15) return MX_ERR_ALIGN;
   if (((uintptr_t)sA | (uintptr_t)sB) & 3) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;

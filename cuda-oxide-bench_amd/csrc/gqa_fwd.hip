@@ -18,15 +18,20 @@
 //    V is never transposed in registers.
 //  * A wave owns QT tiles of 32 queries of one head; every K and V fragment
 //    read from LDS feeds QT MFMAs, which is what bounds LDS traffic per FLOP.
-//  * One workgroup = 8 waves (two per SIMD, one workgroup per CU) or 4
-//    waves (two workgroups per CU) = (up to 4 query heads sharing a KV
-//    head) x (query sub-blocks).  K and V tiles of 64 keys are staged once
-//    in LDS (double buffered, next tile's global loads in flight during the
-//    current tile's MFMAs, one barrier per tile) and shared by all waves.
+//  * One workgroup = hpw query heads sharing a KV head x query sub-blocks:
+//    QT = 1 runs 8 waves (two per SIMD, one workgroup per CU; 4 waves, two
+//    workgroups per CU, for head dims whose stage does not split into 8
+//    waves' loads), QT = 2 runs 4 waves (one per SIMD, 512 registers).  K
+//    and V tiles of 64 keys are staged once in LDS (a 2- or 3-stage ring,
+//    next tile's global loads in flight during the current tile's MFMAs,
+//    one barrier per tile) and shared by all waves.  The workgroup's query
+//    rows per head (the tile's BLOCK_M) are waves x 32 QT / hpw; hpw is a
+//    launch argument, so every BLOCK_M with hpw | G is the same kernel.
 //  * Softmax: the running max only moves when a lane's block max exceeds it
-//    by more than 2^8 (lazy rescale, wave-uniform vote), the scale is folded
-//    into the exp2 argument (one FMA + one exp2 per score), and the row sum
-//    is accumulated with v_dot2 on the rounded P the PV MFMA consumes.
+//    by more than 2^8 (lazy rescale, wave-uniform vote).  The scale, in log2
+//    units, is folded into Q once in the prologue, so the score MFMAs return
+//    log2-domain scores and each score costs one exp2; the row sum is
+//    accumulated with v_dot2 on the rounded P the PV MFMA consumes.
 //  * Causal: each workgroup takes a heavy and a light query block (block p
 //    and its mirror nqb-1-p), so all workgroups carry the same number of
 //    key tiles and finish together; only diagonal / ragged tiles are
@@ -34,14 +39,6 @@
 #include <type_traits>
 
 #include "mx_common.h"
-
-// Query tiles (of 32) per wave.  1 keeps two waves per SIMD (the pair hides
-// each other's softmax and LDS latency); 2 halves LDS fragment reads per
-// FLOP (each K and V fragment feeds two MFMAs) but runs one wave per SIMD
-// and is slower on MI355X, so it is not the default.
-#ifndef MX_GQA_QT
-#define MX_GQA_QT 1
-#endif
 
 namespace mx {
 namespace gqa {
@@ -101,6 +98,12 @@ template <int QT>
 struct Ring {
   static constexpr int NS = QT == 1 ? 2 : 3;  // stages (QT=1 keeps two waves per SIMD)
 };
+
+// Waves of a workgroup for the default kernel of a head-dim pair (QT = 1).
+template <int DQK, int DV>
+constexpr int default_waves() {
+  return waves_for<DQK, DV>();
+}
 
 template <int DQK, int DV, typename T, bool CAUSAL, int QT, int NWAVES>
 __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(const uint16_t* __restrict__ Q,
@@ -296,6 +299,18 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
         return lds_ld128(koff[dc] + st + t * 32 * L::ROWK);
       };
       f32x16 s[QT][2];
+      // Start value of the score chains.  With QT = 2 it is rebuilt from
+      // m_run for every tile instead of holding 32 registers across the loop.
+      auto start_m = [&](int qt) {
+        if constexpr (QT == 1) {
+          return neg_m[qt];
+        } else {
+          f32x16 v;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) v[e] = -m_run[qt];
+          return v;
+        }
+      };
       // Wave priority: the two waves sharing a SIMD issue their MFMA phases
       // ahead of the other's softmax VALU work, which then fills the gaps.
       __builtin_amdgcn_s_setprio(1);
@@ -316,7 +331,7 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt)
-            s[qt][t] = mfma32<T>(kb[dc % (KLA + 1)][t], qf[qt][dc], dc == 0 ? neg_m[qt] : s[qt][t]);
+            s[qt][t] = mfma32<T>(kb[dc % (KLA + 1)][t], qf[qt][dc], dc == 0 ? start_m(qt) : s[qt][t]);
 #pragma unroll
         for (int n = 0; n < L::LPW; ++n)
           if (dc == n * DC / L::LPW && load_next) issue_part(blk + NS - 1, n);
@@ -380,7 +395,7 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
 #pragma unroll
             for (int e = 0; e < 16; ++e) s[qt][t][e] -= shift;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) neg_m[qt][e] = -m_run[qt];
+          for (int e = 0; e < 16; ++e) neg_m[qt][e] = QT == 1 ? -m_run[qt] : 0.f;
         }
         // exp2 of key chunk 0 now; chunk c+1 is exponentiated inside the
         // P.V step of chunk c, in the shadow of its MFMAs.
@@ -467,12 +482,10 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
 }  // q-block loop
 }
 
-template <int DQK, int DV, typename T, bool CAUSAL, int QT>
+template <int DQK, int DV, typename T, bool CAUSAL, int QT, int NWAVES>
 static int launch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
-                  hipStream_t stream) {
+                  int hpw, hipStream_t stream) {
   const int G = Hq / Hkv;
-  const int hpw = (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1);
-  constexpr int NWAVES = waves_for<DQK, DV>();
   const int QB = 32 * QT * (NWAVES / hpw);
   const int nqb = (S + QB - 1) / QB;
   const long long grid = (long long)(CAUSAL ? (nqb + 1) / 2 : nqb) * B * Hkv * (G / hpw);
@@ -486,23 +499,77 @@ static int launch(const void* Q, const void* K, const void* V, void* O, int B, i
   return MX_OK;
 }
 
-template <int DQK, int DV, typename T, int QT>
-static int launch_c(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, float scale,
-                    int causal, hipStream_t s) {
-  return causal ? launch<DQK, DV, T, true, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s)
-                : launch<DQK, DV, T, false, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, s);
+// A GQA launch shape: the kernel variant (queries per wave = 32 QT, waves
+// per workgroup) and hpw heads of one KV group per workgroup.  Kernel
+// variants: (QT 1, 8 waves) two waves per SIMD and one workgroup per CU;
+// (QT 1, 4 waves) two workgroups per CU; (QT 2, 4 waves) one wave per SIMD
+// with 512 registers, where each K and V fragment feeds two MFMAs.
+struct Tile {
+  int qt, nwaves, hpw;
+};
+
+// Heads per workgroup of the default tile: as many heads of a KV group as
+// divide G, up to 4 (with 8 waves, each K/V tile then serves 256 queries).
+inline int default_hpw(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0 ? 2 : 1); }
+
+// The launch of a tile (BLOCK_M query rows of a head per workgroup,
+// BLOCK_N keys per LDS stage, wave_m query rows per wave), or
+// MX_ERR_UNSUPPORTED when no kernel of this library has it.  BLOCK_N is the
+// kernels' 64-key stage.  wave_m 32 takes the 8-wave kernel when hpw =
+// 256 / BLOCK_M divides G, else the 4-wave one (hpw = 128 / BLOCK_M); wave_m
+// 64 the QT = 2 kernel (hpw = 256 / BLOCK_M).  GQA head dims 64 and 128.
+inline int tile_for(int G, int D, int block_m, int block_n, int wave_m, Tile* t) {
+  if (block_n != BN || block_m <= 0 || (D != 64 && D != 128)) return MX_ERR_UNSUPPORTED;
+  auto fits = [&](int qt, int nwaves) {
+    const int rows = nwaves * 32 * qt;  // query rows of a workgroup, over all its heads
+    if (rows % block_m) return false;
+    const int hpw = rows / block_m;
+    if (hpw > nwaves || nwaves % hpw || G % hpw) return false;
+    *t = Tile{qt, nwaves, hpw};
+    return true;
+  };
+  if (wave_m == 32) return fits(1, 8) || fits(1, 4) ? MX_OK : MX_ERR_UNSUPPORTED;
+  if (wave_m == 64) return fits(2, 4) ? MX_OK : MX_ERR_UNSUPPORTED;
+  return MX_ERR_UNSUPPORTED;
+}
+
+template <int D, typename T, bool CAUSAL>
+static int launch_tile(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S,
+                       float scale, const Tile& t, hipStream_t s) {
+  if (t.qt == 2) return launch<D, D, T, CAUSAL, 2, 4>(Q, K, V, O, B, Hq, Hkv, S, scale, t.hpw, s);
+  if (t.nwaves == 4) return launch<D, D, T, CAUSAL, 1, 4>(Q, K, V, O, B, Hq, Hkv, S, scale, t.hpw, s);
+  return launch<D, D, T, CAUSAL, 1, 8>(Q, K, V, O, B, Hq, Hkv, S, scale, t.hpw, s);
+}
+
+template <typename T>
+static int dispatch_tile(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int D,
+                         float scale, int causal, const Tile& t, hipStream_t s) {
+  if (D == 128)
+    return causal ? launch_tile<128, T, true>(Q, K, V, O, B, Hq, Hkv, S, scale, t, s)
+                  : launch_tile<128, T, false>(Q, K, V, O, B, Hq, Hkv, S, scale, t, s);
+  return causal ? launch_tile<64, T, true>(Q, K, V, O, B, Hq, Hkv, S, scale, t, s)
+                : launch_tile<64, T, false>(Q, K, V, O, B, Hq, Hkv, S, scale, t, s);
+}
+
+template <int DQK, int DV, typename T>
+static int launch_default(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S,
+                          float scale, int causal, hipStream_t s) {
+  constexpr int NW = default_waves<DQK, DV>();
+  const int hpw = default_hpw(Hq / Hkv);
+  return causal ? launch<DQK, DV, T, true, 1, NW>(Q, K, V, O, B, Hq, Hkv, S, scale, hpw, s)
+                : launch<DQK, DV, T, false, 1, NW>(Q, K, V, O, B, Hq, Hkv, S, scale, hpw, s);
 }
 
 // (qk head dim, v head dim) pairs with a kernel: the GQA head dims 64 and
 // 128, and the MLA prefill pairs 192/128 (DeepSeek-V3: 128 nope + 64 rope,
 // v 128) and 96/64 (the reference's correctness shape).
-template <typename T, int QT>
+template <typename T>
 static int dispatch(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S, int dqk,
                     int dv, float scale, int causal, hipStream_t s) {
-  if (dqk == 128 && dv == 128) return launch_c<128, 128, T, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
-  if (dqk == 64 && dv == 64) return launch_c<64, 64, T, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
-  if (dqk == 192 && dv == 128) return launch_c<192, 128, T, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
-  if (dqk == 96 && dv == 64) return launch_c<96, 64, T, QT>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
+  if (dqk == 128 && dv == 128) return launch_default<128, 128, T>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
+  if (dqk == 64 && dv == 64) return launch_default<64, 64, T>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
+  if (dqk == 192 && dv == 128) return launch_default<192, 128, T>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
+  if (dqk == 96 && dv == 64) return launch_default<96, 64, T>(Q, K, V, O, B, Hq, Hkv, S, scale, causal, s);
   return MX_ERR_UNSUPPORTED;
 }
 
@@ -525,9 +592,68 @@ extern "C" int mx_gqa_fwd(const void* Q, const void* K, const void* V, void* O, 
   if (D != 64 && D != 128) return (!Q || !K || !V || !O) ? MX_ERR_NULL : MX_ERR_SHAPE;
   if (const int e = mx::gqa::check_args(Q, K, V, O, B, Hq, Hkv, S, D, scale, dtype)) return e;
   hipStream_t s = (hipStream_t)stream;
-  constexpr int QT = MX_GQA_QT;
-  if (dtype == MX_DTYPE_BF16) return mx::gqa::dispatch<mx::BF16, QT>(Q, K, V, O, B, Hq, Hkv, S, D, D, scale, causal, s);
-  return mx::gqa::dispatch<mx::F16, QT>(Q, K, V, O, B, Hq, Hkv, S, D, D, scale, causal, s);
+  if (dtype == MX_DTYPE_BF16) return mx::gqa::dispatch<mx::BF16>(Q, K, V, O, B, Hq, Hkv, S, D, D, scale, causal, s);
+  return mx::gqa::dispatch<mx::F16>(Q, K, V, O, B, Hq, Hkv, S, D, D, scale, causal, s);
+}
+
+extern "C" int mx_gqa_fwd_tile_check(int Hq, int Hkv, int D, int block_m, int block_n, int wave_m) {
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || (D != 64 && D != 128)) return MX_ERR_SHAPE;
+  mx::gqa::Tile t;
+  return mx::gqa::tile_for(Hq / Hkv, D, block_m, block_n, wave_m, &t);
+}
+
+extern "C" int mx_gqa_fwd_default_block_m(int Hq, int Hkv, int D) {
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || (D != 64 && D != 128)) return MX_ERR_SHAPE;
+  return 8 * 32 / mx::gqa::default_hpw(Hq / Hkv);
+}
+
+extern "C" int mx_gqa_fwd_tile(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S,
+                               int D, float scale, int causal, int dtype, int block_m, int block_n, int wave_m,
+                               void* stream) {
+  if (D != 64 && D != 128) return (!Q || !K || !V || !O) ? MX_ERR_NULL : MX_ERR_SHAPE;
+  if (const int e = mx::gqa::check_args(Q, K, V, O, B, Hq, Hkv, S, D, scale, dtype)) return e;
+  mx::gqa::Tile t;
+  if (const int e = mx::gqa::tile_for(Hq / Hkv, D, block_m, block_n, wave_m, &t)) return e;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == MX_DTYPE_BF16)
+    return mx::gqa::dispatch_tile<mx::BF16>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, t, s);
+  return mx::gqa::dispatch_tile<mx::F16>(Q, K, V, O, B, Hq, Hkv, S, D, scale, causal, t, s);
+}
+
+namespace mx {
+namespace gqa {
+template <int D, typename T, bool C>
+static const void* tile_kernel(const Tile& t) {
+  if (t.qt == 2) return reinterpret_cast<const void*>(gqa_fwd_kernel<D, D, T, C, 2, 4>);
+  if (t.nwaves == 4) return reinterpret_cast<const void*>(gqa_fwd_kernel<D, D, T, C, 1, 4>);
+  return reinterpret_cast<const void*>(gqa_fwd_kernel<D, D, T, C, 1, 8>);
+}
+template <int D, typename T>
+static const void* tile_kernel_c(const Tile& t, int causal) {
+  return causal ? tile_kernel<D, T, true>(t) : tile_kernel<D, T, false>(t);
+}
+}  // namespace gqa
+}  // namespace mx
+
+// Registers and scratch (spill) bytes per lane of the kernel a tile runs:
+// what the reference's block sweep reads from its compiled kernels.
+extern "C" int mx_gqa_fwd_tile_info(int Hq, int Hkv, int D, int dtype, int causal, int block_m, int block_n,
+                                    int wave_m, int* vgprs, int* scratch_bytes) {
+  if (!vgprs || !scratch_bytes) return MX_ERR_NULL;
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || (D != 64 && D != 128)) return MX_ERR_SHAPE;
+  if (dtype != MX_DTYPE_BF16 && dtype != MX_DTYPE_F16) return MX_ERR_DTYPE;
+  mx::gqa::Tile t;
+  if (const int e = mx::gqa::tile_for(Hq / Hkv, D, block_m, block_n, wave_m, &t)) return e;
+  using mx::gqa::tile_kernel_c;
+  const void* f = D == 128 ? (dtype == MX_DTYPE_BF16 ? tile_kernel_c<128, mx::BF16>(t, causal)
+                                                    : tile_kernel_c<128, mx::F16>(t, causal))
+                           : (dtype == MX_DTYPE_BF16 ? tile_kernel_c<64, mx::BF16>(t, causal)
+                                                    : tile_kernel_c<64, mx::F16>(t, causal));
+  hipFuncAttributes a{};
+  MX_RETURN_IF_HIP(hipFuncGetAttributes(&a, f));
+  *vgprs = a.numRegs;
+  *scratch_bytes = (int)a.localSizeBytes;
+  return MX_OK;
 }
 
 extern "C" int mx_mla_prefill_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H, int S, int d_qk,
@@ -537,8 +663,7 @@ extern "C" int mx_mla_prefill_fwd(const void* Q, const void* K, const void* V, v
         (d_qk == 64 && d_v == 64)))
     return MX_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
-  constexpr int QT = MX_GQA_QT;
   if (dtype == MX_DTYPE_BF16)
-    return mx::gqa::dispatch<mx::BF16, QT>(Q, K, V, O, B, H, H, S, d_qk, d_v, scale, causal, s);
-  return mx::gqa::dispatch<mx::F16, QT>(Q, K, V, O, B, H, H, S, d_qk, d_v, scale, causal, s);
+    return mx::gqa::dispatch<mx::BF16>(Q, K, V, O, B, H, H, S, d_qk, d_v, scale, causal, s);
+  return mx::gqa::dispatch<mx::F16>(Q, K, V, O, B, H, H, S, d_qk, d_v, scale, causal, s);
 }

@@ -97,11 +97,15 @@ def gemm_fp8_bs(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Te
 
 
 def gqa_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
-            scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+            scale: float | None = None, out: torch.Tensor | None = None, block_m: int | None = None,
+            block_n: int | None = None, wave_m: int | None = None) -> torch.Tensor:
     """Fused GQA forward.  q [B,Hq,S,D]; k, v [B,Hkv,S,D]; bf16 or f16.
 
     Semantics of cutile-attn-gqa/main.py:64-170 (scale defaults to 1/sqrt(D)
-    as in :85) with an optional causal mask.
+    as in :85) with an optional causal mask.  block_m / block_n / wave_m
+    select the tile (mx_gqa_fwd_tile: query rows of a head per workgroup,
+    keys per LDS stage, query rows per wave); unset ones take the default
+    tile's value, and a tile the library has no kernel for raises MXError.
     """
     _require(q, "q", _IO_DTYPES, 4)
     _require(k, "k", (q.dtype,), 4)
@@ -120,9 +124,40 @@ def gqa_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = Fa
     if out.shape != q.shape:
         raise ValueError(f"out must be {tuple(q.shape)}")
     _same_device(q, k, v, out)
-    _lib.call("mx_gqa_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
-              float(scale), int(bool(causal)), _IO_DTYPES[q.dtype], _stream())
+    if block_m is None and block_n is None and wave_m is None:
+        _lib.call("mx_gqa_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
+                  float(scale), int(bool(causal)), _IO_DTYPES[q.dtype], _stream())
+        return out
+    bm = gqa_default_block_m(Hq, Hkv, D) if block_m is None else int(block_m)
+    bn = 64 if block_n is None else int(block_n)
+    wm = 32 if wave_m is None else int(wave_m)
+    _lib.call("mx_gqa_fwd_tile", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
+              float(scale), int(bool(causal)), _IO_DTYPES[q.dtype], bm, bn, wm, _stream())
     return out
+
+
+def gqa_default_block_m(n_q: int, n_kv: int, d_head: int) -> int:
+    """BLOCK_M of the default GQA tile (queries of a head per workgroup)."""
+    r = int(_lib.load().mx_gqa_fwd_default_block_m(n_q, n_kv, d_head))
+    if r < 0:
+        raise ValueError(f"no GQA tile for n_q={n_q} n_kv={n_kv} d={d_head}: {_lib.strerror(r)}")
+    return r
+
+
+def gqa_tile_supported(n_q: int, n_kv: int, d_head: int, block_m: int, block_n: int = 64, wave_m: int = 32) -> bool:
+    """Whether mx_gqa_fwd_tile has a kernel for this tile (host logic, no GPU call)."""
+    return int(_lib.load().mx_gqa_fwd_tile_check(n_q, n_kv, d_head, block_m, block_n, wave_m)) == 0
+
+
+def gqa_tile_info(n_q: int, n_kv: int, d_head: int, dtype: torch.dtype, causal: bool, block_m: int,
+                  block_n: int = 64, wave_m: int = 32) -> tuple[int, int]:
+    """(registers per lane, scratch bytes per lane) of the kernel a tile runs."""
+    import ctypes
+
+    regs, scratch = ctypes.c_int(0), ctypes.c_int(0)
+    _lib.call("mx_gqa_fwd_tile_info", n_q, n_kv, d_head, _IO_DTYPES[dtype], int(bool(causal)), block_m, block_n,
+              wave_m, ctypes.byref(regs), ctypes.byref(scratch))
+    return regs.value, scratch.value
 
 
 def mla_decode_workspace_bytes(B: int, H: int, T: int, d_latent: int = 512) -> int:

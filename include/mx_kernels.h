@@ -132,6 +132,43 @@ int mx_gqa_fwd(const void* Q, const void* K, const void* V, void* O, int B, int 
                int D, float scale, int causal, int dtype, void* stream);
 
 /*
+ * mx_gqa_fwd with an explicit tile: block_m query rows of each head per
+ * workgroup, block_n keys per LDS stage, wave_m query rows per wave.
+ * block_n must be 64 (the kernels' key stage).  A workgroup covers hpw =
+ * waves * wave_m / block_m heads of one KV group, a whole number dividing
+ * both the wave count and G = Hq / Hkv.  wave_m = 32 runs 8 waves (two per
+ * SIMD) when that allows, else 4 waves (two workgroups per CU); wave_m = 64
+ * runs 4 waves (one per SIMD, 512 registers; each K/V fragment feeds two
+ * MFMAs).  A tile no kernel has returns MX_ERR_UNSUPPORTED before anything
+ * is enqueued.  Any S is
+ * accepted (ragged query and key tiles are masked).  mx_gqa_fwd runs
+ * block_m = mx_gqa_fwd_default_block_m(Hq, Hkv, D), block_n 64, wave_m 32.
+ * Replaces: cutile-attn-gqa/main.py:202-230 (pick_blocks with the
+ * --block-m / --block-n overrides, each pair compiled by make_gqa_kernel,
+ * :64-66) and the launch at :249-252.
+ */
+int mx_gqa_fwd_tile(const void* Q, const void* K, const void* V, void* O, int B, int Hq, int Hkv, int S,
+                    int D, float scale, int causal, int dtype, int block_m, int block_n, int wave_m,
+                    void* stream);
+
+/* MX_OK if mx_gqa_fwd_tile has a kernel for this tile at (Hq, Hkv, D), else
+ * MX_ERR_UNSUPPORTED (MX_ERR_SHAPE for invalid head counts or D).  Host
+ * logic only: no GPU call. */
+int mx_gqa_fwd_tile_check(int Hq, int Hkv, int D, int block_m, int block_n, int wave_m);
+
+/* BLOCK_M of mx_gqa_fwd's default tile (8 waves of 32 queries over hpw =
+ * 4, 2 or 1 heads of a KV group as G allows: 256 / hpw), or MX_ERR_SHAPE.
+ * Host logic only. */
+int mx_gqa_fwd_default_block_m(int Hq, int Hkv, int D);
+
+/* Registers per lane (numRegs) and scratch bytes per lane (spills) of the
+ * gfx950 kernel that mx_gqa_fwd_tile runs for this tile; what the
+ * reference's block sweep reads from its compiled kernels
+ * (cutile-attn-gqa/sweep_block_m.py, lmem_check).  Needs the HIP runtime. */
+int mx_gqa_fwd_tile_info(int Hq, int Hkv, int D, int dtype, int causal, int block_m, int block_n, int wave_m,
+                         int* vgprs, int* scratch_bytes);
+
+/*
  * Pre-projected MLA prefill attention (multi-head, every head its own K/V):
  *   O[b,h,s,:] = softmax_t( scale * Q[b,h,s,:]·K[b,h,t,:] + mask ) · V[b,h,t,:]
  * Q, K: [B, H, S, d_qk]; V, O: [B, H, S, d_v]; contiguous bf16 or f16;

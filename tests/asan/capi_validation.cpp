@@ -49,6 +49,7 @@ int main() {
   EXPECT(mx_gemm_fp8_bs(P, F, P, F, nullptr, 64, 64, 128, nullptr), MX_ERR_NULL);
   EXPECT(mx_gemm_fp8_bs(P, F, P, F, P, 64, 64, 100, nullptr), MX_ERR_SHAPE);
   EXPECT(mx_gemm_fp8_bs(P, F, P, F, P, 64, 40, 128, nullptr), MX_ERR_ALIGN);
+  EXPECT(mx_gemm_fp8_bs(P, F, P, F, P, (1 << 30) + 1, 16, 128, nullptr), MX_ERR_SHAPE);
   EXPECT(mx_quant_fp8_act(nullptr, P, F, 4, 128, 128, 0, nullptr), MX_ERR_NULL);
   EXPECT(mx_quant_fp8_act(P, P, F, 4, 96, 96, 0, nullptr), MX_ERR_SHAPE);
   EXPECT(mx_quant_fp8_act(P, P, F, 4, 128, 132, 0, nullptr), MX_ERR_ALIGN);
@@ -58,6 +59,11 @@ int main() {
   EXPECT(mx_gqa_fwd(nullptr, P, P, P, 1, 4, 2, 16, 64, 0.125f, 1, 0, nullptr), MX_ERR_NULL);
   EXPECT(mx_gqa_fwd(P, P, P, P, 1, 4, 3, 16, 64, 0.125f, 1, 0, nullptr), MX_ERR_SHAPE);
   EXPECT(mx_gqa_fwd(P, P, P, P, 1, 4, 2, 16, 64, 0.125f, 1, 7, nullptr), MX_ERR_DTYPE);
+  EXPECT(mx_gqa_fwd_tile(P, P, P, P, 1, 32, 8, 256, 128, 0.088f, 1, 0, 64, 32, 32, nullptr), MX_ERR_UNSUPPORTED);
+  EXPECT(mx_gqa_fwd_tile(P, P, P, P, 1, 32, 8, 256, 128, 0.088f, 1, 0, 16, 64, 32, nullptr), MX_ERR_UNSUPPORTED);
+  EXPECT(mx_gqa_fwd_tile_check(32, 8, 128, 128, 64, 64), MX_OK);
+  EXPECT(mx_gqa_fwd_tile_check(32, 7, 128, 128, 64, 64), MX_ERR_SHAPE);
+  EXPECT(mx_gqa_fwd_tile_info(32, 8, 128, 0, 1, 64, 64, 32, nullptr, nullptr), MX_ERR_NULL);
   EXPECT(mx_mla_prefill_fwd(P, P, P, P, 1, 4, 16, 160, 128, 0.07f, 0, 0, nullptr), MX_ERR_UNSUPPORTED);
   EXPECT(mx_mla_prefill_fwd(P, P, P, P, 1, 4, 16, 192, 128, 0.0f, 0, 0, nullptr), MX_ERR_SHAPE);
 

@@ -70,6 +70,8 @@ def test_gemm_fp8_validation():
     assert f(P, P, P, P, None, 64, 64, 128, None) == _lib.MX_ERR_NULL
     assert f(P, P, P, P, P, 64, 64, 100, None) == _lib.MX_ERR_SHAPE
     assert f(P, P, P, P, P, 64, 40, 128, None) == _lib.MX_ERR_ALIGN
+    # M*K below the 2^40 element limit, but the sA byte offsets pass 2^32
+    assert f(P, P, P, P, P, (1 << 30) + 1, 16, 128, None) == _lib.MX_ERR_SHAPE
 
 
 def test_gqa_validation():
@@ -79,6 +81,46 @@ def test_gqa_validation():
     assert f(P, P, P, P, 1, 4, 2, 16, 96, 0.125, 1, 0, None) == _lib.MX_ERR_SHAPE   # D
     assert f(P, P, P, P, 1, 4, 2, 16, 64, 0.125, 1, 7, None) == _lib.MX_ERR_DTYPE
     assert f(P, P, P, P, 1, 4, 2, 16, 64, -1.0, 1, 0, None) == _lib.MX_ERR_SHAPE
+
+
+def test_gqa_tile_validation():
+    f = _lib.load().mx_gqa_fwd_tile
+    ok = (P, P, P, P, 1, 32, 8, 256, 128, 0.088, 1, 0)
+    assert f(None, *ok[1:], 64, 64, 32, None) == _lib.MX_ERR_NULL
+    assert f(*ok, 64, 32, 32, None) == _lib.MX_ERR_UNSUPPORTED    # BLOCK_N is the 64-key stage
+    assert f(*ok, 16, 64, 32, None) == _lib.MX_ERR_UNSUPPORTED    # 8 or 16 heads per workgroup: more than G = 4
+    assert f(*ok, 96, 64, 32, None) == _lib.MX_ERR_UNSUPPORTED    # 256 rows are not whole 96-row blocks
+    assert f(*ok, 512, 64, 32, None) == _lib.MX_ERR_UNSUPPORTED   # fewer rows than one block
+    assert f(*ok, 64, 64, 48, None) == _lib.MX_ERR_UNSUPPORTED    # wave_m
+    assert f(P, P, P, P, 1, 32, 8, 256, 128, 0.088, 1, 9, 64, 64, 32, None) == _lib.MX_ERR_DTYPE
+
+
+@pytest.mark.parametrize("hq,hkv,d,bm,wm,code", [
+    # G = 4 (the bench shapes): 8 waves of 32 cover 4, 2 or 1 heads, 4 waves of 32 cover 4 heads in 32-row
+    # blocks, 4 waves of 64 cover 4, 2 or 1 heads
+    (32, 8, 128, 64, 32, 0), (32, 8, 128, 128, 32, 0), (32, 8, 128, 256, 32, 0), (32, 8, 128, 32, 32, 0),
+    (32, 8, 128, 64, 64, 0), (32, 8, 128, 128, 64, 0), (32, 8, 128, 256, 64, 0),
+    (32, 8, 128, 16, 32, _lib.MX_ERR_UNSUPPORTED), (32, 8, 128, 32, 64, _lib.MX_ERR_UNSUPPORTED),
+    (32, 8, 128, 512, 32, _lib.MX_ERR_UNSUPPORTED), (32, 8, 128, 96, 32, _lib.MX_ERR_UNSUPPORTED),
+    # G = 2 (the correctness shape): 64-row blocks on the 4-wave kernel, 128 and 256 on the 8-wave one
+    (4, 2, 64, 64, 32, 0), (4, 2, 64, 128, 32, 0), (4, 2, 64, 256, 32, 0), (4, 2, 64, 32, 32, _lib.MX_ERR_UNSUPPORTED),
+    (4, 2, 64, 64, 64, _lib.MX_ERR_UNSUPPORTED), (4, 2, 64, 128, 64, 0),
+    # G = 1 (MHA): whole-workgroup blocks only
+    (4, 4, 64, 256, 32, 0), (4, 4, 64, 128, 32, 0), (4, 4, 64, 64, 32, _lib.MX_ERR_UNSUPPORTED),
+    (64, 8, 64, 32, 32, 0),
+    (32, 8, 96, 64, 32, _lib.MX_ERR_SHAPE), (32, 7, 128, 64, 32, _lib.MX_ERR_SHAPE),
+])
+def test_gqa_tile_check(hq, hkv, d, bm, wm, code):
+    assert _lib.load().mx_gqa_fwd_tile_check(hq, hkv, d, bm, 64, wm) == code
+
+
+def test_gqa_default_block_m():
+    f = _lib.load().mx_gqa_fwd_default_block_m
+    assert [f(32, 8, 128), f(4, 2, 64), f(4, 4, 64), f(64, 8, 128)] == [64, 128, 256, 64]
+    assert f(32, 7, 128) == _lib.MX_ERR_SHAPE
+    # the default tile is always one mx_gqa_fwd_tile accepts
+    for hq, hkv in ((32, 8), (4, 2), (4, 4), (12, 4), (6, 2)):
+        assert _lib.load().mx_gqa_fwd_tile_check(hq, hkv, 128, f(hq, hkv, 128), 64, 32) == 0
 
 
 def test_mla_prefill_validation():

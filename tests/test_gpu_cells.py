@@ -90,10 +90,53 @@ def test_gdn_sweep_csv(tmp_path):
         assert d_v % bv == 0 and nblk == int(r[3]) * int(r[4]) * (d_v // bv)
 
 
+@pytest.mark.parametrize("argv", [["--block-m", "128"], ["--block-m", "256", "--block-n", "64"],
+                                  ["--block-m", "128", "--wave-m", "64"]])
+def test_gqa_tile_override_runs(tmp_path, argv):
+    """--block-m / --block-n select the tile that runs (cutile-attn-gqa/main.py:202-230);
+    results.csv reports it."""
+    announce(f"cell hip-attn-gqa --bench {' '.join(argv)}")
+    out = tmp_path / "results.csv"
+    assert run_cell("hip-attn-gqa", ["--bench", *argv, "--iters", "2", "--csv-out", str(out)]) == 0
+    got, rows = read_csv(out)
+    bm = int(argv[argv.index("--block-m") + 1])
+    wm = int(argv[argv.index("--wave-m") + 1]) if "--wave-m" in argv else 32
+    assert all(int(r[got.index("block_m")]) == bm and int(r[got.index("block_n")]) == 64 for r in rows)
+    assert all(int(r[got.index("wave_m")]) == wm for r in rows)
+
+
 def test_gqa_tile_override_rejected(tmp_path):
-    """A BLOCK_M the kernel is not built for fails like the reference's
-    pick_blocks assertion (cutile-attn-gqa/main.py:213-219)."""
-    announce("cell hip-attn-gqa --block-m 128 (rejected)")
+    """A tile no kernel has (BLOCK_N other than the 64-key stage) fails like
+    the reference's pick_blocks assertion (cutile-attn-gqa/main.py:213-219)."""
+    announce("cell hip-attn-gqa --block-n 32 (rejected)")
     with pytest.raises(AssertionError):
-        run_cell("hip-attn-gqa", ["--bench", "--block-m", "128", "--iters", "2", "--csv-out",
+        run_cell("hip-attn-gqa", ["--bench", "--block-m", "64", "--block-n", "32", "--iters", "2", "--csv-out",
                                   str(tmp_path / "r.csv")])
+
+
+def test_gqa_block_m_sweep(tmp_path):
+    """sweep_block_m.py: the reference's BLOCK_M sweep rows and CSV columns
+    (cutile-attn-gqa/sweep_block_m.py, sweep_block_m_results.csv:1): 64 and
+    128 pass the correctness shape, 256 is a compile-only SKIP there; every
+    tile has a kernel at the bench shape.  wave_m is an appended column."""
+    announce("cell hip-attn-gqa sweep_block_m.py")
+    path = CELLS / "hip-attn-gqa" / "sweep_block_m.py"
+    spec = importlib.util.spec_from_file_location("gqa_sweep", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    out = tmp_path / "sweep.csv"
+    old = sys.argv
+    sys.argv = [str(path), "--csv-out", str(out), "--wave-m", "32", "64"]
+    try:
+        assert mod.main() == 0
+    finally:
+        sys.argv = old
+    got, rows = read_csv(out)
+    assert got == ["block_m", "block_n", "correctness_status", "compile_status", "notes", "wave_m"]
+    table = {(int(r[0]), int(r[5])): (r[2], r[3]) for r in rows}
+    assert table[(64, 32)] == ("PASS", "OK") and table[(128, 32)] == ("PASS", "OK")
+    assert table[(256, 32)] == ("SKIP", "OK") and table[(256, 64)] == ("SKIP", "OK")
+    assert table[(128, 64)] == ("PASS", "OK")
+    # 64-row blocks of 64-query waves would need 4 heads per workgroup: not at the correctness shape's G = 2
+    assert table[(64, 64)][1] == "OK" and table[(64, 64)][0] == "ERROR"
+    assert all(int(r[1]) == 64 for r in rows)

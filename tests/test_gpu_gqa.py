@@ -101,3 +101,69 @@ def test_causal_first_row_is_first_value(ops):
     o = run(ops, q, k, v, True).float()
     for h in range(4):
         assert torch.allclose(o[0, h, 0], v[0, h // 2, 0].float(), atol=1e-2, rtol=1e-2)
+
+
+# Every tile mx_gqa_fwd_tile accepts at these head groupings: (B, S, Hq, Hkv, D, BLOCK_M, wave_m).
+# G = 4 covers the 8-wave kernel at 1, 2, 4 heads per workgroup, the 4-wave kernel at 32-row blocks and
+# the one-wave-per-SIMD kernel (wave_m 64); G = 2 the 4-wave kernel at 64-row blocks; G = 1 whole-workgroup
+# blocks; G = 8 eight heads per workgroup.  Ragged S everywhere.
+TILES = [
+    (1, 300, 8, 2, 128, 32, 32), (1, 300, 8, 2, 128, 64, 32), (1, 300, 8, 2, 128, 128, 32),
+    (1, 300, 8, 2, 128, 256, 32), (1, 300, 8, 2, 128, 64, 64), (2, 300, 8, 2, 128, 128, 64),
+    (1, 300, 8, 2, 128, 256, 64),
+    (1, 200, 4, 2, 64, 64, 32), (1, 200, 4, 2, 64, 128, 32), (1, 200, 4, 2, 64, 256, 32),
+    (1, 200, 4, 2, 64, 128, 64), (1, 200, 4, 2, 64, 256, 64),
+    (1, 170, 4, 4, 64, 128, 32), (1, 170, 4, 4, 64, 256, 32), (1, 170, 4, 4, 128, 256, 64),
+    (1, 130, 8, 1, 64, 32, 32), (1, 130, 8, 1, 128, 64, 64),
+]
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["c", "n"])
+@pytest.mark.parametrize("case", TILES, ids=lambda c: f"B{c[0]}S{c[1]}H{c[2]}/{c[3]}D{c[4]}bm{c[5]}wm{c[6]}")
+def test_tile_parity_vs_oracle(ops, case, causal):
+    """Each explicit tile (the reference's --block-m override,
+    cutile-attn-gqa/main.py:202-230) against gqa_naive, both dtypes."""
+    B, S, Hq, Hkv, D, bm, wm = case
+    for dt in (torch.bfloat16, torch.float16):
+        announce(f"gqa tile BLOCK_M={bm} wave_m={wm} B{B} S{S} Hq{Hq} Hkv{Hkv} D{D} causal={causal} {dt}")
+        assert ops.gqa_tile_supported(Hq, Hkv, D, bm, 64, wm)
+        s = shapes.GQAShape("t", B, S, Hq, Hkv, D, causal)
+        q, k, v = inputs.gqa_inputs(s, dtype=dt, seed=inputs.SEED + bm + wm)
+        o = ops.gqa_fwd(q.cuda(), k.cuda(), v.cuda(), causal=causal, block_m=bm, block_n=64, wave_m=wm)
+        torch.cuda.synchronize()
+        ref = ogqa.gqa_naive(q, k, v, causal=causal)
+        err = normwise_rel_err(o.cpu(), ref)
+        assert err <= TOL, f"normwise rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("bm,wm", [(64, 32), (128, 32), (256, 32), (64, 64), (128, 64), (256, 64)])
+def test_tile_baseline_config(ops, bm, wm):
+    """The BASELINE shape (B1 Hq32 Hkv8 S4096 D128 bf16 causal) on every
+    tile of the reference's BLOCK_M sweep: three heads against the oracle,
+    and the tile's output equal to the default tile's up to rounding."""
+    announce(f"gqa BASELINE tile BLOCK_M={bm} wave_m={wm}")
+    s = shapes.GQA_BASELINE
+    q, k, v = (t.cuda() for t in inputs.gqa_inputs(s))
+    o = ops.gqa_fwd(q, k, v, causal=True, block_m=bm, block_n=64, wave_m=wm)
+    torch.cuda.synchronize()
+    heads = [0, 13, 31]
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    ref = ogqa.gqa_naive(qc, kc, vc, causal=True, heads=heads)
+    err = normwise_rel_err(o.cpu()[:, heads], ref[:, heads])
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    assert torch.isfinite(o.float()).all()
+
+
+def test_tile_rejections_enqueue_nothing(ops):
+    """A tile no kernel has raises before any launch, and leaves out untouched."""
+    import importlib
+
+    _lib = importlib.import_module("cuda-oxide-bench_amd._lib")
+    s = shapes.GQAShape("t", 1, 128, 8, 2, 128, True)
+    q, k, v = (t.cuda() for t in inputs.gqa_inputs(s))
+    out = torch.full_like(q, float("nan"))
+    for bm, bn, wm in ((64, 32, 32), (16, 64, 32), (32, 64, 64)):
+        with pytest.raises(_lib.MXError):
+            ops.gqa_fwd(q, k, v, causal=True, out=out, block_m=bm, block_n=bn, wave_m=wm)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
