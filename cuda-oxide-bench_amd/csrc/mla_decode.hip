@@ -31,8 +31,9 @@
 //  * cache rows go HBM -> LDS with global_load_lds_dwordx4 (no VGPR
 //    staging): latent rows into a 4-slot ring (a stage is read by the
 //    scores of one iteration and the values of the next), rope rows into a
-//    3-slot ring; 16-byte chunks are XOR-swizzled so both the K reads and
-//    the transposing V reads are bank-conflict free;
+//    3-slot ring; 16-byte chunks are XOR-swizzled per row (swz_lat,
+//    swz_rope below) so the K reads and the transposing V reads each hit
+//    distinct bank slots;
 //  * T is split across workgroups to fill the 256 CUs; each split writes
 //    its normalised partial output (bf16, coalesced 512 B stores) and
 //    (m, l) to the workspace, and a second kernel merges the splits with
@@ -75,12 +76,26 @@ static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 static_assert(NWAVES * Q_WAVE_B <= LDS_BYTES, "Q staging fits the LDS allocation");
 static_assert(DV / 16 == 32 && (DQK - DV) / 16 == 4, "Q fragment split: 32 latent + 4 rope k-steps");
 
-// Chunk c of row t sits at chunk position c ^ swz(t) of its row.  swz maps
-// t%8 to 0,2,4,6,1,3,5,7: distinct over 8 rows (K reads: 8 consecutive
-// tokens, one chunk) and with distinct halves over each aligned group of 4
-// rows (transposing V reads: 4 consecutive tokens, two adjacent chunks), so
-// both read patterns are bank-conflict free on 1024 B and 128 B rows.
-__device__ __forceinline__ int swz(int t) { return ((t & 3) << 1) | ((t >> 2) & 1); }
+// Chunk c of latent row t sits at chunk position c ^ swz_lat(t) of its
+// 1024-byte row, chunk c of rope row t at c ^ swz_rope(t) of its 128-byte
+// row.  LDS serves a 64-lane ds_read_b128 in four groups of 16 lanes, keyed
+// by lane bit 5 and the parity of lane bits 2..4, and each group must hit
+// 16 distinct 16-byte slots of the 256-byte bank window; a transposing
+// ds_read_b64_tr_b16 is served in two 32-lane halves that must hit 32
+// distinct 8-byte slots.
+//  * K reads (lane l: token l%32, one chunk): the 16 tokens of a group are
+//    {4a..4a+3} for four values of a with equal bit parity; swz_lat(t) =
+//    (t%4)*4 + (t/4)%4 takes 16 distinct values over them.  Latent rows are
+//    1024 B (every row starts at bank 0), so the slot is position % 16.
+//    Rope rows are 128 B (two per window): swz_rope(t) = (t/2)%8 takes 8
+//    distinct values over each parity of t in a group.
+//  * V reads (a half-wave: 4 consecutive tokens 4a..4a+3 x one aligned quad
+//    of 4 chunks): swz_lat's bits 2..3 are t%4, so the four rows land in
+//    four different 64-byte quads; its bits 0..1 permute within a quad.
+// swz_lat(t + 16) = swz_lat(t), so fragments 16 rows apart share lane
+// offsets; rows 8 apart do not (they meet in one K read group).
+__device__ __forceinline__ int swz_lat(int t) { return ((t & 3) << 2) | ((t >> 2) & 3); }
+__device__ __forceinline__ int swz_rope(int t) { return (t >> 1) & 7; }
 
 struct Split {
   int nsplit;
@@ -102,10 +117,10 @@ __host__ __device__ inline Split pick_split(int B, int H, int T) {
 
 // Stage i of a split: 32 latent rows of 1024 B (64 chunks) in latent slot
 // i%4 and 32 rope rows of 128 B (8 chunks) in rope slot i%3, chunk c of row
-// t at position c ^ swz(t).  Each 1 KB wave load fills one latent row (lane
-// j <- chunk j ^ swz(t), from a wave-uniform row address) or eight rope
-// rows.  Rows past the end of the split re-read the last valid row (finite
-// data whose scores are masked).
+// t at position c ^ swz_lat(t) (latent) or c ^ swz_rope(t) (rope).  Each
+// 1 KB wave load fills one latent row (lane j <- chunk j ^ swz_lat(t), from
+// a wave-uniform row address) or eight rope rows.  Rows past the end of the
+// split re-read the last valid row (finite data whose scores are masked).
 __device__ __forceinline__ void issue_part(const unsigned char* kvb, int tok0, int t1, uint32_t lat, uint32_t rope,
                                            int wave, int lane, int n) {
   constexpr int LR = BT / NWAVES;  // latent rows per wave
@@ -114,12 +129,12 @@ __device__ __forceinline__ void issue_part(const unsigned char* kvb, int tok0, i
     asm volatile("" : "+v"(l16));  // keep the per-row XOR here instead of a hoisted VGPR per row
     const int r = wave * LR + n;
     const int tok = min(tok0 + r, t1 - 1);
-    dma16(kvb + (size_t)tok * ROW_B, l16 ^ (uint32_t)(16 * swz(r)), lat + r * 1024);
+    dma16(kvb + (size_t)tok * ROW_B, l16 ^ (uint32_t)(16 * swz_lat(r)), lat + r * 1024);
   } else {
     const int r0 = wave * 8;
     const int tb = min(tok0 + r0, t1 - 1);
     const int tok = min(tok0 + r0 + (lane >> 3), t1 - 1);
-    const uint32_t off = (uint32_t)(tok - tb) * ROW_B + 16 * (64 + ((lane & 7) ^ swz(lane >> 3)));
+    const uint32_t off = (uint32_t)(tok - tb) * ROW_B + 16 * (64 + ((lane & 7) ^ swz_rope(r0 + (lane >> 3))));
     dma16(kvb + (size_t)tb * ROW_B, off, rope + r0 * 128);
   }
 }
@@ -210,22 +225,28 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
   if (nblk > 1) issue(1);
 
   // K fragment (A operand): row l32, chunk c = 2 ks + hsel at position
-  // 8 (ks/4) + ((2 (ks%4) + hsel) ^ swz(l32)): four lane offsets plus an
-  // immediate per k-step; the rope rows (ks >= 32) are 128 B apart.
-  const int kx = swz(l32);
-  int koff[4];
+  // 16 (ks/8) + ((2 (ks%8) + hsel) ^ swz_lat(l32)): eight lane offsets plus
+  // an immediate per k-step; the rope rows (ks >= 32, 128 B apart) have
+  // four of their own.
+  int koff[8], kroff[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) koff[m] = l32 * 1024 + 16 * ((2 * m + hsel) ^ kx);
+  for (int m = 0; m < 8; ++m) koff[m] = l32 * 1024 + 16 * ((2 * m + hsel) ^ swz_lat(l32));
+#pragma unroll
+  for (int m = 0; m < 4; ++m) kroff[m] = l32 * 128 + 16 * ((2 * m + hsel) ^ swz_rope(l32));
   // V^T fragment via transposing reads: in lane group q = lane/16, lane
-  // 4j + a addresses row 16 k2 + 4 (q>>1) + j (+8 for the upper half of
-  // k) and latent column 128 wave + 32 dt + 16 (q&1) + 4a.
+  // 4j + a addresses row 16 k2 + 4 (q>>1) + j + 8 h (h = 1 for the upper
+  // half of k) and latent column 128 wave + 32 dt + 16 (q&1) + 4a, i.e.
+  // chunk 16 wave + 4 dt + vw of that row: one lane offset per (dt, h).
   const int q4 = lane >> 4, ja = lane & 15;
   const int vj = ja >> 2, va = ja & 3;
   const int vrow = 4 * (q4 >> 1) + vj;
   const int vw = 2 * (q4 & 1) + (va >> 1);
-  const int v_base = vrow * 1024 + 256 * wave + 8 * (va & 1);
-  const int v_off_e = v_base + 16 * (vw ^ swz(vrow));
-  const int v_off_o = v_base + 16 * ((vw + 4) ^ swz(vrow));
+  int v_off[VTW][2];
+#pragma unroll
+  for (int dt = 0; dt < VTW; ++dt)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      v_off[dt][h] = (vrow + 8 * h) * 1024 + 256 * wave + 8 * (va & 1) + 16 * ((4 * dt + vw) ^ swz_lat(vrow + 8 * h));
 
   // Value role accumulators: head group g, latent tile dt of this wave.
   f32x16 acc[NWAVES][VTW];
@@ -242,9 +263,9 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
   // at the address unit all at once. ----
   auto score_mfma = [&](int si, int dma) {
     const unsigned char* lat = smem + (si & (NLAT - 1)) * LAT_B;
-    const unsigned char* rope = smem + ROPE_OFF + (si % NROPE) * ROPE_B - l32 * (1024 - 128);
+    const unsigned char* rope = smem + ROPE_OFF + (si % NROPE) * ROPE_B;
     auto kread = [&](int ks) {
-      return ks < 32 ? ld128(lat + koff[ks & 3] + 128 * (ks >> 2)) : ld128(rope + koff[ks & 3]);
+      return ks < 32 ? ld128(lat + koff[ks & 7] + 256 * (ks >> 3)) : ld128(rope + kroff[ks & 3]);
     };
     constexpr int KLA = 6;
     f32x16 sa = f32x16{};
@@ -346,9 +367,9 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
       for (int dt = 0; dt < VTW; ++dt) {
-        const unsigned char* p = lat + 16 * k2 * 1024 + ((dt & 1) ? v_off_o : v_off_e) + 128 * (dt >> 1);
-        const u32x2 lo = lds_read_tr16(p);
-        const u32x2 hi = lds_read_tr16(p + 8 * 1024);
+        const unsigned char* p = lat + 16 * k2 * 1024;
+        const u32x2 lo = lds_read_tr16(p + v_off[dt][0]);
+        const u32x2 hi = lds_read_tr16(p + v_off[dt][1]);
         vf[k2][dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
     float mx = -INFINITY;
