@@ -263,7 +263,7 @@ def parity_failures(results: dict) -> list[str]:
     for name, rec in results.items():
         par = rec.get("parity")
         if par is None:
-            if name != "hipblaslt_8192":  # the vendor reference line computes nothing of this path
+            if name not in REFERENCE_LINES:
                 bad.append(f"{name}: no parity check")
             continue
         e = par.get("output_normwise")
@@ -522,6 +522,25 @@ def case_hipblaslt_8192(c: Ctx) -> dict:
             "fp8_per_tensor_mean_ms": ms_fp8,
             "bf16_1024_tflops": c.F.tflops(c.F.gemm_flops(s0), ms_1024), "bf16_1024_mean_ms": ms_1024,
             "note": "vendor library on the same GPU for comparison; not part of this repository's path"}
+
+
+def case_hbm_copy(c: Ctx) -> dict:
+    """A plain device copy (torch's copy kernel, 128 MiB read + 128 MiB
+    written per step) over rotated buffers, timed like the HBM-bound cases:
+    the streaming bandwidth this GPU delivers with caches defeated, as a
+    reference line for the decode kernels' rotated figures."""
+    import torch
+
+    n = 128 << 20
+    per_set = 2 * n
+    sets = [(torch.ones(n, dtype=torch.uint8, device="cuda"), torch.empty(n, dtype=torch.uint8, device="cuda"))
+            for _ in range(rotation_count(per_set))]
+    ms, wall = time_graph_rotated([lambda t=t: t[1].copy_(t[0]) for t in sets], c.steps, c.warmup)
+    del sets
+    return {"workload": f"device copy {n >> 20} MiB -> {n >> 20} MiB, rotated buffers", "unit": "GB/s",
+            "mean_ms": ms, "wall_ms": wall, "value": c.F.gbps(per_set, ms),
+            "frac_hbm_peak": c.F.gbps(per_set, ms) / c.F.PEAK_HBM_GBPS,
+            "note": "reference line: torch's device copy, not this repository's path"}
 
 
 def case_mla_decode(c: Ctx) -> dict:
@@ -814,7 +833,10 @@ CASES = {
     "quant_fp8_act": case_quant_fp8_act,
     "mla_prefill": case_mla_prefill,
     "hipblaslt_8192": case_hipblaslt_8192,
+    "hbm_copy": case_hbm_copy,
 }
+# vendor / runtime reference lines: they compute nothing of this path
+REFERENCE_LINES = ("hipblaslt_8192", "hbm_copy")
 # the BASELINE.json configs; these and the absorbed step, KDA, the
 # quantiser and the prefill carry a roofline block and a CPU leg
 BASELINE_CASES = ("gqa", "gemm_bf16_1024", "gemm_bf16_8192", "gemm_fp8_8192", "mla_decode", "gdn_decode")

@@ -123,7 +123,7 @@ def main() -> int:
     args = ap.parse_args()
 
     H.banner()
-    print("bf16 row: mx_gemm_bf16 (32x32x16 bf16 MFMA, fp32 accumulate, bf16 out)")
+    print("bf16 row: mx_gemm_bf16 (bf16 MFMA kernels chosen by shape, fp32 accumulate, bf16 out)")
     print()
     if args.export_cubins:
         lib = importlib.import_module("cuda-oxide-bench_amd._lib")

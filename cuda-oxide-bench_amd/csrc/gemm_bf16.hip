@@ -4,28 +4,32 @@
 // accumulator -> bf16 store, zero padding at ragged edges) and the bf16 row
 // of cutile-matmul-tiled-mixed/main.py:121-130.
 //
-// Two kernels (MI355X-first designs, not translations of the reference's
-// cuTile/WMMA kernels), both on 32x32x16 bf16 MFMAs issued as
-// D^T = B^T . A^T, so each lane holds runs of four consecutive n of one row
-// of C and the epilogue writes 8-byte bf16 quads; workgroup ids are
-// remapped so that tiles sharing A rows / B columns run on the same XCD
-// (own L2), in groups of GROUP_M tile rows.
+// The kernels (MI355X-first designs, not translations of the reference's
+// cuTile/WMMA kernels) all compute D^T = B^T . A^T, so each lane holds runs
+// of four consecutive n of one row of C and the epilogue writes 8-byte bf16
+// quads; workgroup ids are remapped so that tiles sharing A rows / B
+// columns run on the same XCD (own L2), in groups of GROUP_M tile rows.
 //
-// gemm_bf16_dma_kernel (at least one 256x256 tile per CU, K % 32 == 0):
-// 256x256 tiles, 8 waves, A/B tiles copied HBM -> LDS by direct loads into
-// a 5-stage ring, one barrier per K tile, the next k-step's LDS reads
-// interleaved with the current MFMAs.  Details at the kernel.
+// gemm_bf16_dma16_kernel (the large problems: at least one 256x256 tile
+// per CU, K % 32 == 0; also 128x128 tiles when those are at least one per
+// CU): 16x16x32 bf16 MFMAs, 8 waves of 128x64 (64x32 at 128x128 tiles),
+// A/B tiles copied HBM -> LDS by direct loads into a 5-stage (6 at
+// 128x128) ring, one barrier per K tile, the next K tile's fragments read
+// during the current tile's MFMAs.  Details at the kernel.
 //
-// gemm_bf16_dma16_kernel on 128x128 tiles (at least one per CU, fewer than
-// one 256x256 tile per CU, K % 32 == 0, e.g. 2048^3): the same design with
-// 8 waves of 64x32 and a 6-stage ring of 16 KB stages.
+// gemm_bf16_sdma_kernel (about one 64x64 tile per CU and a long K, e.g.
+// 1024^3): two wave groups split K, each with its own direct-load ring.
 //
 // gemm_bf16_stream_kernel (K % 64 == 0; M <= 64 and N >= 256, or at most 64
 // tiles of 64x64 and K >= 512): products too small to fill the CUs with
 // tiles stream B through workgroups of 32 columns x 32 or 64 rows whose
 // waves split K.
 //
-// gemm_bf16_kernel (everything else: small or ragged-K problems):
+// gemm_bf16_smallm_kernel / gemm_bf16_smallm_sk_kernel (batched items with
+// M <= 32): single-wave or K-split 4-wave workgroups over the whole K.
+//
+// gemm_bf16_kernel (everything else: small or ragged-K problems; 32x32x16
+// bf16 MFMAs):
 //  * One workgroup computes a BM x BN tile of C with WM x WN waves; each
 //    wave owns a (BM/WM) x (BN/WN) sub-tile of 32x32 fragments.
 //  * K advances in 64-deep tiles staged through LDS via registers, double
@@ -45,40 +49,15 @@
 
 #include "mx_common.h"
 
-// K depth and ring stages of the direct-load kernel.
-#ifndef MX_BF16_BK
-#define MX_BF16_BK 32
-#endif
-#ifndef MX_BF16_NS
-#define MX_BF16_NS 5
-#endif
-#ifndef MX_BF16_WM
-#define MX_BF16_WM 2
-#endif
-#ifndef MX_BF16_WN
-#define MX_BF16_WN 4
-#endif
-// 1: the 16x16x32-MFMA direct-load kernel (BK fixed at 32), 0: the 32x32x16 one
-#ifndef MX_BF16_SMALLM_SK
-#define MX_BF16_SMALLM_SK 1
-#endif
-#ifndef MX_BF16_SDMA
-#define MX_BF16_SDMA 1
-#endif
-#ifndef MX_BF16_MFMA16
-#define MX_BF16_MFMA16 1
-#endif
-// Ring stages and waves across N of the same kernel on 128x128 tiles (16 KB
-// stages; 6 measured best of 4..9 at 2048^3).
-#ifndef MX_BF16_D128_NS
-#define MX_BF16_D128_NS 6
-#endif
-#ifndef MX_BF16_D128_WN
-#define MX_BF16_D128_WN 4
-#endif
-
 namespace mx {
 namespace gemm {
+
+// The direct-load 16x16x32 kernel: K depth of a ring stage (bf16 elements),
+// ring stages and waves at 256x256 tiles, and stages and waves across N at
+// 128x128 tiles (16 KB stages; 6 measured best of 4..9 at 2048^3).
+constexpr int DMA_BK = 32;
+constexpr int DMA_NS = 5, DMA_WM = 2, DMA_WN = 4;
+constexpr int D128_NS = 6, D128_WN = 4;
 
 constexpr int BK = 64;  // K tile depth (bf16 elements)
 constexpr int GROUP_M = 8;
@@ -332,257 +311,13 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 1) void gemm_bf16_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// Large-problem kernel: 256x256 tiles fed by direct HBM -> LDS loads.
-//
-//  * WM x WN waves; each wave owns a (256/WM) x (256/WN) block of C as
-//    32x32 fragments, accumulated as C^T = B^T . A^T so a lane holds one m
-//    and runs of four n (8-byte bf16 stores).
-//  * A [256][BK] and B [BK][256] tiles are copied HBM -> LDS with
-//    global_load_lds_dwordx4 (1 KB per instruction, no VGPR staging) into
-//    an NS-stage ring; loads run NS-1 tiles ahead of the MFMAs.  The ring
-//    depth matters on MI355X: at BK=32, 3 stages reach ~1.06 PFLOP/s at
-//    8192^3, 4 stages ~1.23 and 5 (all 160 KB of LDS) ~1.24-1.27.
-//  * The next k-step's fragments are read between the current k-step's
-//    MFMAs (one or two LDS reads per MFMA): lgkmcnt counts at most 15
-//    outstanding LDS instructions, so a whole k-step of reads (8) cannot
-//    be waited for separately from the next one's otherwise.
-//  * One barrier per K tile, placed before the MFMAs of the tile's last
-//    k-step: it publishes tile kt+1 (so its first fragments are read while
-//    those MFMAs run) and frees the stage of tile kt-1 for tile kt+NS-1.
-//  * 16-byte chunks are XOR-swizzled per row (the DMA writes rows in lane
-//    order, so rows cannot be padded):
-//      A rows (BK*2 bytes): a 16-lane ds_read_b128 phase reads one chunk of
-//        16 consecutive rows -> chunk ^ swz_a(m) puts them in 16 distinct
-//        16-byte slots of the 256-byte bank sweep;
-//      B rows (512 bytes): a 32-lane ds_read_b64_tr_b16 phase reads 4
-//        consecutive k-rows x 64 bytes -> chunk ^ ((k & 3) << 2) gives each
-//        row its own 64-byte quarter.
-// ---------------------------------------------------------------------------
+// A-row chunk swizzle of the small-M kernels' LDS rows: a 16-lane
+// ds_read_b128 phase reads one chunk of 16 consecutive rows, and chunk ^
+// swz_a(m) puts them in 16 distinct 16-byte slots of the 256-byte bank
+// window (64-byte rows: (m >> 2) & 3; 128-byte rows: (m >> 1) & 7).
 template <int BK>
 __device__ __forceinline__ int swz_a(int m) {
   return BK == 64 ? ((m >> 1) & 7) : ((m >> 2) & 3);
-}
-__device__ __forceinline__ int swz_b(int k) { return (k & 3) << 2; }
-
-template <int BK, int NS, int WM, int WN>
-struct DCfg {
-  static constexpr int BM = 256, BN = 256;
-  static constexpr int NW = WM * WN, NT = 64 * NW;
-  static constexpr int TM = BM / WM, TN = BN / WN;  // wave block
-  static constexpr int FM = TM / 32, FN = TN / 32;
-  static constexpr int KS = BK / 16;                // k-steps per tile
-  static constexpr int RA = BK * 2;                 // A row bytes in LDS
-  static constexpr int RB = BN * 2;                 // B row bytes in LDS
-  static constexpr int A_B = BM * RA, B_B = BK * RB;
-  static constexpr int STAGE = A_B + B_B;
-  static constexpr int A_LPW = A_B / 1024 / NW;     // 1 KB loads per wave per stage
-  static constexpr int B_LPW = B_B / 1024 / NW;
-  static constexpr int LPW = A_LPW + B_LPW;
-  static constexpr int A_CH = RA / 16, A_RPL = 1024 / RA;  // chunks per A row, A rows per load
-  static constexpr int B_CH = RB / 16, B_RPL = 1024 / RB;
-  static_assert(BK == 32 || BK == 64, "A swizzle");
-  static_assert(NS >= 3 && NS <= 5 && NS * STAGE <= 160 * 1024, "LDS ring");
-  static_assert((NS - 3) * LPW < 64, "vmcnt range");
-  static_assert(A_LPW >= 1 && B_LPW >= 1 && FM >= 1 && FN >= 1, "tile split");
-};
-
-template <int BK, int NS, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_dma_kernel(const uint16_t* __restrict__ A,
-                                                                      const uint16_t* __restrict__ B,
-                                                                      uint16_t* __restrict__ C, int M, int N,
-                                                                      int K, int lda, int ldb, int ldc) {
-  using CF = DCfg<BK, NS, WM, WN>;
-  constexpr int FM = CF::FM, FN = CF::FN, KS = CF::KS;
-  extern __shared__ __align__(1024) unsigned char smem[];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;
-  const int g = lane >> 5;
-
-  // ---- tile -> (tm, tn), grouped for L2 reuse, XCD-aware ----
-  const int tiles_m = (M + CF::BM - 1) / CF::BM, tiles_n = (N + CF::BN - 1) / CF::BN;
-  const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
-  const int per_group = GROUP_M * tiles_n;
-  const int group = id / per_group;
-  const int first_m = group * GROUP_M;
-  const int gsz = min(tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (id % per_group) % gsz;
-  const int tn = (id % per_group) / gsz;
-  const int m0 = tm * CF::BM, n0 = tn * CF::BN;
-  const int nk = K / BK;
-
-  // ---- direct-load lane offsets (bytes from the tile's first element).
-  // A load n of this wave: rows A_RPL*(wave*A_LPW+n) + lane/A_CH; B load n:
-  // k-rows B_RPL*(wave*B_LPW+n) + lane/B_CH.  Rows past M / columns past N
-  // re-read the last valid ones; their results are never stored. ----
-  const uint32_t lds0 = lds_addr(smem);
-  const bool full_m = m0 + CF::BM <= M, full_n = n0 + CF::BN <= N;
-  uint32_t a_off[CF::A_LPW], b_off[CF::B_LPW];
-#pragma unroll
-  for (int n = 0; n < CF::A_LPW; ++n) {
-    const int row = CF::A_RPL * (wave * CF::A_LPW + n) + lane / CF::A_CH;
-    const int gm = full_m ? m0 + row : min(m0 + row, M - 1);
-    a_off[n] = (uint32_t)(gm - m0) * (uint32_t)lda * 2u + 16u * ((lane % CF::A_CH) ^ swz_a<BK>(row));
-  }
-#pragma unroll
-  for (int n = 0; n < CF::B_LPW; ++n) {
-    const int row = CF::B_RPL * (wave * CF::B_LPW + n) + lane / CF::B_CH;
-    int col = 8 * ((lane % CF::B_CH) ^ swz_b(row));  // elements
-    if (!full_n) col = min(n0 + col, N - 8) - n0;
-    b_off[n] = (uint32_t)row * (uint32_t)ldb * 2u + 2u * col;
-  }
-  auto issue = [&](int kt, int stage) {
-    const uint32_t st = lds0 + stage * CF::STAGE;
-    const uint16_t* abase = A + (size_t)m0 * lda + (size_t)kt * BK;
-    const uint16_t* bbase = B + (size_t)kt * BK * ldb + n0;
-#pragma unroll
-    for (int n = 0; n < CF::A_LPW; ++n) dma16(abase, a_off[n], st + (wave * CF::A_LPW + n) * 1024);
-#pragma unroll
-    for (int n = 0; n < CF::B_LPW; ++n) dma16(bbase, b_off[n], st + CF::A_B + (wave * CF::B_LPW + n) * 1024);
-  };
-
-  // ---- fragment lane addresses, one set per ring stage: stages start past
-  // the 16-bit immediate offset of ds_read, so each stage gets base
-  // registers and a stage's fragments differ only by immediates. ----
-  // A^T (B operand of the MFMA): m = wm*TM + 32 mf + lane%32, k-chunk 2 ks + g.
-  const int am = wm * CF::TM + (lane & 31);
-  uint32_t a_col[NS][KS];
-#pragma unroll
-  for (int st = 0; st < NS; ++st)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      a_col[st][ks] = lds0 + st * CF::STAGE + am * CF::RA + 16 * ((2 * ks + g) ^ swz_a<BK>(am));
-      asm volatile("" : "+v"(a_col[st][ks]));  // keep it a base register
-    }
-  // B^T (A operand) by transposing reads: lane (g, sg, 4j+a) reads k-row
-  // 16 ks + 8 g + 4 r + j, columns wn*TN + 32 nf + 16 sg + 4a .. +3.
-  const int b_sg = (lane >> 4) & 1, b_j = (lane >> 2) & 3, b_a = lane & 3;
-  uint32_t b_col[NS][FN];
-#pragma unroll
-  for (int st = 0; st < NS; ++st)
-#pragma unroll
-    for (int nf = 0; nf < FN; ++nf) {
-      const int chunk = (wn * CF::TN + 32 * nf + 16 * b_sg + 4 * b_a) >> 3;
-      b_col[st][nf] = lds0 + st * CF::STAGE + CF::A_B + (8 * g + b_j) * CF::RB + 16 * (chunk ^ swz_b(b_j)) +
-                      8 * (b_a & 1);
-      asm volatile("" : "+v"(b_col[st][nf]));
-    }
-
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
-
-  // Fragments, double buffered by k-step parity.
-  u32x4 bf[2][FN], af[2][FM];
-  auto read = [&](int stg, int ks, int buf) {
-#pragma unroll
-    for (int nf = 0; nf < FN; ++nf) {
-      const uint32_t p = b_col[stg][nf] + 16 * ks * CF::RB;
-      const u32x2 lo = lds_read_tr16_at(p);
-      const u32x2 hi = lds_read_tr16_at(p + 4 * CF::RB);
-      bf[buf][nf] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-    }
-#pragma unroll
-    for (int mf = 0; mf < FM; ++mf) af[buf][mf] = lds_ld128(a_col[stg][ks] + 32 * mf * CF::RA);
-  };
-  // One K tile.  On entry the fragments of its k-step 0 are in buffer 0;
-  // the reads of the next k-step are spread between the MFMAs of the
-  // current one.  Every step issues exactly one tile of loads (near the end
-  // the last tile again, into stages nobody reads), so the ring's load
-  // accounting is the same in every step and the loop has no branches.
-  constexpr int NM = FM * FN, NR = 2 * FN + FM;  // MFMAs and LDS reads per k-step
-  auto mfmas = [&](int buf) {
-#pragma unroll
-    for (int mf = 0; mf < FM; ++mf)
-#pragma unroll
-      for (int nf = 0; nf < FN; ++nf) acc[mf][nf] = mfma32<BF16>(bf[buf][nf], af[buf][mf], acc[mf][nf]);
-  };
-  auto step = [&](int kt, auto stg_tag) {
-    constexpr int STG = decltype(stg_tag)::value;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < KS) {
-        read(STG, ks + 1, cur ^ 1);
-      } else {
-        // Every wave has consumed tile kt-1 (its MFMAs needed those reads)
-        // and its own loads of tile kt+1 have landed (at most the NS-3
-        // tiles issued after it are in flight): after the barrier, tile
-        // kt+1 is readable and stage (kt-1)%NS takes tile kt+NS-1.
-        wait_vmcnt<(NS - 3) * CF::LPW>();
-        lds_barrier();
-        issue(min(kt + NS - 1, nk - 1), (STG + NS - 1) % NS);
-        __builtin_amdgcn_sched_barrier(0);
-        read((STG + 1) % NS, 0, 0);
-      }
-      mfmas(cur);
-      interleave_mfma_ds<NM, NR>();
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  static_assert(KS % 2 == 0, "k-step 0 of every tile uses buffer 0");
-
-  land_args(C);  // C is used only after the K loop
-  // Prologue: tiles 0 .. NS-2 in flight (as in every step, tiles past the
-  // end re-load the last one), wait for tile 0.
-#pragma unroll
-  for (int p = 0; p < NS - 1; ++p) issue(min(p, nk - 1), p);
-  wait_vmcnt<(NS - 2) * CF::LPW>();
-  lds_barrier();
-  read(0, 0, 0);
-  int kt = 0;
-  for (; kt + NS <= nk; kt += NS) {
-    step(kt, std::integral_constant<int, 0>{});
-    step(kt + 1, std::integral_constant<int, 1>{});
-    step(kt + 2, std::integral_constant<int, 2>{});
-    if constexpr (NS >= 4) step(kt + 3, std::integral_constant<int, 3>{});
-    if constexpr (NS >= 5) step(kt + 4, std::integral_constant<int, 4>{});
-  }
-  // the last nk % NS tiles (stage of tile kt is 0 here)
-  if (kt < nk) step(kt, std::integral_constant<int, 0>{});
-  if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
-  if constexpr (NS >= 4)
-    if (kt + 2 < nk) step(kt + 2, std::integral_constant<int, 2>{});
-  if constexpr (NS >= 5)
-    if (kt + 3 < nk) step(kt + 3, std::integral_constant<int, 3>{});
-  wait_vmcnt<0>();  // no DMA may land in LDS after the workgroup ends
-
-  // ---- epilogue: lane holds m = m0 + am + 32 mf, n = n0 + wn*TN + 32 nf + 8 i + 4 g + {0..3} ----
-#pragma unroll
-  for (int mf = 0; mf < FM; ++mf) {
-    const int gm = m0 + am + 32 * mf;
-    if (gm >= M) continue;
-    uint16_t* crow = C + (size_t)gm * ldc;
-#pragma unroll
-    for (int nf = 0; nf < FN; ++nf)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int gn = n0 + wn * CF::TN + 32 * nf + 8 * i + 4 * g;
-        if (gn < N) {
-          const f32x16& a = acc[mf][nf];
-          st64(crow + gn, u32x2{pack_bf16x2(a[4 * i], a[4 * i + 1]), pack_bf16x2(a[4 * i + 2], a[4 * i + 3])});
-        }
-      }
-  }
-}
-
-template <int BK, int NS, int WM, int WN>
-static int launch_dma(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
-                      hipStream_t stream) {
-  using CF = DCfg<BK, NS, WM, WN>;
-  const long long tiles = (long long)((M + CF::BM - 1) / CF::BM) * ((N + CF::BN - 1) / CF::BN);
-  if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
-  const int smem = NS * CF::STAGE;
-  constexpr auto kern = gemm_bf16_dma_kernel<BK, NS, WM, WN>;
-  MX_RETURN_IF_HIP(lds_limit_once<kern>(smem));
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CF::NT), smem, stream, (const uint16_t*)A,
-                     (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
-  MX_RETURN_IF_HIP(hipGetLastError());
-  return MX_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -1275,7 +1010,6 @@ __global__ __launch_bounds__(64 * KW) void gemm_bf16_smallm_sk_kernel(const uint
 static int launch_smallm(const void* A, const void* B, void* C, int batch, int M, int N, int K, int lda, int ldb,
                          int ldc, long long sA, long long sB, long long sC, hipStream_t stream) {
   auto groups = [&](int tn) { return (long long)batch * ((N + tn - 1) / tn); };
-#if MX_BF16_SMALLM_SK
   // 4..12 chunks of K, split among 4 waves: one workgroup per 32 x 64 tile
   // when that still gives >= 256 workgroups (one per CU), else 32 x 32.
   const int nkc = K / SM_BK;
@@ -1298,7 +1032,6 @@ static int launch_smallm(const void* A, const void* B, void* C, int batch, int M
     MX_RETURN_IF_HIP(hipGetLastError());
     return MX_OK;
   }
-#endif
   // Widest column tile that still leaves >= 512 workgroups (two per CU).
   const int nf = groups(128) >= 512 ? 4 : (groups(64) >= 512 ? 2 : 1);
   const long long grid = groups(32 * nf);
@@ -1496,10 +1229,6 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   if ((K % 8) || (N % 8) || (lda % 8) || (ldb % 8) || (ldc % 8)) return MX_ERR_ALIGN;
   if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15) return MX_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-#ifndef MX_BF16_STREAM
-#define MX_BF16_STREAM 1
-#endif
-#if MX_BF16_STREAM
   // Stream the weights with whole 64-deep K blocks (32-bit lane offsets: 64
   // rows of A and 64 k-rows of B span < 4 GiB) for decode-sized M against
   // at least 256 columns, and for any product with at most 64 tiles of
@@ -1511,7 +1240,6 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
       (long long)lda * 2 * 64 <= 0xffffffffLL && (long long)ldb * 2 * 64 <= 0xffffffffLL)
     return M <= 32 ? mx::gemm::launch_stream<1, 4>(A, B, C, M, N, K, lda, ldb, ldc, s)
                    : mx::gemm::launch_stream<2, 3>(A, B, C, M, N, K, lda, ldb, ldc, s);
-#endif
   const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
   const long long tiles128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
   // Rounds of 256 workgroups: a round of 256x256 tiles of the direct-load
@@ -1523,31 +1251,26 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   const bool big = tiles256 >= 256 || 13 * r256 < 5 * r128;
   // Whole K tiles: the direct-load kernel (its lane offsets are 32-bit: 256
   // rows of A must span < 4 GiB).
-  if (big && K % MX_BF16_BK == 0 && (long long)lda * 2 * 256 <= 0xffffffffLL) {
-#if MX_BF16_MFMA16
-    return mx::gemm::launch_dma16<MX_BF16_NS, MX_BF16_WM, MX_BF16_WN>(A, B, C, M, N, K, lda, ldb, ldc, s);
-#else
-    return mx::gemm::launch_dma<MX_BF16_BK, MX_BF16_NS, MX_BF16_WM, MX_BF16_WN>(A, B, C, M, N, K, lda, ldb, ldc, s);
-#endif
-  }
+  if (big && K % mx::gemm::DMA_BK == 0 && (long long)lda * 2 * 256 <= 0xffffffffLL)
+    return mx::gemm::launch_dma16<mx::gemm::DMA_NS, mx::gemm::DMA_WM, mx::gemm::DMA_WN>(A, B, C, M, N, K, lda, ldb,
+                                                                                          ldc, s);
   // Otherwise: register-staged kernels, big tiles when they still cover the
   // 256 CUs twice, else smaller tiles for parallelism.
   if (tiles256 >= 512) return mx::gemm::launch<256, 256, 2, 4>(A, B, C, M, N, K, lda, ldb, ldc, s);
   // At least one 128x128 tile per CU and whole K tiles: the direct-load
   // kernel on 128x128 tiles, whose 16 KB stages allow a deeper ring.
-  if (tiles128 >= 256 && K % MX_BF16_BK == 0 && (long long)lda * 2 * 128 <= 0xffffffffLL)
-    return mx::gemm::launch_dma16<MX_BF16_D128_NS, 2, MX_BF16_D128_WN, 128, 128>(A, B, C, M, N, K, lda, ldb, ldc, s);
+  if (tiles128 >= 256 && K % mx::gemm::DMA_BK == 0 && (long long)lda * 2 * 128 <= 0xffffffffLL)
+    return mx::gemm::launch_dma16<mx::gemm::D128_NS, 2, mx::gemm::D128_WN, 128, 128>(A, B, C, M, N, K, lda, ldb,
+                                                                                      ldc, s);
   if (tiles128 >= 256) return mx::gemm::launch<128, 128, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
   // About one 64x64 tile per CU or fewer and a long K (e.g. 1024^3): split
   // K between two wave groups of each workgroup.
   const long long tiles64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
-#if MX_BF16_SDMA
   // ... with whole 64x64 tiles and 128-deep K chunks: the direct-load ring
   // (32-bit lane offsets: 64 rows of A and 64 k-rows of B span < 4 GiB).
   if (tiles64 <= 256 && K >= 512 && M % 64 == 0 && N % 64 == 0 && K % 128 == 0 &&
       (long long)lda * 2 * 64 <= 0xffffffffLL && (long long)ldb * 2 * 64 <= 0xffffffffLL)
     return mx::gemm::launch_sdma(A, B, C, M, N, K, lda, ldb, ldc, s);
-#endif
   if (tiles64 <= 256 && K >= 512) return mx::gemm::launch<64, 64, 2, 2, 2, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
   return mx::gemm::launch<64, 64, 2, 2, 1, 2>(A, B, C, M, N, K, lda, ldb, ldc, s);
 }

@@ -621,17 +621,15 @@ extern "C" int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, con
   // so the big tile wins unless the small one needs fewer than 2.4 times
   // its rounds (3072^3: 1 round against 3, 57 vs 72 us; 2560^3: 1 against
   // 2, 44 vs 38 us).
-#ifndef MX_FP8_SMALLM_NW
-#define MX_FP8_SMALLM_NW 4
-#endif
+  constexpr int SMALLM_NW = 4;  // waves of the weight-streaming kernel (each takes every 4th scale block)
   // Decode-sized M, or at most 64 tiles of 128x128 with M <= 512: stream
   // the weights with 32-column workgroups (graph-replayed: 256x4096x4096
   // 27.5 -> 22.5 us, 512x1024x4096 27.4 -> 12.3 us; 1024^3 stays tiled,
   // 10.6 against 11.8 us).
-  if (M <= 32) return mx::gemm8::launch_smallm<1, MX_FP8_SMALLM_NW, 4>(A, sA, B, sB, C, M, N, K, s);
+  if (M <= 32) return mx::gemm8::launch_smallm<1, SMALLM_NW, 4>(A, sA, B, sB, C, M, N, K, s);
   const long long tiles128s = (long long)((M + 127) / 128) * ((N + 127) / 128);
   if (M <= 64 || (tiles128s <= 64 && M <= 512))
-    return mx::gemm8::launch_smallm<2, MX_FP8_SMALLM_NW, 3>(A, sA, B, sB, C, M, N, K, s);
+    return mx::gemm8::launch_smallm<2, SMALLM_NW, 3>(A, sA, B, sB, C, M, N, K, s);
   const long long r256 = (tiles256 + 255) / 256, r128 = (tiles128 + 255) / 256;
   if (tiles256 >= 256 || 12 * r256 < 5 * r128) return mx::gemm8::launch<256, 256>(A, sA, B, sB, C, M, N, K, s);
   return mx::gemm8::launch<128, 128>(A, sA, B, sB, C, M, N, K, s);

@@ -477,19 +477,17 @@ __global__ __launch_bounds__(NT, 1) void mla_decode_kernel(const uint16_t* __res
 // with 128-bit loads.  With many splits (small batches) SG threads share an
 // element, each summing one of SG slices of the splits, and their sums meet
 // in LDS: the serial chain of loads per thread stays near nsplit / SG.
-#ifndef MX_MLA_CMB_WG_MANY
-#define MX_MLA_CMB_WG_MANY 512
-#endif
-#ifndef MX_MLA_CMB_WG_ONE
-#define MX_MLA_CMB_WG_ONE 256
-#endif
+// Merge workgroup sizes: 256 threads with one slice per element, 512 with
+// split slices (measured: 512 took B4 H128 T4096 from 27.9 to 25.9 us; at
+// one slice 256 measured 0.5-2 us faster than 512 at B16-B64).
+constexpr int CMB_WG_ONE = 256, CMB_WG_MANY = 512;
 constexpr int CMB_ET = VT * 4 * 32;  // element-threads per (b, 32-head group) tile = 2048
 
 template <int SG>
 struct CmbCfg {
   // Threads per workgroup: with split slices, larger workgroups cover more
   // output elements each, so fewer of them stage the same (m, l) pairs.
-  static constexpr int WG = SG == 1 ? MX_MLA_CMB_WG_ONE : MX_MLA_CMB_WG_MANY;
+  static constexpr int WG = SG == 1 ? CMB_WG_ONE : CMB_WG_MANY;
   static constexpr int ET = WG / SG;         // element-threads per workgroup
   static constexpr int PER = CMB_ET / ET;    // workgroups per tile
   static constexpr int MAXS = SG == 1 ? 32 : 256;  // most splits; their (m, l) are staged in LDS (8 or 64 KB)
@@ -719,59 +717,6 @@ extern "C" int mx_mla_decode(const void* Q, const void* KV, void* O, int B, int 
   if (need > 0 && (!workspace || ws_bytes < need)) return MX_ERR_WORKSPACE;
   if (need > 0 && ((uintptr_t)workspace & 15)) return MX_ERR_ALIGN;
   return launch_decode(Q, (const uint16_t*)Q + DV, DQK, DQK, KV, O, B, H, T, scale, workspace, (hipStream_t)stream);
-}
-
-// ---------------------------------------------------------------------------
-// Allocation-free decode: the split partials go to a library-owned device
-// array instead of a caller workspace.  `scratch` is a host-side stand-in
-// for the array in host code, not a device address: its device address
-// is looked up once per device (with that device current) and only that
-// address is ever passed to a kernel.  Every call on one GPU shares that
-// GPU's array, so calls that overlap on one GPU race; the kernels write
-// every partial before the combine reads it, so nothing needs clearing.
-// ---------------------------------------------------------------------------
-namespace mx {
-namespace mla {
-
-static __device__ __align__(256) unsigned char scratch[MX_MLA_SCRATCH_BYTES];
-
-static std::once_flag scratch_once[kMaxDevices];
-static void* scratch_dev[kMaxDevices];
-static hipError_t scratch_rc[kMaxDevices];
-
-// Device address of this device's `scratch`, looked up on the first call.
-static int scratch_ptr(void** out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return MX_ERR_LAUNCH;
-  if (dev < 0 || dev >= kMaxDevices) return MX_ERR_UNSUPPORTED;
-  std::call_once(scratch_once[dev], [dev] {
-    void* p = nullptr;
-    scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    scratch_dev[dev] = scratch_rc[dev] == hipSuccess ? p : nullptr;
-  });
-  if (scratch_rc[dev] != hipSuccess || !scratch_dev[dev]) return MX_ERR_LAUNCH;
-  *out = scratch_dev[dev];
-  return MX_OK;
-}
-
-}  // namespace mla
-}  // namespace mx
-
-extern "C" int mx_mla_decode_noalloc(const void* Q, const void* KV, void* O, int B, int H, int T, int d_latent,
-                                     int d_rope, float scale, void* stream) {
-  using namespace mx::mla;
-  if (!Q || !KV || !O) return MX_ERR_NULL;
-  if (B <= 0 || H <= 0 || T <= 0) return MX_ERR_SHAPE;
-  if (d_latent != DV || d_rope != DQK - DV) return MX_ERR_UNSUPPORTED;
-  if (const int e = check_decode(KV, B, H, T, scale)) return e;
-  if (((uintptr_t)Q | (uintptr_t)O) & 15) return MX_ERR_ALIGN;
-  const size_t need = workspace_bytes(B, H, T);
-  if (need > (size_t)MX_MLA_SCRATCH_BYTES) return MX_ERR_WORKSPACE;
-  void* ws = nullptr;
-  if (need > 0) {
-    if (const int e = scratch_ptr(&ws)) return e;
-  }
-  return launch_decode(Q, (const uint16_t*)Q + DV, DQK, DQK, KV, O, B, H, T, scale, ws, (hipStream_t)stream);
 }
 
 extern "C" size_t mx_mla_decode_absorbed_workspace(int B, int H, int T) {

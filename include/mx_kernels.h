@@ -215,7 +215,10 @@ int mx_mla_decode_splits(int B, int H, int T);
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The same kernels and results as mx_mla_decode; the split
  * partials go to a library-owned device array of MX_MLA_SCRATCH_BYTES per
- * GPU (held from the library's load until the process ends).  Problems
+ * GPU.  The array sits in a code object of its own (csrc/mla_noalloc.hip),
+ * so only processes that use this entry point hold it: with the HIP
+ * runtime's deferred code-object loading, a GPU holds it from the first
+ * call of this entry point there until the process ends.  Problems
  * whose mx_mla_decode_workspace(B, H, T, d_latent) exceeds that size return
  * MX_ERR_WORKSPACE.  All calls on one GPU share its array: calls that
  * overlap on one GPU (concurrent streams or host threads) race and must be

@@ -53,3 +53,58 @@ def test_noalloc_matches_workspace_entry_point(ops):
         ref = omla.mla_decode_ref(q, kv, s.scale, batches=list(range(min(B, 4))))
         err = normwise_rel_err(o_na.cpu()[:4], ref[:4])
         assert err <= TOL, f"normwise rel err {err:.3e}"
+
+
+_FIRST_CALL_IN_CAPTURE = r'''
+import importlib, math, sys
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+import torch
+from oracle import mla as omla
+from oracle.metrics import normwise_rel_err
+lib = importlib.import_module("cuda-oxide-bench_amd._lib").load()
+shapes = importlib.import_module("cuda-oxide-bench_amd.shapes")
+inputs = importlib.import_module("cuda-oxide-bench_amd.inputs")
+B, H, T = 3, 20, 500
+s = shapes.MLADecodeShape("t", B, H, T)
+q, kv = inputs.mla_inputs(s, seed=inputs.SEED + 7)
+qd, kvd = q.cuda(), kv.cuda()
+o = torch.full((B, H, 512), float("nan"), dtype=torch.bfloat16, device="cuda")
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):  # the process's first MLA call: scratch lookup and kernel attributes inside the capture
+    rc = lib.mx_mla_decode_noalloc(qd.data_ptr(), kvd.data_ptr(), o.data_ptr(), B, H, T, 512, 64, s.scale,
+                                   torch.cuda.current_stream().cuda_stream)
+assert rc == 0, rc
+ref = omla.mla_decode_ref(q, kv, s.scale)
+for r in range(3):
+    o.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    err = normwise_rel_err(o.cpu(), ref)
+    assert err <= 2e-2, (r, err)
+    print(f"replay {r}: normwise rel err {err:.3e}", flush=True)
+print("OK", flush=True)
+'''
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_inside_graph_capture(tmp_path):
+    """A fresh process whose first MLA call is mx_mla_decode_noalloc under
+    HIP graph capture (the caller the entry point is for): the per-device
+    scratch lookup and the kernels' LDS attributes run inside the capture,
+    and every replay of the graph matches the oracle."""
+    import subprocess
+    import sys
+
+    from conftest import REPO_ROOT
+
+    announce("mla_decode_noalloc first call inside graph capture (subprocess)")
+    script = tmp_path / "first_call_capture.py"
+    script.write_text(_FIRST_CALL_IN_CAPTURE)
+    proc = subprocess.run([sys.executable, str(script), str(REPO_ROOT)], capture_output=True, text=True,
+                          timeout=240)
+    print(proc.stdout[-2000:])
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-3000:]
+    assert proc.stdout.strip().endswith("OK")
