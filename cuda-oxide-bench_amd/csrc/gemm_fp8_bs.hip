@@ -334,22 +334,47 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   }
   wait_scales<0>(sa_n, sb_n);  // no DMA may land in LDS after the workgroup ends
 
-  // ---- store C: lane holds m = m0 + am + 32 mf, n = n0 + wn*TN + 32 nf + 8 i + 4 (l/32) + j ----
+  // ---- store C through LDS.  Lane results are runs of four n of one row
+  // (8 bytes), so direct stores would write each row of the tile in 16-byte
+  // pieces from eight instructions, which the memory system writes back as
+  // partial lines.  Instead the tile goes to LDS as bf16 rows (padded by
+  // 16 bytes so the 32 rows of a fragment store land on distinct bank
+  // slots), and the workgroup then writes whole rows, each lane 16
+  // contiguous bytes.  The ring is free: every DMA has landed (vmcnt(0)
+  // above) and the barrier below waits for every wave's last fragment
+  // reads. ----
+  constexpr int CROW = BN * 2 + 16;  // LDS bytes per staged C row
+  static_assert(BM * CROW <= CF::LDS, "C tile fits the ring");
+  __syncthreads();
+  {
+    unsigned char* ct = smem;
 #pragma unroll
-  for (int mf = 0; mf < FM; ++mf) {
-    const int gm = m0 + am + 32 * mf;
-    if (gm >= M) continue;
-    uint16_t* crow = C + (size_t)gm * N;
+    for (int mf = 0; mf < FM; ++mf) {
+      const int r = am + 32 * mf;  // tile row
 #pragma unroll
-    for (int nf = 0; nf < FN; ++nf)
+      for (int nf = 0; nf < FN; ++nf)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int gn = n0 + wn * CF::TN + 32 * nf + 8 * i + 4 * (lane >> 5);
-        if (gn < N) {
+        for (int i = 0; i < 4; ++i) {
+          const int c = wn * CF::TN + 32 * nf + 8 * i + 4 * (lane >> 5);  // tile column
           const f32x16& a = acc[nf][mf];
-          st64(crow + gn, u32x2{pack_bf16x2(a[4 * i], a[4 * i + 1]), pack_bf16x2(a[4 * i + 2], a[4 * i + 3])});
+          *reinterpret_cast<u32x2*>(ct + r * CROW + 2 * c) =
+              u32x2{pack_bf16x2(a[4 * i], a[4 * i + 1]), pack_bf16x2(a[4 * i + 2], a[4 * i + 3])};
         }
-      }
+    }
+  }
+  __syncthreads();
+  {
+    constexpr int CPR = BN / 8;          // 16-byte chunks per tile row
+    constexpr int RPI = NT / CPR;        // rows per workgroup-wide store
+    const int t = threadIdx.x;
+    const int cc = t % CPR, r0 = t / CPR;
+    const int gn = n0 + 8 * cc;
+#pragma unroll 4
+    for (int r = r0; r < BM; r += RPI) {
+      const int gm = m0 + r;
+      if (gm < M && gn < N)
+        st128(C + (size_t)gm * N + gn, *reinterpret_cast<const u32x4*>(smem + r * CROW + 16 * cc));
+    }
   }
 }
 
