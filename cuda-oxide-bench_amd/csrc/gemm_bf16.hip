@@ -698,19 +698,36 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_dma16_kernel(const 
   step_tail<NS, P>(step, kt, nk - kt);
   wait_vmcnt<0>();  // no DMA may land in LDS after the workgroup ends
 
-  // ---- epilogue: lane holds m = m0 + am + 16 mf, n = n0 + wn*TN + 16 nf + 4 kg + {0..3} ----
+  // ---- epilogue: lane holds m = am + 16 mf, n = wn*TN + 16 nf + 4 kg + {0..3}
+  // of the tile.  The tile goes through LDS (bf16 rows padded by 16 bytes)
+  // and is stored as whole rows, each lane 16 contiguous bytes, instead of
+  // 8-byte pieces that the memory system writes back as partial lines.  The
+  // ring is free once every wave is past its last fragment reads. ----
+  constexpr int CROW = CF::BN * 2 + 16;
+  static_assert(CF::BM * CROW <= NS * CF::STAGE, "C tile fits the ring");
+  __syncthreads();
 #pragma unroll
   for (int mf = 0; mf < FM; ++mf) {
-    const int gm = m0 + am + 16 * mf;
-    if (gm >= M) continue;
-    uint16_t* crow = C + (size_t)gm * ldc;
+    const int r = am + 16 * mf;
 #pragma unroll
     for (int nf = 0; nf < FN; ++nf) {
-      const int gn = n0 + wn * CF::TN + 16 * nf + 4 * kg;
-      if (gn < N) {
-        const f32x4& a = acc[mf][nf];
-        st64(crow + gn, u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])});
-      }
+      const int c = wn * CF::TN + 16 * nf + 4 * kg;
+      const f32x4& a = acc[mf][nf];
+      *reinterpret_cast<u32x2*>(smem + r * CROW + 2 * c) = u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+    }
+  }
+  __syncthreads();
+  {
+    constexpr int CPR = CF::BN / 8;     // 16-byte chunks per tile row
+    constexpr int RPI = CF::NT / CPR;   // rows per workgroup-wide store
+    const int t = threadIdx.x;
+    const int cc = t % CPR, r0 = t / CPR;
+    const int gn = n0 + 8 * cc;
+#pragma unroll 4
+    for (int r = r0; r < CF::BM; r += RPI) {
+      const int gm = m0 + r;
+      if (gm < M && gn < N)
+        st128(C + (size_t)gm * ldc + gn, *reinterpret_cast<const u32x4*>(smem + r * CROW + 16 * cc));
     }
   }
 }
