@@ -23,11 +23,9 @@
 //    O^T += V^T . P^T, where each V^T fragment (ds_read_b64_tr_b16 straight
 //    from the row-major cache rows) serves the 4 head groups.  Per stage a
 //    wave reads 8 KB of V and 8 KB of P instead of 32 KB of V;
-//  * software pipeline: iteration i computes the scores of stage i and the
-//    values of stage i-1, even waves in that order and odd waves the other
-//    way round, so at any time about half the SIMDs run the LDS-heavy
-//    score phase and half the MFMA-heavy value phase (one barrier per
-//    stage);
+//  * software pipeline: iteration i computes the scores of stage i, then
+//    the values of stage i-1 with the softmax of stage i beside their
+//    MFMAs (one barrier per stage);
 //  * cache rows go HBM -> LDS with global_load_lds_dwordx4 (no VGPR
 //    staging): latent rows into a 4-slot ring (a stage is read by the
 //    scores of one iteration and the values of the next), rope rows into a
