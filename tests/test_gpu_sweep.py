@@ -97,6 +97,37 @@ def test_gqa_random(ops, case):
     assert normwise_rel_err(o.cpu(), ref) <= TOL
 
 
+def _gqa_tile_case(rng):
+    """A random shape and a random tile among those mx_gqa_fwd_tile has at its head grouping."""
+    G = int(rng.choice([1, 2, 4, 8]))
+    wm = int(rng.choice([32, 64]))
+    waves = 8 if wm == 32 else 4
+    bms = sorted({waves * wm // h for h in (1, 2, 4, 8) if h <= waves and waves % h == 0 and G % h == 0}
+                 | ({128 // h for h in (1, 2, 4) if G % h == 0} if wm == 32 else set()))
+    return (int(rng.integers(1, 3)), int(rng.choice([1, 2])), G, int(rng.integers(1, 500)),
+            int(rng.choice([64, 128])), bool(rng.integers(0, 2)), bool(rng.integers(0, 2)),
+            int(rng.choice(bms)), wm)
+
+
+@pytest.mark.parametrize("case", _draws(211, 12, _gqa_tile_case),
+                         ids=lambda c: f"B{c[0]}kv{c[1]}G{c[2]}S{c[3]}D{c[4]}{'c' if c[5] else 'n'}"
+                                       f"{'h' if c[6] else 'b'}bm{c[7]}wm{c[8]}")
+def test_gqa_tile_random(ops, case):
+    """Seeded random shapes on random explicit tiles (mx_gqa_fwd_tile)."""
+    B, hkv, G, S, D, causal, half, bm, wm = case
+    dt = torch.float16 if half else torch.bfloat16
+    announce(f"sweep gqa tile BLOCK_M={bm} wave_m={wm} B{B} Hkv{hkv} G{G} S{S} D{D} causal={causal} {dt}")
+    assert ops.gqa_tile_supported(hkv * G, hkv, D, bm, 64, wm)
+    g = torch.Generator().manual_seed(B * 5 + hkv * 3 + G * 17 + S + D + bm + wm)
+    q = torch.randn((B, hkv * G, S, D), generator=g).to(dt)
+    k = torch.randn((B, hkv, S, D), generator=g).to(dt)
+    v = torch.randn((B, hkv, S, D), generator=g).to(dt)
+    o = ops.gqa_fwd(q.cuda(), k.cuda(), v.cuda(), causal=causal, block_m=bm, block_n=64, wave_m=wm)
+    torch.cuda.synchronize()
+    ref = ogqa.gqa_naive(q, k, v, causal=causal, scale=1.0 / math.sqrt(D))
+    assert normwise_rel_err(o.cpu(), ref) <= TOL
+
+
 # ---- MLA prefill pairs (qk 192 / v 128 and qk 96 / v 64) ----
 def _prefill_case(rng):
     dqk, dv = [(192, 128), (96, 64)][int(rng.integers(0, 2))]
