@@ -47,13 +47,28 @@ def common_flags() -> list[str]:
     ]
 
 
+# Flags for single sources.  gqa_fwd.hip: its one-wave-per-SIMD kernels
+# (512 registers) would otherwise get every builtin MFMA in AGPR form, so the
+# softmax would copy each score tile out of AGPRs; with VGPR-form builtins
+# the score MFMAs write VGPRs and only the P.V accumulators, issued as
+# inline asm, live in AGPRs.  The kernels with at most 256 registers
+# already get the VGPR form.
+SOURCE_FLAGS = {
+    "gqa_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
+def source_flags(src: Path) -> list[str]:
+    return SOURCE_FLAGS.get(src.name, [])
+
+
 def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *common_flags(), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *common_flags(), *source_flags(src), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     if verbose:
@@ -107,7 +122,8 @@ def build_host_asan(verbose: bool = False, out_dir: Path | None = None) -> Path:
 
     def one(src: Path) -> Path:
         obj = out / (src.stem + ".o")
-        cmd = [hipcc(), *(["-x", "hip"] if src.suffix == ".cpp" else []), *flags, "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc(), *(["-x", "hip"] if src.suffix == ".cpp" else []), *flags, *source_flags(src), "-c", str(src),
+               "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -385,10 +385,12 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
           l_run[qt] *= corr;
 #pragma unroll
           for (int i = 0; i < DT; ++i) {
-            if constexpr (QT == 1)
+            if constexpr (QT == 1) {
               acc_o[qt][i] *= corr;
-            else
+            } else {
+              agpr_settle(acc_o[qt][i]);
               scale_acc(acc_o[qt][i], corr);
+            }
           }
 #pragma unroll
           for (int t = 0; t < 2; ++t)
@@ -434,10 +436,18 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) acc_o[qt][dt] = mfma32<T>(vb[c & 1][dt], pf[qt], acc_o[qt][dt]);
+          for (int qt = 0; qt < QT; ++qt) {
+            // QT = 2: O^T stays in AGPRs (see mfma32_agpr)
+            if constexpr (QT == 1)
+              acc_o[qt][dt] = mfma32<T>(vb[c & 1][dt], pf[qt], acc_o[qt][dt]);
+            else
+              mfma32_agpr<T>(acc_o[qt][dt], vb[c & 1][dt], pf[qt]);
+          }
         if (c + 1 < 4) {
           // packs and row sums of chunk c first, then each MFMA followed by
-          // its share of chunk c+1's exp2 and the next chunk's V reads
+          // its share of chunk c+1's exp2 and the next chunk's V reads (QT =
+          // 2's asm MFMAs are in no group; the compiler places them, which
+          // measured faster than one scheduling region per MFMA)
           __builtin_amdgcn_sched_group_barrier(0x002, 4 * QT, 0);
 #pragma unroll
           for (int m = 0; m < DT * QT; ++m) {
@@ -462,6 +472,12 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
   }
 
   // ---- normalise and store: lane holds query qrow, d = 32dt + 8i + 4g + j ----
+  if constexpr (QT != 1) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) agpr_settle(acc_o[qt][dt]);
+  }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const float l_tot = sum_xor32(l_run[qt]);

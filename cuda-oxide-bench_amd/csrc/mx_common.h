@@ -114,6 +114,34 @@ __device__ __forceinline__ f32x4 mfma16_fp8(const i32x8& a, const i32x8& b, cons
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
+// acc += a·b on a 32x32x16 MFMA whose accumulator stays in AGPRs.  The
+// builtin MFMAs of a kernel all take one register class, chosen by the
+// compiler; issuing this one as inline asm keeps its accumulator in AGPRs
+// while the kernel's other MFMAs write VGPRs.  The compiler does not know
+// the asm is an MFMA, so this code covers the hazards it would otherwise
+// insert wait states for: `s_nop 1` gives a VALU-written A or B operand
+// (and an accumulator written by v_accvgpr_write) its two wait states, and
+// any other reader or writer of the accumulator calls agpr_settle() first.
+// Back-to-back accumulation into the same registers needs no wait states.
+template <typename T>
+__device__ __forceinline__ void mfma32_agpr(f32x16& acc, const u32x4& a, const u32x4& b);
+template <>
+__device__ __forceinline__ void mfma32_agpr<BF16>(f32x16& acc, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+template <>
+__device__ __forceinline__ void mfma32_agpr<F16>(f32x16& acc, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// 21 wait states after the last mfma32_agpr into acc, before any other
+// instruction reads or writes those AGPRs (a 32x32 MFMA's result needs up
+// to 19 before a VALU or v_accvgpr_* access).  acc is an operand, so the
+// accesses that follow cannot be scheduled above it.
+__device__ __forceinline__ void agpr_settle(f32x16& acc) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4" : "+a"(acc));
+}
+
 // acc *= c for an accumulator held in AGPRs: read, multiply, write back one
 // register at a time (VALU cannot read AGPRs), without ever materialising
 // the whole tile in VGPRs.

@@ -17,102 +17,43 @@ issued after the load on that path, so that the wait lands it.
 from __future__ import annotations
 
 import re
-import subprocess
 
 import pytest
 
+import asm_walk
 from conftest import REPO_ROOT, import_submodule
 
 SRC = REPO_ROOT / "cuda-oxide-bench_amd" / "csrc" / "gemm_fp8_bs.hip"
 KERNEL = "_ZN2mx5gemm818gemm_fp8_bs_kernel"
 
-_VREG = re.compile(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b")
 _VMEM = re.compile(r"^\s*(global_|buffer_|flat_|scratch_)")
 
 
-def _kernels(asm: str) -> dict[str, list[str]]:
-    out, cur, name = {}, None, None
-    for line in asm.splitlines():
-        m = re.match(r"^(_Z\w+):", line)
-        if m:
-            name, cur = m.group(1), []
-            continue
-        if cur is not None:
-            cur.append(line)
-            if "s_endpgm" in line:
-                out[name] = cur
-                cur = None
-    return out
-
-
-def _instrs(lines: list[str]):
-    """(kind, text) per line: 'label', 'instr' or None for comments/directives."""
-    res = []
-    for raw in lines:
-        t = raw.split(";")[0].rstrip()
-        s = t.strip()
-        if not s or s.startswith(".") and not re.match(r"^\.LBB\w+:", s) or s.startswith("//"):
-            res.append((None, s))
-        elif re.match(r"^\.LBB\w+:", s):
-            res.append(("label", s[:-1]))
-        else:
-            res.append(("instr", s))
-    return res
-
-
-def _regs(text: str) -> set[int]:
-    regs = set()
-    for a, b, one in _VREG.findall(text):
-        if one:
-            regs.add(int(one))
-        else:
-            regs.update(range(int(a), int(b) + 1))
-    return regs
-
-
 def _check_kernel(lines: list[str]) -> tuple[int, list[str]]:
-    ins = _instrs(lines)
-    labels = {t: i for i, (k, t) in enumerate(ins) if k == "label"}
+    ins = asm_walk.instrs(lines)
     loads = [i for i, (k, t) in enumerate(ins)
              if k == "instr" and re.match(r"^global_load_dword\s+v\d+,\s*v\d+,\s*s\[", t)]
     problems = []
     for li in loads:
-        reg = int(re.match(r"^global_load_dword\s+v(\d+)", ins[li][1]).group(1))
-        seen = set()
-        stack = [(li + 1, 0)]  # (instruction index, vector-memory ops issued since the load)
-        while stack:
-            i, nv = stack.pop()
-            while i < len(ins):
-                if (i, nv) in seen:
-                    break
-                seen.add((i, nv))
-                k, t = ins[i]
-                if k != "instr":
-                    i += 1
-                    continue
-                m = re.match(r"^s_waitcnt\b.*vmcnt\((\d+)\)", t)
-                if m:
-                    if int(m.group(1)) > nv:
-                        problems.append(f"{ins[li][1]!r}: {t!r} does not land it ({nv} loads after it on this path)")
-                    break
-                if reg in _regs(t):
-                    problems.append(f"{ins[li][1]!r}: {t!r} names v{reg} before the load is waited for")
-                    break
-                if t.startswith("s_endpgm"):
-                    problems.append(f"{ins[li][1]!r}: kernel ends before a vmcnt wait")
-                    break
-                if _VMEM.match(t):
-                    nv += 1
-                bm = re.match(r"^s_(c)?branch\w*\s+(\.LBB\w+)", t)
-                if bm:
-                    target = labels[bm.group(2)]
-                    if bm.group(1):  # conditional: both ways
-                        stack.append((target, nv))
-                        i += 1
-                        continue
-                    i = target
-                    continue
-                i += 1
+        load = ins[li][1]
+        reg = int(re.match(r"^global_load_dword\s+v(\d+)", load).group(1))
+
+        # state: vector-memory instructions issued since the load on this path
+        def step(i, t, nv, load=load, reg=reg):
+            m = re.match(r"^s_waitcnt\b.*vmcnt\((\d+)\)", t)
+            if m:
+                if int(m.group(1)) > nv:
+                    problems.append(f"{load!r}: {t!r} does not land it ({nv} loads after it on this path)")
+                return True, nv
+            if reg in asm_walk.vregs(t):
+                problems.append(f"{load!r}: {t!r} names v{reg} before the load is waited for")
+                return True, nv
+            if t.startswith("s_endpgm"):
+                problems.append(f"{load!r}: kernel ends before a vmcnt wait")
+                return True, nv
+            return False, nv + (1 if _VMEM.match(t) else 0)
+
+        asm_walk.walk(ins, li + 1, step)
     return len(loads), problems
 
 
@@ -120,19 +61,14 @@ def _check_kernel(lines: list[str]) -> tuple[int, list[str]]:
 def fp8_asm(tmp_path_factory):
     build = import_submodule("build")
     try:
-        hipcc = build.hipcc()
+        build.hipcc()
     except RuntimeError:
         pytest.skip("hipcc not available")
-    out = tmp_path_factory.mktemp("fp8asm") / "gemm_fp8_bs.s"
-    flags = [f for f in build.common_flags() if f != "-fPIC"]
-    proc = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", str(SRC), "-o", str(out)],
-                          capture_output=True, text=True, timeout=600)
-    assert proc.returncode == 0, proc.stderr[-2000:]
-    return out.read_text()
+    return asm_walk.compile_asm(build, SRC, tmp_path_factory.mktemp("fp8asm") / "gemm_fp8_bs.s")
 
 
 def test_scale_registers_untouched_until_their_wait(fp8_asm):
-    kernels = {n: body for n, body in _kernels(fp8_asm).items() if n.startswith(KERNEL)}
+    kernels = {n: body for n, body in asm_walk.kernels(fp8_asm).items() if n.startswith(KERNEL)}
     assert len(kernels) >= 2, "both tile shapes of gemm_fp8_bs_kernel are in the code object"
     for name, body in kernels.items():
         nloads, problems = _check_kernel(body)
