@@ -390,6 +390,7 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
             } else {
               agpr_settle(acc_o[qt][i]);
               scale_acc(acc_o[qt][i], corr);
+              agpr_settle(acc_o[qt][i]);  // before the next asm MFMA reads it
             }
           }
 #pragma unroll
@@ -423,6 +424,7 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
           // the row sum uses the rounded P the MFMA consumes
 #pragma unroll
           for (int w = 0; w < 4; ++w) lsum[qt] = dot2_ones<T>(pf[qt][w], lsum[qt]);
+          if constexpr (QT != 1) operand_settle(pf[qt]);  // read by asm MFMAs
         }
         if (c + 1 < 4) {
 #pragma unroll
@@ -444,10 +446,10 @@ __global__ __launch_bounds__(64 * NWAVES, QT == 1 ? 2 : 1) void gqa_fwd_kernel(c
               mfma32_agpr<T>(acc_o[qt][dt], vb[c & 1][dt], pf[qt]);
           }
         if (c + 1 < 4) {
-          // packs and row sums of chunk c first, then each MFMA followed by
-          // its share of chunk c+1's exp2 and the next chunk's V reads (QT =
-          // 2's asm MFMAs are in no group; the compiler places them, which
-          // measured faster than one scheduling region per MFMA)
+          // packs of chunk c first, then each MFMA followed by its share of
+          // chunk c+1's exp2, the next chunk's V reads and the row sums
+          // (QT = 2's asm MFMAs are in no group; the compiler places them,
+          // which measured faster than one scheduling region per MFMA)
           __builtin_amdgcn_sched_group_barrier(0x002, 4 * QT, 0);
 #pragma unroll
           for (int m = 0; m < DT * QT; ++m) {

@@ -118,21 +118,29 @@ __device__ __forceinline__ f32x4 mfma16_fp8(const i32x8& a, const i32x8& b, cons
 // builtin MFMAs of a kernel all take one register class, chosen by the
 // compiler; issuing this one as inline asm keeps its accumulator in AGPRs
 // while the kernel's other MFMAs write VGPRs.  The compiler does not know
-// the asm is an MFMA, so this code covers the hazards it would otherwise
-// insert wait states for: `s_nop 1` gives a VALU-written A or B operand
-// (and an accumulator written by v_accvgpr_write) its two wait states, and
-// any other reader or writer of the accumulator calls agpr_settle() first.
-// Back-to-back accumulation into the same registers needs no wait states.
+// the asm is an MFMA and inserts none of the wait states around it: any
+// other reader or writer of the accumulator calls agpr_settle() first, and
+// a VALU-written A or B operand goes through operand_settle() (two wait
+// states) before the MFMA reads it; the build check of the assembly asserts
+// both (an `s_nop` in front of every MFMA would cost ~7 cycles each in a
+// stream of MFMAs).  Back-to-back accumulation into the same registers needs no
+// wait states.
 template <typename T>
 __device__ __forceinline__ void mfma32_agpr(f32x16& acc, const u32x4& a, const u32x4& b);
 template <>
 __device__ __forceinline__ void mfma32_agpr<BF16>(f32x16& acc, const u32x4& a, const u32x4& b) {
-  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 template <>
 __device__ __forceinline__ void mfma32_agpr<F16>(f32x16& acc, const u32x4& a, const u32x4& b) {
-  asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
+
+// Two wait states after the VALU writes that produced x, before an
+// mfma32_agpr reads it as an operand.  x is an operand of the wait, so the
+// MFMAs that read it cannot be scheduled above it, and no VALU write to it
+// can follow it.
+__device__ __forceinline__ void operand_settle(u32x4& x) { asm volatile("s_nop 1" : "+v"(x)); }
 
 // 21 wait states after the last mfma32_agpr into acc, before any other
 // instruction reads or writes those AGPRs (a 32x32 MFMA's result needs up

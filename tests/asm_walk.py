@@ -100,3 +100,66 @@ def walk(ins, start: int, step):
                 i = target
                 continue
             i += 1
+
+
+def _successors(ins) -> dict[int, list[int]]:
+    """Instruction-level control flow: index -> indices of the instructions
+    that can run next."""
+    order = [i for i, (k, _) in enumerate(ins) if k == "instr"]
+    first_after = {}
+    pending = []
+    for i, (k, t) in enumerate(ins):
+        if k == "label":
+            pending.append(t)
+        elif k == "instr":
+            for lab in pending:
+                first_after[lab] = i
+            pending = []
+    nxt = {a: b for a, b in zip(order, order[1:])}
+    succ = {}
+    for i in order:
+        t = ins[i][1]
+        bm = _BRANCH.match(t)
+        if t.startswith("s_endpgm"):
+            succ[i] = []
+        elif bm and not bm.group(1):
+            succ[i] = [first_after[bm.group(2)]]
+        elif bm:
+            succ[i] = [j for j in (nxt.get(i), first_after.get(bm.group(2))) if j is not None]
+        else:
+            succ[i] = [nxt[i]] if i in nxt else []
+    return succ
+
+
+def predecessors(ins) -> dict[int, list[int]]:
+    pred = {}
+    for i, js in _successors(ins).items():
+        pred.setdefault(i, [])
+        for j in js:
+            pred.setdefault(j, []).append(i)
+    return pred
+
+
+def walk_back(ins, pred, start: int, step):
+    """As walk(), backwards along every path that reaches instruction `start`
+    (its predecessors first)."""
+    seen = set()
+    stack = [(p, 0) for p in pred.get(start, [])]
+    while stack:
+        i, st = stack.pop()
+        if (i, st) in seen:
+            continue
+        seen.add((i, st))
+        stop, st = step(i, ins[i][1], st)
+        if not stop:
+            stack.extend((p, st) for p in pred.get(i, []))
+
+
+def valu_dsts(text: str) -> tuple[set[int], set[int]]:
+    """(VGPRs, AGPRs) a VALU instruction writes: its first operand (both
+    operands of a permlane swap).  Empty for anything that is not VALU."""
+    if not text.startswith("v_") or text.startswith("v_mfma"):
+        return set(), set()
+    ops = [o.strip() for o in text.split(None, 1)[1].split(",")] if " " in text else []
+    dst = ops[:2] if "permlane" in text and "swap" in text else ops[:1]
+    return vregs(" ".join(dst)), aregs(" ".join(dst))
