@@ -51,6 +51,22 @@ def instrs(lines: list[str]):
     return res
 
 
+def asm_origin(lines: list[str]) -> set[int]:
+    """Indices (as in instrs(lines)) of instructions written as inline asm
+    in the source, which the compiler brackets with ;;#ASMSTART / ;;#ASMEND:
+    the compiler inserts no wait states for their hazards."""
+    out, inside = set(), False
+    for i, raw in enumerate(lines):
+        s = raw.strip()
+        if s.startswith(";;#ASMSTART"):
+            inside = True
+        elif s.startswith(";;#ASMEND"):
+            inside = False
+        elif inside:
+            out.add(i)
+    return out
+
+
 def _regs(pattern: re.Pattern, text: str) -> set[int]:
     regs = set()
     for a, b, one in pattern.findall(text):

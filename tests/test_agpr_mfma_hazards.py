@@ -18,7 +18,10 @@ accumulator) within the 2 wait states before it, which the hardware needs
 and which the asm does not add (an `s_nop` in front of every MFMA would
 cost ~7 cycles each in a stream of MFMAs).  The second check covers every
 MFMA of the GQA and MLA decode kernels, whose rare rescale writes
-accumulators through asm the compiler cannot see into.  A register copy
+accumulators through asm the compiler cannot see into; a third asserts
+that no inline-asm instruction (such as that rescale's reads) touches an
+MFMA's result within 19 wait states, since the compiler guards only its
+own instructions.  A register copy
 the allocator placed next to one of them, or a settle the scheduler
 moved, fails it.
 """
@@ -59,6 +62,35 @@ def _check_kernel(lines: list[str]) -> tuple[int, list[str]]:
                 return True, ws
             m = re.match(r"^s_nop (\d+)$", t)
             ws = min(NEED, ws + (int(m.group(1)) + 1 if m else 1))
+            return ws >= NEED, ws
+
+        asm_walk.walk(ins, li + 1, step)
+    return len(mfmas), problems
+
+
+def _check_asm_readers(lines: list[str]) -> tuple[int, list[str]]:
+    """Every MFMA: no inline-asm instruction touches its result registers
+    within NEED wait states after it (the compiler guards only its own
+    instructions; an asm reader such as scale_acc after a builtin MFMA is
+    the code's to guard)."""
+    ins = asm_walk.instrs(lines)
+    origin = asm_walk.asm_origin(lines)
+    mfmas = [i for i, (k, t) in enumerate(ins) if k == "instr" and t.startswith("v_mfma")]
+    problems = []
+    for li in mfmas:
+        mf = ins[li][1]
+        dst = mf.split(None, 1)[1].split(",")[0]
+        dv, da = asm_walk.vregs(dst), asm_walk.aregs(dst)
+
+        # the walk goes on past the compiler's own accesses to the registers
+        # (it guards those), so an asm access behind one is still seen
+        def step(i, t, ws, mf=mf, dst=dst, dv=dv, da=da):
+            if i in origin and (dv & asm_walk.vregs(t) or da & asm_walk.aregs(t)):
+                m = _ACCUM.match(t)
+                if not (m and m.group(1) == dst and m.group(2) == dst) and ws < NEED:
+                    problems.append(f"{mf!r}: asm {t!r} touches {dst} {ws} wait states after it")
+                    return True, ws
+            ws = min(NEED, ws + _waits(t))
             return ws >= NEED, ws
 
         asm_walk.walk(ins, li + 1, step)
@@ -138,6 +170,14 @@ def test_mfma_sources_wait_for_valu_writes(which, request):
     assert total > 0
 
 
+@pytest.mark.parametrize("which", ["gqa", "mla"])
+def test_asm_readers_wait_for_mfma_results(which, request):
+    asm = request.getfixturevalue(f"{which}_asm")
+    for name, body in asm_walk.kernels(asm).items():
+        _, problems = _check_asm_readers(body)
+        assert not problems, f"{name}:\n" + "\n".join(problems[:10])
+
+
 def test_checker_sees_planted_hazards():
     """The walks flag an accumulator read too soon (also across a branch) and
     a source written too soon (also along a loop's back edge), and accept a
@@ -157,6 +197,13 @@ def test_checker_sees_planted_hazards():
     assert "v_accvgpr_write_b32 a3, v9" in _check_sources(acc)[1][0]
     other = ["v_mov_b32_e32 v20, 0", mf, "s_endpgm"]
     assert _check_sources(other) == (1, [])
+    # an asm reader right after a builtin MFMA; the compiler's own reader is not the check's concern
+    vmf = "v_mfma_f32_32x32x16_bf16 a[0:15], v[0:3], v[4:7], a[0:15]"
+    asm_read = [vmf, ";;#ASMSTART", "v_accvgpr_read_b32 v9, a2", ";;#ASMEND", "s_endpgm"]
+    assert "asm 'v_accvgpr_read_b32 v9, a2' touches a[0:15] 0 wait states" in _check_asm_readers(asm_read)[1][0]
+    assert _check_asm_readers([vmf, "s_nop 7", "v_accvgpr_read_b32 v9, a2", "s_endpgm"]) == (1, [])
+    assert _check_asm_readers([vmf, *settle, ";;#ASMSTART", "v_accvgpr_read_b32 v9, a2", ";;#ASMEND",
+                               "s_endpgm"]) == (1, [])
     # a write on the path that branches back to the MFMA
     loop = [".LBB0_1:", mf, "v_add_u32_e32 v1, 1, v1", "v_mov_b32_e32 v2, 0", "s_cbranch_scc0 .LBB0_1", "s_endpgm"]
     assert "v_mov_b32_e32 v2, 0" in _check_sources(loop)[1][0]
