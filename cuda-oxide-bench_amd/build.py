@@ -94,7 +94,27 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIB_PATH)
+    build_probes(verbose)
     return LIB_PATH
+
+
+PROBES_DIR = PKG_DIR / "microbench"
+PROBES_LIB = PROBES_DIR / "libmxprobes.so"
+
+
+def build_probes(verbose: bool = False) -> Path:
+    """The hardware characterisation probes (microbench/hw_probes.hip) as
+    their own library, libmxprobes.so; the kernel library does not use it."""
+    src = PROBES_DIR / "hw_probes.hip"
+    tmp = PROBES_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *common_flags(), "-shared", str(src), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"probe build failed\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, PROBES_LIB)
+    return PROBES_LIB
 
 
 ASAN_DIR = PKG_DIR / "_build_asan"

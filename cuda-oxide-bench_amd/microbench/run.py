@@ -1,0 +1,176 @@
+"""Run the MI355X characterisation probes (libmxprobes.so, built with the
+kernel library) and print their results as Markdown tables.
+
+    python cuda-oxide-bench_amd/microbench/run.py [--overlap] [--wg-read]
+
+--overlap: how much of a wave's other work runs beside its own MFMAs at one
+wave per SIMD.  For each instruction mix: shader-clock cycles per iteration
+of 8 independent 32x32x16 bf16 MFMAs alone, of the mix alone, and of both
+interleaved (one MFMA, then its share of the mix); "hidden" is the part of
+the mix's own time that the combination does not add.
+
+--wg-read: the read bandwidth of one workgroup (256 threads, 16-byte loads,
+eight in flight per thread) against many, on data just written and on data
+evicted by a 512 MB write: event time per launch, less an empty launch.
+
+Both start after the device settle bench.py uses (300 ms of a device GEMM),
+so the GPU runs at its load clocks.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import statistics
+import sys
+import time
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libmxprobes.so"
+
+OVERLAP_PROBES = [
+    (1, "32 v_exp_f32"),
+    (2, "32 v_cvt_pk_bf16_f32"),
+    (3, "32 v_dot2_f32_bf16"),
+    (4, "32 v_add_f32"),
+    (5, "32 v_mul_f32"),
+    (6, "32 v_fma_f32"),
+    (7, "8 s_nop 0 (one per MFMA)"),
+    (8, "8 s_nop 1 (one per MFMA)"),
+    (9, "32 v_exp_f32 + 8 s_nop 1 (one per MFMA)"),
+]
+
+
+def load() -> ctypes.CDLL:
+    # torch first: the library binds to whichever libamdhip64.so.7 the process
+    # loaded first, and it must be torch's, which owns the device here.
+    import torch  # noqa: F401
+
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build the package first (python cuda-oxide-bench_amd/build.py)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    i, vp, ll = ctypes.c_int, ctypes.c_void_p, ctypes.c_longlong
+    lib.mxp_overlap_launch.argtypes = [i, i, i, i, vp, vp, vp]
+    lib.mxp_overlap_launch.restype = i
+    lib.mxp_wg_read_launch.argtypes = [vp, ll, ll, i, vp, vp]
+    lib.mxp_wg_read_launch.restype = i
+    lib.mxp_error_string.argtypes = [i]
+    lib.mxp_error_string.restype = ctypes.c_char_p
+    return lib
+
+
+def settle(ms: float = 300.0) -> None:
+    import torch
+
+    a = torch.randn(8192, 8192, device="cuda").to(torch.bfloat16)
+    c = torch.empty_like(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            torch.matmul(a, a, out=c)
+        torch.cuda.synchronize()
+
+
+def overlap_cycles(lib, probe: int, with_mfma: int, iters: int, reps: int) -> float:
+    """Median over reps of the workgroups' mean cycles per iteration."""
+    import torch
+
+    nwg = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(nwg * 256, dtype=torch.float32, device="cuda")
+    cyc = torch.zeros(nwg, dtype=torch.int64, device="cuda")
+    vals = []
+    for _ in range(reps):
+        rc = lib.mxp_overlap_launch(probe, with_mfma, nwg, iters, out.data_ptr(), cyc.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"mxp_overlap_launch({probe}, {with_mfma}): {lib.mxp_error_string(rc).decode()} ({rc})")
+        torch.cuda.synchronize()
+        vals.append(cyc.double().mean().item() / iters)
+    return statistics.median(vals)
+
+
+def overlap(lib, iters: int = 2000, reps: int = 3) -> list[str]:
+    mfma = overlap_cycles(lib, 0, 1, iters, reps)
+    lines = ["| mix per iteration | mix alone | beside 8 MFMAs | 8 MFMAs alone | hidden |", "|---|---:|---:|---:|---:|"]
+    for probe, name in OVERLAP_PROBES:
+        alone = overlap_cycles(lib, probe, 0, iters, reps)
+        both = overlap_cycles(lib, probe, 1, iters, reps)
+        hidden = max(0.0, min(1.0, (alone + mfma - both) / alone)) if alone > 0 else 0.0
+        lines.append(f"| {name} | {alone:.1f} | {both:.1f} | {mfma:.1f} | {100 * hidden:.0f}% |")
+    return lines
+
+
+WG_READ_CASES = [  # (name, workgroups, element stride between workgroups, elements per workgroup)
+    ("1 workgroup x 896 KB", 1, 0, 896 * 1024 // 16),
+    ("32 workgroups x 896 KB", 32, (1 << 20) // 16, 896 * 1024 // 16),
+    ("256 workgroups x 112 KB", 256, 7168, 7168),
+]
+
+
+def wg_read(lib, reps: int = 20) -> list[str]:
+    import torch
+
+    total = (32 << 20) // 16
+    src = torch.empty(total * 16, dtype=torch.uint8, device="cuda")
+    evict = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    out = torch.empty(256 * 256, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for _, nwg, stride, n in WG_READ_CASES:
+        assert (nwg - 1) * stride + n <= total
+
+    def timed(nwg, stride, n, cold):
+        ts = []
+        for r in range(reps):
+            src.fill_(r & 0xff)  # freshly written
+            if cold:
+                evict.fill_(r & 0xff)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            rc = lib.mxp_wg_read_launch(src.data_ptr(), stride, n, nwg, out.data_ptr(), stream)
+            if rc != 0:
+                raise RuntimeError(f"mxp_wg_read_launch: {lib.mxp_error_string(rc).decode()} ({rc})")
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        return statistics.mean(ts)
+
+    lines = ["| case | data | µs per launch | less an empty launch | GB/s per workgroup |", "|---|---|---:|---:|---:|"]
+    for cold in (False, True):
+        empty = timed(1, 0, 0, cold)
+        for name, nwg, stride, n in WG_READ_CASES:
+            us = timed(nwg, stride, n, cold)
+            net = us - empty
+            rate = f"{n * 16 / net / 1e3:.1f}" if net >= 0.5 else "below the timing resolution"
+            lines.append(f"| {name} | {'evicted' if cold else 'just written'} | {us:.2f} | {net:.2f} | {rate} |")
+        lines.append(f"| empty launch | {'evicted' if cold else 'just written'} | {empty:.2f} | | |")
+    return lines
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--overlap", action="store_true")
+    ap.add_argument("--wg-read", action="store_true")
+    ap.add_argument("--iters", type=int, default=2000, help="overlap-probe iterations per launch")
+    args = ap.parse_args()
+    both = not (args.overlap or args.wg_read)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("no GPU", file=sys.stderr)
+        return 2
+    lib = load()
+    print(f"device: {torch.cuda.get_device_name(0)}, "
+          f"{torch.cuda.get_device_properties(0).multi_processor_count} CUs", flush=True)
+    settle()
+    if both or args.overlap:
+        print("\n## Overlap with a wave's own MFMAs (cycles per iteration, one wave per SIMD)\n")
+        print("\n".join(overlap(lib, args.iters)), flush=True)
+    if both or args.wg_read:
+        print("\n## Read bandwidth of one workgroup against many\n")
+        print("\n".join(wg_read(lib)), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
