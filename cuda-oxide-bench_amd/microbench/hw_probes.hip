@@ -11,14 +11,30 @@
 //    workgroup writes the shader-clock cycles its loop took.  Comparing the
 //    three timings (MFMAs alone, mix alone, both) shows how much of the mix
 //    runs beside the wave's own MFMAs.
+//  * mxp_mfma_rate_launch: the MFMA throughput of the whole chip, two waves
+//    per SIMD (8-wave workgroups, one per CU), as 32x32x16 or 16x16x32 bf16
+//    or 32x32x64 or 16x16x128 fp8 MFMAs on operands read from a caller
+//    buffer: each wave rotates through
+//    four A and four B fragments, so with random data the operands change
+//    from one MFMA to the next, and with constant data they never do.  The
+//    MFMA datapath's power, and with it the clock the chip holds, depends
+//    on that.
 //  * mxp_wg_read_launch: nwg workgroups of 256 threads; workgroup w reads n16
 //    16-byte elements starting at element w * stride16 (eight loads in
 //    flight per thread) and writes one XOR per thread, so the time of a
 //    launch against an empty one gives the read bandwidth of that many
 //    workgroups.
+//  * mxp_stream_launch: the same reads with a chosen number in flight, as
+//    loads into registers (DEPTH per thread, consumed as a batch) or as
+//    direct global -> LDS loads (global_load_lds_dwordx4, the kernels' tile
+//    copies: 1 KB per wave instruction, DEPTH of them in flight per wave
+//    through a ring of DEPTH KB), so the time of a launch gives a
+//    workgroup's read rate against the bytes it keeps in flight.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+
+#include "mx_common.h"
 
 namespace {
 
@@ -114,6 +130,103 @@ int launch_op(int with_mfma, int nwg, int iters, float* out, long long* cycles, 
                    : launch_overlap<OP, false>(nwg, iters, out, cycles, s);
 }
 
+constexpr int kRateWaves = 8;
+
+// 8 accumulators per wave; MFMA j of an iteration takes A fragment j % 4 and
+// B fragment (j / 2) % 4, so consecutive MFMAs differ in an operand.
+// SHAPE 0: 32x32x16 bf16 (VGPR accumulators), 1: 16x16x32 bf16, 2: 32x32x16
+// bf16 with AGPR accumulators, 3: 32x32x64 fp8 e4m3, 4: 16x16x128 fp8 e4m3
+// (the fp8 ones in the scaled form with unit scales, as the kernels issue
+// them; a 32-byte operand is two of the 16-byte fragments).
+template <int SHAPE>
+__global__ __launch_bounds__(64 * kRateWaves, 1) void mfma_rate_kernel(const u32x4* __restrict__ ops, float* out,
+                                                                      int iters) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  u32x4 a[4], b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a[j] = ops[t * 8 + j];
+    b[j] = ops[t * 8 + 4 + j];
+  }
+  float r = 0.f;
+  if constexpr (SHAPE == 2) {
+    // inline asm keeps the accumulators in AGPRs; 21 wait states before they
+    // are read back (the compiler does not guard asm MFMAs)
+    f32x16 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc[j]) : "v"(a[j & 3]), "v"(b[(j >> 1) & 3]));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4" : "+a"(acc[j]));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 15];
+  } else if constexpr (SHAPE == 3 || SHAPE == 4) {
+    typedef int i32x8 __attribute__((ext_vector_type(8)));
+    i32x8 a8[4], b8[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 a0 = a[j], a1 = a[(j + 1) & 3], b0 = b[j], b1 = b[(j + 1) & 3];
+      a8[j] = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+      b8[j] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+    }
+    if constexpr (SHAPE == 3) {
+      f32x16 acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
+      for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8[j & 3], b8[(j >> 1) & 3], acc[j], 0, 0, 0, 127,
+                                                                   0, 127);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 15];
+    } else {
+      f32x4 acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = f32x4{};
+      for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8[j & 3], b8[(j >> 1) & 3], acc[j], 0, 0, 0, 127,
+                                                                    0, 127);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 3];
+    }
+  } else if constexpr (SHAPE == 0) {
+    f32x16 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[j & 3]),
+                                                         __builtin_bit_cast(bf16x8, b[(j >> 1) & 3]), acc[j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 15];
+  } else {
+    f32x4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x4{};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[j & 3]),
+                                                         __builtin_bit_cast(bf16x8, b[(j >> 1) & 3]), acc[j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 3];
+  }
+  out[t] = r;
+}
+
 __global__ __launch_bounds__(256) void wg_read_kernel(const uint4* __restrict__ src, long long stride16, long long n16,
                                                      unsigned* out) {
   const uint4* p = src + blockIdx.x * stride16;
@@ -129,6 +242,62 @@ __global__ __launch_bounds__(256) void wg_read_kernel(const uint4* __restrict__ 
     for (int j = 0; j < 8; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
   }
   out[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+template <int DEPTH>
+__global__ __launch_bounds__(256) void stream_reg_kernel(const uint4* __restrict__ src, long long stride16,
+                                                        long long n16, unsigned* out) {
+  const uint4* p = src + blockIdx.x * stride16;
+  unsigned acc = 0;
+  for (long long i = threadIdx.x; i < n16; i += 256 * DEPTH) {
+    uint4 v[DEPTH];
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) {
+      const long long k = i + (long long)j * 256;
+      v[j] = k < n16 ? p[k] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  out[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+// Wave w copies the 1 KB chunks w, w + 4, ... of its workgroup's n16
+// elements (n16 % 64 == 0) into ring slot c % DEPTH of its own DEPTH KB,
+// where c counts its chunks; before reusing a slot it waits until at most
+// DEPTH - 1 of its loads are outstanding, i.e. the slot's previous load has
+// landed.
+template <int DEPTH>
+__global__ __launch_bounds__(256) void stream_lds_kernel(const uint4* __restrict__ src, long long stride16,
+                                                        long long n16, unsigned* out) {
+  extern __shared__ __align__(1024) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint4* p = src + blockIdx.x * stride16;
+  const uint32_t ring = mx::lds_addr(smem) + wave * DEPTH * 1024;
+  const long long chunks = n16 / 64;
+  int c = 0;
+  for (long long k = wave; k < chunks; k += 4, ++c) {
+    if (c >= DEPTH) mx::wait_vmcnt<DEPTH - 1>();
+    mx::dma16(p + k * 64, 16u * lane, ring + (c % DEPTH) * 1024);
+  }
+  mx::wait_vmcnt<0>();
+  __syncthreads();
+  out[blockIdx.x * 256 + threadIdx.x] = reinterpret_cast<const unsigned*>(smem)[threadIdx.x];
+}
+
+template <int MODE, int DEPTH>
+int launch_stream(const uint4* src, long long stride16, long long n16, int nwg, unsigned* out, hipStream_t s) {
+  if constexpr (MODE == 0) {
+    hipLaunchKernelGGL(stream_reg_kernel<DEPTH>, dim3(nwg), dim3(256), 0, s, src, stride16, n16, out);
+  } else {
+    constexpr int lds = 4 * DEPTH * 1024;
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(stream_lds_kernel<DEPTH>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return hip_status(e);
+    hipLaunchKernelGGL(stream_lds_kernel<DEPTH>, dim3(nwg), dim3(256), lds, s, src, stride16, n16, out);
+  }
+  return hip_status(hipGetLastError());
 }
 
 }  // namespace
@@ -157,6 +326,27 @@ extern "C" int mxp_overlap_launch(int probe, int with_mfma, int nwg, int iters, 
   }
 }
 
+// shape 0: 32x32x16, 1: 16x16x32, 2: 32x32x16 with AGPR accumulators (bf16);
+// 3: 32x32x64, 4: 16x16x128 (fp8 e4m3).  ops: nwg * 512 * 8 16-byte
+// fragments (lane t of the grid reads its 8 at 8 t); out: nwg * 512 floats.
+// FLOPs of a launch: nwg * 8 waves * iters * 8 MFMAs * 32768 (shapes 0, 2),
+// 16384 (1), 131072 (3) or 65536 (4).  The builtins (all but shape 2) get
+// VGPR accumulators from this compiler at two waves per SIMD.
+extern "C" int mxp_mfma_rate_launch(int shape, int nwg, int iters, const void* ops, float* out, void* stream) {
+  if (nwg <= 0 || iters <= 0 || !ops || !out || shape < 0 || shape > 4) return -1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const u32x4* o = static_cast<const u32x4*>(ops);
+  const dim3 grid(nwg), block(64 * kRateWaves);
+  switch (shape) {
+    case 0: hipLaunchKernelGGL(mfma_rate_kernel<0>, grid, block, 0, s, o, out, iters); break;
+    case 1: hipLaunchKernelGGL(mfma_rate_kernel<1>, grid, block, 0, s, o, out, iters); break;
+    case 2: hipLaunchKernelGGL(mfma_rate_kernel<2>, grid, block, 0, s, o, out, iters); break;
+    case 3: hipLaunchKernelGGL(mfma_rate_kernel<3>, grid, block, 0, s, o, out, iters); break;
+    default: hipLaunchKernelGGL(mfma_rate_kernel<4>, grid, block, 0, s, o, out, iters); break;
+  }
+  return hip_status(hipGetLastError());
+}
+
 // src must hold (nwg - 1) * stride16 + n16 16-byte elements; out nwg * 256.
 extern "C" int mxp_wg_read_launch(const void* src, long long stride16, long long n16, int nwg, unsigned* out,
                                   void* stream) {
@@ -164,6 +354,29 @@ extern "C" int mxp_wg_read_launch(const void* src, long long stride16, long long
   hipLaunchKernelGGL(wg_read_kernel, dim3(nwg), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint4*>(src), stride16, n16, out);
   return hip_status(hipGetLastError());
+}
+
+// mode 0: loads into registers, depth 4, 8, 16 or 32 per thread; mode 1:
+// direct LDS loads, depth 4, 8, 16 or 32 KB in flight per wave (n16 a
+// multiple of 64).  src must hold (nwg - 1) * stride16 + n16 16-byte
+// elements; out nwg * 256.
+extern "C" int mxp_stream_launch(int mode, int depth, const void* src, long long stride16, long long n16, int nwg,
+                                 unsigned* out, void* stream) {
+  if (nwg <= 0 || n16 < 0 || stride16 < 0 || !src || !out || mode < 0 || mode > 1) return -1;
+  if (mode == 1 && n16 % 64 != 0) return -1;
+  const uint4* p = static_cast<const uint4*>(src);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (mode * 100 + depth) {
+    case 4: return launch_stream<0, 4>(p, stride16, n16, nwg, out, s);
+    case 8: return launch_stream<0, 8>(p, stride16, n16, nwg, out, s);
+    case 16: return launch_stream<0, 16>(p, stride16, n16, nwg, out, s);
+    case 32: return launch_stream<0, 32>(p, stride16, n16, nwg, out, s);
+    case 104: return launch_stream<1, 4>(p, stride16, n16, nwg, out, s);
+    case 108: return launch_stream<1, 8>(p, stride16, n16, nwg, out, s);
+    case 116: return launch_stream<1, 16>(p, stride16, n16, nwg, out, s);
+    case 132: return launch_stream<1, 32>(p, stride16, n16, nwg, out, s);
+    default: return -1;
+  }
 }
 
 // The HIP error behind a status below -1000.

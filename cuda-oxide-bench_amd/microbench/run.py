@@ -1,7 +1,7 @@
 """Run the MI355X characterisation probes (libmxprobes.so, built with the
 kernel library) and print their results as Markdown tables.
 
-    python cuda-oxide-bench_amd/microbench/run.py [--overlap] [--wg-read]
+    python cuda-oxide-bench_amd/microbench/run.py [--overlap] [--mfma-rate] [--wg-read] [--stream]
 
 --overlap: how much of a wave's other work runs beside its own MFMAs at one
 wave per SIMD.  For each instruction mix: shader-clock cycles per iteration
@@ -9,11 +9,22 @@ of 8 independent 32x32x16 bf16 MFMAs alone, of the mix alone, and of both
 interleaved (one MFMA, then its share of the mix); "hidden" is the part of
 the mix's own time that the combination does not add.
 
+--mfma-rate: chip-wide MFMA throughput (two waves per SIMD, ~70 ms
+launches) for bf16 32x32x16 and 16x16x32 and fp8 32x32x64 and 16x16x128
+MFMAs, on random operands that change from one MFMA to the next and on
+constant ones: at the power cap the first run at a lower clock than the
+second.
+
 --wg-read: the read bandwidth of one workgroup (256 threads, 16-byte loads,
 eight in flight per thread) against many, on data just written and on data
 evicted by a 512 MB write: event time per launch, less an empty launch.
 
-Both start after the device settle bench.py uses (300 ms of a device GEMM),
+--stream: the same reads with 4 to 32 loads in flight, into registers
+(per thread) or by direct global -> LDS loads (per wave, the kernels' tile
+copies), by one workgroup and by 256 workgroups (one per CU) that read
+either distinct data or all the same 256 KB.
+
+All start after the device settle bench.py uses (300 ms of a device GEMM),
 so the GPU runs at its load clocks.
 """
 from __future__ import annotations
@@ -54,6 +65,10 @@ def load() -> ctypes.CDLL:
     lib.mxp_overlap_launch.restype = i
     lib.mxp_wg_read_launch.argtypes = [vp, ll, ll, i, vp, vp]
     lib.mxp_wg_read_launch.restype = i
+    lib.mxp_mfma_rate_launch.argtypes = [i, i, i, vp, vp, vp]
+    lib.mxp_mfma_rate_launch.restype = i
+    lib.mxp_stream_launch.argtypes = [i, i, vp, ll, ll, i, vp, vp]
+    lib.mxp_stream_launch.restype = i
     lib.mxp_error_string.argtypes = [i]
     lib.mxp_error_string.restype = ctypes.c_char_p
     return lib
@@ -98,6 +113,50 @@ def overlap(lib, iters: int = 2000, reps: int = 3) -> list[str]:
         both = overlap_cycles(lib, probe, 1, iters, reps)
         hidden = max(0.0, min(1.0, (alone + mfma - both) / alone)) if alone > 0 else 0.0
         lines.append(f"| {name} | {alone:.1f} | {both:.1f} | {mfma:.1f} | {100 * hidden:.0f}% |")
+    return lines
+
+
+def mfma_rate(lib, target_ms: float = 70.0, reps: int = 3) -> list[str]:
+    import torch
+
+    nwg = torch.cuda.get_device_properties(0).multi_processor_count
+    threads = nwg * 512
+    out = torch.empty(threads, dtype=torch.float32, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    bf16 = {"random": torch.randn(threads * 64, device="cuda", generator=g).to(torch.bfloat16),
+            "constant (all 0.5)": torch.full((threads * 64,), 0.5, device="cuda", dtype=torch.bfloat16)}
+    fp8 = {k: v.float().to(torch.float8_e4m3fn) for k, v in
+           (("random", torch.randn(threads * 128, device="cuda", generator=g)),
+            ("constant (all 0.5)", torch.full((threads * 128,), 0.5, device="cuda")))}
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(shape, ops, iters):
+        rc = lib.mxp_mfma_rate_launch(shape, nwg, iters, ops.data_ptr(), out.data_ptr(), stream)
+        if rc != 0:
+            raise RuntimeError(f"mxp_mfma_rate_launch: {lib.mxp_error_string(rc).decode()} ({rc})")
+
+    def ms_of(shape, ops, iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        launch(shape, ops, iters)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    lines = ["| MFMA | operands | iterations per launch | ms per launch | PFLOP/s |", "|---|---|---:|---:|---:|"]
+    for shape, name, flop, operands in ((0, "32x32x16 bf16, VGPR accumulators", 32768, bf16),
+                                        (2, "32x32x16 bf16, AGPR accumulators", 32768, bf16),
+                                        (1, "16x16x32 bf16, VGPR accumulators", 16384, bf16),
+                                        (3, "32x32x64 fp8, VGPR accumulators", 131072, fp8),
+                                        (4, "16x16x128 fp8, VGPR accumulators", 65536, fp8)):
+        for label, ops in operands.items():
+            iters = 2000
+            t = ms_of(shape, ops, iters)
+            iters = max(1, int(iters * target_ms / max(t, 1e-3)))
+            ms_of(shape, ops, iters)  # at load clocks before the timed launches
+            ms = statistics.median(ms_of(shape, ops, iters) for _ in range(reps))
+            flops = nwg * 8 * iters * 8 * flop
+            lines.append(f"| {name} | {label} | {iters} | {ms:.2f} | {flops / ms / 1e12:.3f} |")
     return lines
 
 
@@ -147,13 +206,63 @@ def wg_read(lib, reps: int = 20) -> list[str]:
     return lines
 
 
+STREAM_CASES = [  # (name, workgroups, element stride between workgroups, elements per workgroup)
+    ("1 workgroup x 1 MB", 1, 0, (1 << 20) // 16),
+    ("256 workgroups x 256 KB, distinct", 256, (256 << 10) // 16, (256 << 10) // 16),
+    ("256 workgroups x 256 KB, all the same", 256, 0, (256 << 10) // 16),
+]
+STREAM_DEPTHS = (4, 8, 16, 32)
+
+
+def stream(lib, reps: int = 20) -> list[str]:
+    import torch
+
+    total = (64 << 20) // 16
+    src = torch.empty(total * 16, dtype=torch.uint8, device="cuda")
+    out = torch.empty(256 * 256, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    for _, nwg, stride, n in STREAM_CASES:
+        assert (nwg - 1) * stride + n <= total and n % 64 == 0
+
+    def timed(mode, depth, nwg, stride, n):
+        ts = []
+        for r in range(reps):
+            src.fill_(r & 0xff)  # freshly written
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            rc = lib.mxp_stream_launch(mode, depth, src.data_ptr(), stride, n, nwg, out.data_ptr(), st)
+            if rc != 0:
+                raise RuntimeError(f"mxp_stream_launch: {lib.mxp_error_string(rc).decode()} ({rc})")
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        return statistics.mean(ts)
+
+    lines = ["| case | loads | in flight per workgroup | µs less an empty launch | GB/s per workgroup | GB/s in all |",
+             "|---|---|---:|---:|---:|---:|"]
+    for name, nwg, stride, n in STREAM_CASES:
+        for mode, kind in ((0, "registers"), (1, "direct to LDS")):
+            for depth in STREAM_DEPTHS:
+                empty = timed(mode, depth, 1, 0, 0)
+                net = timed(mode, depth, nwg, stride, n) - empty
+                kb = 256 * depth * 16 // 1024 if mode == 0 else 4 * depth
+                if net >= 0.5:
+                    per, total_rate = f"{n * 16 / net / 1e3:.1f}", f"{nwg * n * 16 / net / 1e3:.0f}"
+                else:
+                    per = total_rate = "below the timing resolution"
+                lines.append(f"| {name} | {kind} | {kb} KB | {net:.2f} | {per} | {total_rate} |")
+    return lines
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--overlap", action="store_true")
+    ap.add_argument("--mfma-rate", action="store_true")
     ap.add_argument("--wg-read", action="store_true")
+    ap.add_argument("--stream", action="store_true")
     ap.add_argument("--iters", type=int, default=2000, help="overlap-probe iterations per launch")
     args = ap.parse_args()
-    both = not (args.overlap or args.wg_read)
+    every = not (args.overlap or args.mfma_rate or args.wg_read or args.stream)
     import torch
 
     if not torch.cuda.is_available():
@@ -163,12 +272,18 @@ def main() -> int:
     print(f"device: {torch.cuda.get_device_name(0)}, "
           f"{torch.cuda.get_device_properties(0).multi_processor_count} CUs", flush=True)
     settle()
-    if both or args.overlap:
+    if every or args.overlap:
         print("\n## Overlap with a wave's own MFMAs (cycles per iteration, one wave per SIMD)\n")
         print("\n".join(overlap(lib, args.iters)), flush=True)
-    if both or args.wg_read:
+    if every or args.mfma_rate:
+        print("\n## Chip-wide MFMA throughput, two waves per SIMD\n")
+        print("\n".join(mfma_rate(lib)), flush=True)
+    if every or args.wg_read:
         print("\n## Read bandwidth of one workgroup against many\n")
         print("\n".join(wg_read(lib)), flush=True)
+    if every or args.stream:
+        print("\n## Read rate against the loads in flight\n")
+        print("\n".join(stream(lib)), flush=True)
     return 0
 
 

@@ -1,5 +1,5 @@
 """The hardware characterisation probes (cuda-oxide-bench_amd/microbench):
-the library builds with the package and exports its two launchers, which
+the library builds with the package and exports its launchers, which
 reject invalid arguments before launching (CPU); one short run of each
 probe on the GPU returns finite, positive figures (gpu)."""
 from __future__ import annotations
@@ -25,7 +25,8 @@ def runner():
 
 def test_probe_library_exports_its_launchers(runner):
     lib = runner.load()
-    for name in ("mxp_overlap_launch", "mxp_wg_read_launch"):
+    for name in ("mxp_overlap_launch", "mxp_mfma_rate_launch", "mxp_wg_read_launch", "mxp_stream_launch",
+                 "mxp_error_string"):
         assert hasattr(lib, name), name
     # invalid arguments are rejected before any HIP call
     assert lib.mxp_overlap_launch(0, 1, 0, 10, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == -1
@@ -33,6 +34,13 @@ def test_probe_library_exports_its_launchers(runner):
     assert lib.mxp_overlap_launch(0, 1, 4, 10, None, ctypes.c_void_p(16), None) == -1
     assert lib.mxp_wg_read_launch(ctypes.c_void_p(16), 0, -1, 1, ctypes.c_void_p(16), None) == -1
     assert lib.mxp_wg_read_launch(None, 0, 8, 1, ctypes.c_void_p(16), None) == -1
+    assert lib.mxp_mfma_rate_launch(5, 4, 10, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == -1
+    assert lib.mxp_mfma_rate_launch(0, 4, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == -1
+    p = ctypes.c_void_p(16)
+    assert lib.mxp_stream_launch(0, 12, p, 0, 64, 1, p, None) == -1   # no such depth
+    assert lib.mxp_stream_launch(2, 8, p, 0, 64, 1, p, None) == -1    # no such mode
+    assert lib.mxp_stream_launch(1, 8, p, 0, 100, 1, p, None) == -1   # LDS copies take whole 1 KB chunks
+    assert lib.mxp_stream_launch(1, 8, p, 0, 64, 0, p, None) == -1
 
 
 @pytest.mark.gpu
@@ -44,6 +52,12 @@ def test_probes_run(runner):
     both = runner.overlap_cycles(lib, 3, 1, 200, 1)
     for v in (mfma, dot2, both):
         assert math.isfinite(v) and v > 0
+    announce("microbench MFMA rate")
+    lines = runner.mfma_rate(lib, target_ms=2.0, reps=1)
+    assert len(lines) == 2 + 10
     announce("microbench workgroup read")
     lines = runner.wg_read(lib, reps=2)
     assert len(lines) == 2 + 2 * (len(runner.WG_READ_CASES) + 1)
+    announce("microbench read streams")
+    lines = runner.stream(lib, reps=1)
+    assert len(lines) == 2 + 2 * len(runner.STREAM_CASES) * len(runner.STREAM_DEPTHS)
