@@ -51,12 +51,19 @@ def test_parity_vs_oracle(ops, mnk):
                                       ((256, 1024, 2048), "64 tiles: weight streaming"),
                                       ((1024, 1024, 1024), "direct-load ring, 256 tiles (BASELINE configs[0])"),
                                       ((1024, 1024, 576), "K % 128 != 0: register-staged split-K path"),
-                                      ((960, 1024, 512), "M % 64 == 0, 240 tiles: direct-load ring")])
+                                      ((960, 1024, 512), "M % 64 == 0, 240 tiles: direct-load ring"),
+                                      ((1024, 1024, 512), "direct-load ring, 4 K tiles per group"),
+                                      ((768, 1024, 640), "direct-load ring, 5 K tiles per group, 192 tiles"),
+                                      ((1024, 960, 768), "direct-load ring, 6 K tiles per group, 240 tiles"),
+                                      ((512, 2048, 896), "direct-load ring, 7 K tiles per group"),
+                                      ((1024, 1024, 1536), "direct-load ring, 12 K tiles per group"),
+                                      ((512, 1024, 4096), "128 tiles, long K: direct-load ring")])
 def test_small_grid_paths(ops, mnk, path):
     """Grids of at most one 64x64 tile per CU with K >= 512: at most 64
     tiles stream the weights; more, with whole tiles and 128-deep K chunks,
     run the direct-load ring (two K groups per workgroup summed through
-    LDS), other shapes the register-staged split-K kernel."""
+    LDS; K tiles per group from fewer than the ring's 4 slots in flight to
+    many more), other shapes the register-staged split-K kernel."""
     m, n, k = mnk
     announce(f"gemm_bf16 {m}x{n}x{k} ({path})")
     a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
@@ -65,6 +72,32 @@ def test_small_grid_paths(ops, mnk, path):
     err = normwise_rel_err(c, ref)
     assert err <= TOL, f"normwise rel err {err:.3e}"
     assert torch.all((c.float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+
+
+@pytest.mark.parametrize("mnk", [(1024, 1024, 1024), (768, 1024, 640), (1024, 1024, 1536)])
+def test_small_grid_strided(ops, mnk):
+    """Leading dimensions beyond the row lengths (lda > K, ldb > N,
+    ldc > N) on the direct-load ring; C's padding columns are left
+    untouched."""
+    m, n, k = mnk
+    announce(f"gemm_bf16 {m}x{n}x{k} strided")
+    lib = import_submodule("_lib")
+    a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
+    pad = 72
+    a_full = torch.zeros((m, k + pad), dtype=torch.bfloat16, device="cuda")
+    b_full = torch.zeros((k, n + pad), dtype=torch.bfloat16, device="cuda")
+    c_full = torch.full((m, n + pad), 7.0, dtype=torch.bfloat16, device="cuda")
+    a_full[:, :k] = a.cuda()
+    b_full[:, :n] = b.cuda()
+    lib.call("mx_gemm_bf16", a_full.data_ptr(), b_full.data_ptr(), c_full.data_ptr(), m, n, k, k + pad, n + pad,
+             n + pad, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    c = c_full.cpu()
+    ref = ogemm.gemm_ref(a, b)
+    err = normwise_rel_err(c[:, :n], ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+    assert torch.all((c[:, :n].float() - ref).abs() <= 0.2 + 0.05 * ref.abs())
+    assert torch.all(c[:, n:] == 7.0)
 
 
 def test_reference_distribution_sampled_gate(ops):
