@@ -19,6 +19,15 @@
 //    from one MFMA to the next, and with constant data they never do.  The
 //    MFMA datapath's power, and with it the clock the chip holds, depends
 //    on that.
+//  * mxp_contend_launch: how a co-resident wave's work slows a wave's
+//    MFMAs.  One 8-wave workgroup per CU: waves 0-3 issue 8 independent
+//    MFMAs per iteration (bf16 32x32x16 or fp8 32x32x64, accumulators in
+//    VGPRs or, as inline asm, in AGPRs) and time themselves in shader-clock
+//    cycles and in the 100 MHz real-time counter; meanwhile waves 4-7 idle
+//    (busy = 0), run independent v_fma_f32 streams long enough to outlast
+//    them (busy = 1), or issue the same MFMA stream (busy = 2).  Each wave
+//    records its hardware id, so the host can check that waves w and w + 4
+//    share a SIMD.
 //  * mxp_wg_read_launch: nwg workgroups of 256 threads; workgroup w reads n16
 //    16-byte elements starting at element w * stride16 (eight loads in
 //    flight per thread) and writes one XOR per thread, so the time of a
@@ -137,7 +146,9 @@ constexpr int kRateWaves = 8;
 // SHAPE 0: 32x32x16 bf16 (VGPR accumulators), 1: 16x16x32 bf16, 2: 32x32x16
 // bf16 with AGPR accumulators, 3: 32x32x64 fp8 e4m3, 4: 16x16x128 fp8 e4m3
 // (the fp8 ones in the scaled form with unit scales, as the kernels issue
-// them; a 32-byte operand is two of the 16-byte fragments).
+// them; a 32-byte operand is two of the 16-byte fragments); with AGPR
+// accumulators (inline asm): 5: 16x16x32 bf16, 6: 32x32x64 fp8, 7:
+// 16x16x128 fp8.
 template <int SHAPE>
 __global__ __launch_bounds__(64 * kRateWaves, 1) void mfma_rate_kernel(const u32x4* __restrict__ ops, float* out,
                                                                       int iters) {
@@ -165,6 +176,55 @@ __global__ __launch_bounds__(64 * kRateWaves, 1) void mfma_rate_kernel(const u32
     for (int j = 0; j < 8; ++j) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4" : "+a"(acc[j]));
 #pragma unroll
     for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 15];
+  } else if constexpr (SHAPE == 5) {
+    f32x4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x4{};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[j]) : "v"(a[j & 3]), "v"(b[(j >> 1) & 3]));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("s_nop 7\n\ts_nop 3" : "+a"(acc[j]));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 3];
+  } else if constexpr (SHAPE == 6 || SHAPE == 7) {
+    typedef int i32x8 __attribute__((ext_vector_type(8)));
+    i32x8 a8[4], b8[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 a0 = a[j], a1 = a[(j + 1) & 3], b0 = b[j], b1 = b[(j + 1) & 3];
+      a8[j] = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+      b8[j] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+    }
+    if constexpr (SHAPE == 6) {
+      f32x16 acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
+      for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+a"(acc[j]) : "v"(a8[j & 3]), "v"(b8[(j >> 1) & 3]));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4" : "+a"(acc[j]));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 15];
+    } else {
+      f32x4 acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = f32x4{};
+      for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          asm("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(acc[j]) : "v"(a8[j & 3]), "v"(b8[(j >> 1) & 3]));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) asm volatile("s_nop 7\n\ts_nop 3" : "+a"(acc[j]));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 3];
+    }
   } else if constexpr (SHAPE == 3 || SHAPE == 4) {
     typedef int i32x8 __attribute__((ext_vector_type(8)));
     i32x8 a8[4], b8[4];
@@ -242,6 +302,97 @@ __global__ __launch_bounds__(256) void wg_read_kernel(const uint4* __restrict__ 
     for (int j = 0; j < 8; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
   }
   out[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+// FORM 0: bf16 32x32x16, VGPR accumulators; 1: the same in AGPRs (asm);
+// 2: fp8 e4m3 32x32x64, VGPR accumulators (the scaled form with unit
+// scales, as the kernels issue it); 3: fp8 32x32x64 in AGPRs (asm).
+// cycles[8 b + w], rtime[8 b + w] (waves 4-7 only with busy > 0) and
+// hwid[8 b + w] per wave w of workgroup b.
+template <int FORM, int BUSY>
+__global__ __launch_bounds__(512, 1) void contend_kernel(const u32x4* __restrict__ ops, float* out, long long* cycles,
+                                                        long long* rtime, unsigned* hwid, int iters,
+                                                        int valu_iters) {
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if ((threadIdx.x & 63) == 0) hwid[blockIdx.x * 8 + wave] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+  float r = 0.f;
+  if (wave < 4 || BUSY == 2) {
+    u32x4 a[2], b[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      a[j] = ops[t * 4 + j];
+      b[j] = ops[t * 4 + 2 + j];
+    }
+    const i32x8 a8 = __builtin_bit_cast(i32x8, (u32x4[2]){a[0], a[1]});
+    const i32x8 b8 = __builtin_bit_cast(i32x8, (u32x4[2]){b[0], b[1]});
+    f32x16 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
+    const long long r0 = __builtin_amdgcn_s_memrealtime();
+    const long long t0 = __builtin_readcyclecounter();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if constexpr (FORM == 0)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[j & 1]),
+                                                           __builtin_bit_cast(bf16x8, b[(j >> 1) & 1]), acc[j], 0, 0, 0);
+        else if constexpr (FORM == 1)
+          asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc[j]) : "v"(a[j & 1]), "v"(b[(j >> 1) & 1]));
+        else if constexpr (FORM == 2)
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[j], 0, 0, 0, 127, 0, 127);
+        else
+          asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+a"(acc[j]) : "v"(a8), "v"(b8));
+      }
+    }
+    const long long t1 = __builtin_readcyclecounter();
+    const long long r1 = __builtin_amdgcn_s_memrealtime();
+    if constexpr (FORM == 1 || FORM == 3) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4" : "+a"(acc[j]));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 15];
+    if ((threadIdx.x & 63) == 0) {
+      cycles[blockIdx.x * 8 + wave] = t1 - t0;
+      rtime[blockIdx.x * 8 + wave] = r1 - r0;
+    }
+  } else if constexpr (BUSY == 1) {
+    float e[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) e[i] = 1e-6f * (threadIdx.x + i);
+    const long long r0 = __builtin_amdgcn_s_memrealtime();
+    const long long t0 = __builtin_readcyclecounter();
+    for (int it = 0; it < valu_iters; ++it) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) e[i] = __builtin_fmaf(e[i], 0.999f, e[i ^ 2]);
+    }
+    const long long t1 = __builtin_readcyclecounter();
+    const long long r1 = __builtin_amdgcn_s_memrealtime();
+#pragma unroll
+    for (int i = 0; i < 32; ++i) r += e[i];
+    if ((threadIdx.x & 63) == 0) {
+      cycles[blockIdx.x * 8 + wave] = t1 - t0;
+      rtime[blockIdx.x * 8 + wave] = r1 - r0;
+    }
+  }
+  out[t] = r;
+}
+
+template <int FORM>
+int launch_contend(int busy, int nwg, int iters, int valu_iters, const u32x4* ops, float* out, long long* cycles,
+                   long long* rtime, unsigned* hwid, hipStream_t s) {
+  if (busy == 0)
+    hipLaunchKernelGGL((contend_kernel<FORM, 0>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
+                       valu_iters);
+  else if (busy == 1)
+    hipLaunchKernelGGL((contend_kernel<FORM, 1>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
+                       valu_iters);
+  else
+    hipLaunchKernelGGL((contend_kernel<FORM, 2>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
+                       valu_iters);
+  return hip_status(hipGetLastError());
 }
 
 template <int DEPTH>
@@ -327,13 +478,14 @@ extern "C" int mxp_overlap_launch(int probe, int with_mfma, int nwg, int iters, 
 }
 
 // shape 0: 32x32x16, 1: 16x16x32, 2: 32x32x16 with AGPR accumulators (bf16);
-// 3: 32x32x64, 4: 16x16x128 (fp8 e4m3).  ops: nwg * 512 * 8 16-byte
+// 3: 32x32x64, 4: 16x16x128 (fp8 e4m3); AGPR accumulators: 5: 16x16x32
+// bf16, 6: 32x32x64 fp8, 7: 16x16x128 fp8.  ops: nwg * 512 * 8 16-byte
 // fragments (lane t of the grid reads its 8 at 8 t); out: nwg * 512 floats.
 // FLOPs of a launch: nwg * 8 waves * iters * 8 MFMAs * 32768 (shapes 0, 2),
-// 16384 (1), 131072 (3) or 65536 (4).  The builtins (all but shape 2) get
-// VGPR accumulators from this compiler at two waves per SIMD.
+// 16384 (1, 5), 131072 (3, 6) or 65536 (4, 7).  The builtins (shapes 0, 1,
+// 3, 4) get VGPR accumulators from this compiler at two waves per SIMD.
 extern "C" int mxp_mfma_rate_launch(int shape, int nwg, int iters, const void* ops, float* out, void* stream) {
-  if (nwg <= 0 || iters <= 0 || !ops || !out || shape < 0 || shape > 4) return -1;
+  if (nwg <= 0 || iters <= 0 || !ops || !out || shape < 0 || shape > 7) return -1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const u32x4* o = static_cast<const u32x4*>(ops);
   const dim3 grid(nwg), block(64 * kRateWaves);
@@ -342,7 +494,10 @@ extern "C" int mxp_mfma_rate_launch(int shape, int nwg, int iters, const void* o
     case 1: hipLaunchKernelGGL(mfma_rate_kernel<1>, grid, block, 0, s, o, out, iters); break;
     case 2: hipLaunchKernelGGL(mfma_rate_kernel<2>, grid, block, 0, s, o, out, iters); break;
     case 3: hipLaunchKernelGGL(mfma_rate_kernel<3>, grid, block, 0, s, o, out, iters); break;
-    default: hipLaunchKernelGGL(mfma_rate_kernel<4>, grid, block, 0, s, o, out, iters); break;
+    case 4: hipLaunchKernelGGL(mfma_rate_kernel<4>, grid, block, 0, s, o, out, iters); break;
+    case 5: hipLaunchKernelGGL(mfma_rate_kernel<5>, grid, block, 0, s, o, out, iters); break;
+    case 6: hipLaunchKernelGGL(mfma_rate_kernel<6>, grid, block, 0, s, o, out, iters); break;
+    default: hipLaunchKernelGGL(mfma_rate_kernel<7>, grid, block, 0, s, o, out, iters); break;
   }
   return hip_status(hipGetLastError());
 }
@@ -376,6 +531,24 @@ extern "C" int mxp_stream_launch(int mode, int depth, const void* src, long long
     case 116: return launch_stream<1, 16>(p, stride16, n16, nwg, out, s);
     case 132: return launch_stream<1, 32>(p, stride16, n16, nwg, out, s);
     default: return -1;
+  }
+}
+
+// form 0..3 as contend_kernel; busy 0 (waves 4-7 idle), 1 (VALU) or 2
+// (the same MFMAs).  ops: nwg * 512 * 4 16-byte fragments (lane t reads its
+// 4 at 4 t); out: nwg * 512 floats; cycles, rtime and hwid: nwg * 8 each.
+extern "C" int mxp_contend_launch(int form, int busy, int nwg, int iters, int valu_iters, const void* ops, float* out,
+                                  long long* cycles, long long* rtime, unsigned* hwid, void* stream) {
+  if (nwg <= 0 || iters <= 0 || valu_iters < 0 || !ops || !out || !cycles || !rtime || !hwid || form < 0 ||
+      form > 3 || busy < 0 || busy > 2)
+    return -1;
+  const u32x4* o = static_cast<const u32x4*>(ops);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (form) {
+    case 0: return launch_contend<0>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
+    case 1: return launch_contend<1>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
+    case 2: return launch_contend<2>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
+    default: return launch_contend<3>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
   }
 }
 

@@ -1,7 +1,7 @@
 """Run the MI355X characterisation probes (libmxprobes.so, built with the
 kernel library) and print their results as Markdown tables.
 
-    python cuda-oxide-bench_amd/microbench/run.py [--overlap] [--mfma-rate] [--wg-read] [--stream]
+    python cuda-oxide-bench_amd/microbench/run.py [--overlap] [--mfma-rate] [--contend] [--wg-read] [--stream]
 
 --overlap: how much of a wave's other work runs beside its own MFMAs at one
 wave per SIMD.  For each instruction mix: shader-clock cycles per iteration
@@ -14,6 +14,11 @@ launches) for bf16 32x32x16 and 16x16x32 and fp8 32x32x64 and 16x16x128
 MFMAs, on random operands that change from one MFMA to the next and on
 constant ones: at the power cap the first run at a lower clock than the
 second.
+
+--contend: shader-clock cycles per MFMA of a wave issuing independent MFMAs
+(bf16 32x32x16 or fp8 32x32x64, accumulators in VGPRs or AGPRs) while the
+other wave on its SIMD idles, runs independent v_fma_f32 work, or issues the
+same MFMAs, with the clock the chip held meanwhile.
 
 --wg-read: the read bandwidth of one workgroup (256 threads, 16-byte loads,
 eight in flight per thread) against many, on data just written and on data
@@ -67,6 +72,8 @@ def load() -> ctypes.CDLL:
     lib.mxp_wg_read_launch.restype = i
     lib.mxp_mfma_rate_launch.argtypes = [i, i, i, vp, vp, vp]
     lib.mxp_mfma_rate_launch.restype = i
+    lib.mxp_contend_launch.argtypes = [i, i, i, i, i, vp, vp, vp, vp, vp, vp]
+    lib.mxp_contend_launch.restype = i
     lib.mxp_stream_launch.argtypes = [i, i, vp, ll, ll, i, vp, vp]
     lib.mxp_stream_launch.restype = i
     lib.mxp_error_string.argtypes = [i]
@@ -147,8 +154,11 @@ def mfma_rate(lib, target_ms: float = 70.0, reps: int = 3) -> list[str]:
     for shape, name, flop, operands in ((0, "32x32x16 bf16, VGPR accumulators", 32768, bf16),
                                         (2, "32x32x16 bf16, AGPR accumulators", 32768, bf16),
                                         (1, "16x16x32 bf16, VGPR accumulators", 16384, bf16),
+                                        (5, "16x16x32 bf16, AGPR accumulators", 16384, bf16),
                                         (3, "32x32x64 fp8, VGPR accumulators", 131072, fp8),
-                                        (4, "16x16x128 fp8, VGPR accumulators", 65536, fp8)):
+                                        (6, "32x32x64 fp8, AGPR accumulators", 131072, fp8),
+                                        (4, "16x16x128 fp8, VGPR accumulators", 65536, fp8),
+                                        (7, "16x16x128 fp8, AGPR accumulators", 65536, fp8)):
         for label, ops in operands.items():
             iters = 2000
             t = ms_of(shape, ops, iters)
@@ -206,6 +216,59 @@ def wg_read(lib, reps: int = 20) -> list[str]:
     return lines
 
 
+CONTEND_FORMS = [(0, "32x32x16 bf16, VGPR accumulators"), (1, "32x32x16 bf16, AGPR accumulators"),
+                 (2, "32x32x64 fp8, VGPR accumulators"), (3, "32x32x64 fp8, AGPR accumulators")]
+
+
+def contend(lib, iters: int = 4000, reps: int = 3) -> list[str]:
+    import torch
+
+    nwg = torch.cuda.get_device_properties(0).multi_processor_count
+    g = torch.Generator(device="cuda").manual_seed(7)
+    bf16 = torch.randn(nwg * 512 * 32, device="cuda", generator=g).to(torch.bfloat16)
+    fp8 = torch.randn(nwg * 512 * 64, device="cuda", generator=g).to(torch.float8_e4m3fn)
+    out = torch.empty(nwg * 512, dtype=torch.float32, device="cuda")
+    cycles = torch.zeros(nwg * 8, dtype=torch.int64, device="cuda")
+    rtime = torch.zeros(nwg * 8, dtype=torch.int64, device="cuda")
+    hwid = torch.zeros(nwg * 8, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(form, busy):
+        """Median over reps of: cycles per MFMA of waves 0-3, their clock (GHz from the
+        100 MHz real-time counter), waves 4-7's cycles, and the share of workgroups whose
+        waves w and w + 4 report the same SIMD."""
+        valu_iters = 12 * iters if busy == 1 else 0
+        mf, clk, other, paired = [], [], [], []
+        for _ in range(reps):
+            ops = bf16 if form < 2 else fp8
+            rc = lib.mxp_contend_launch(form, busy, nwg, iters, valu_iters, ops.data_ptr(), out.data_ptr(),
+                                        cycles.data_ptr(), rtime.data_ptr(), hwid.data_ptr(), st)
+            if rc != 0:
+                raise RuntimeError(f"mxp_contend_launch: {lib.mxp_error_string(rc).decode()} ({rc})")
+            torch.cuda.synchronize()
+            c = cycles.view(nwg, 8).double()
+            rt = rtime.view(nwg, 8).double()
+            mf.append(c[:, :4].median().item() / (iters * 8))
+            clk.append((c[:, :4] / rt[:, :4].clamp(min=1)).median().item() / 10)
+            other.append(c[:, 4:].median().item())
+            simd = (hwid.view(nwg, 8) >> 4) & 3
+            paired.append((simd[:, :4] == simd[:, 4:]).all(dim=1).float().mean().item())
+        return statistics.median(mf), statistics.median(clk), statistics.median(other), min(paired)
+
+    lines = ["| MFMA (operands random) | waves 4-7 | waves 0-3: cycles per MFMA | clock GHz | "
+             "waves 4-7: cycles per instruction | waves 4-7 took (cycles) | waves 0-3 took | waves share a SIMD |",
+             "|---|---|---:|---:|---:|---:|---:|---:|"]
+    for form, name in CONTEND_FORMS:
+        for busy, label in ((0, "idle"), (1, "v_fma_f32 stream"), (2, "the same MFMA stream")):
+            per_wave, ghz, other, paired = run(form, busy)
+            n_other = 12 * iters * 32 if busy == 1 else iters * 8
+            o_per = f"{other / n_other:.1f}" if busy else ""
+            o_tot = f"{other:.0f}" if busy else ""
+            lines.append(f"| {name} | {label} | {per_wave:.1f} | {ghz:.2f} | {o_per} | {o_tot} | "
+                         f"{per_wave * iters * 8:.0f} | {100 * paired:.0f}% |")
+    return lines
+
+
 STREAM_CASES = [  # (name, workgroups, element stride between workgroups, elements per workgroup)
     ("1 workgroup x 1 MB", 1, 0, (1 << 20) // 16),
     ("256 workgroups x 256 KB, distinct", 256, (256 << 10) // 16, (256 << 10) // 16),
@@ -258,11 +321,12 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--overlap", action="store_true")
     ap.add_argument("--mfma-rate", action="store_true")
+    ap.add_argument("--contend", action="store_true")
     ap.add_argument("--wg-read", action="store_true")
     ap.add_argument("--stream", action="store_true")
     ap.add_argument("--iters", type=int, default=2000, help="overlap-probe iterations per launch")
     args = ap.parse_args()
-    every = not (args.overlap or args.mfma_rate or args.wg_read or args.stream)
+    every = not (args.overlap or args.mfma_rate or args.contend or args.wg_read or args.stream)
     import torch
 
     if not torch.cuda.is_available():
@@ -278,6 +342,9 @@ def main() -> int:
     if every or args.mfma_rate:
         print("\n## Chip-wide MFMA throughput, two waves per SIMD\n")
         print("\n".join(mfma_rate(lib)), flush=True)
+    if every or args.contend:
+        print("\n## MFMAs beside another wave's VALU work (cycles per MFMA, two waves per SIMD)\n")
+        print("\n".join(contend(lib)), flush=True)
     if every or args.wg_read:
         print("\n## Read bandwidth of one workgroup against many\n")
         print("\n".join(wg_read(lib)), flush=True)
