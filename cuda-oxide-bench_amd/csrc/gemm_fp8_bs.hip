@@ -16,10 +16,9 @@
 //  * Each K tile is one 128-deep scale block: two MFMAs build a fresh fp32
 //    partial per 32x32 fragment, promoted with one FMA per element,
 //    acc += (sA[m,kb] * sB[kb,nb]) * partial (arbitrary fp32 scales, so the
-//    power-of-two E8M0 hardware scales cannot carry them).  The fragments
-//    of one row block build their partials side by side, so no MFMA waits
-//    for the one just before it, and the promotion of one row block
-//    overlaps the MFMAs of the next.
+//    power-of-two E8M0 hardware scales cannot carry them).  Each fragment's
+//    two MFMAs issue back to back and the previous fragment's promotion
+//    follows them, so its FMAs run while those two MFMAs execute.
 //  * 256x256 tiles, 8 waves (2 in m x 4 in n, two per SIMD), each wave
 //    128(m) x 64(n): the fp32 accumulators stay in architectural VGPRs,
 //    where the promotion FMAs can reach them.  Grids under 256 such tiles
@@ -247,10 +246,10 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     for (int n = 0; n < LPS; ++n) issue_part(s, s, n);
 
   // Scale block j: stages 2j (slot s0) and 2j+1 (slot s1).  The two MFMAs
-  // of each fragment build a fresh fp32 partial over the block's 128 k; the
-  // fragments of one row block build theirs side by side, then each is
-  // promoted with one FMA per element: acc += (sA sB) * partial.  Stages
-  // 2j+3 and 2j+4 are issued spread over the row blocks.
+  // of each fragment build a fresh fp32 partial over the block's 128 k,
+  // promoted with one FMA per element after the next fragment's two MFMAs:
+  // acc += (sA sB) * partial.  Stages 2j+3 and 2j+4 are issued spread over
+  // the row blocks.
   int s0 = 0;  // slot of stage 2j
   for (int j = 0; j < kblocks; ++j) {
     // Stages 2j, 2j+1 and the scales of block j landed (stage 2j+2 may be
@@ -267,19 +266,22 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     const int s4 = s3 == NS - 1 ? 0 : s3 + 1;
     const uint32_t so0 = s0 * CF::STAGE, so1 = s1 * CF::STAGE;
 
-    // Issue order (pinned by sched barriers): at most ~10 LDS reads in
-    // flight (lgkmcnt counts 15), each MFMA waiting only for its own
-    // fragments; the promotion of partial nf of row block mf is issued
-    // after the MFMA that follows its last one, so its FMAs run in that
-    // MFMA's shadow; a partial is rewritten only after its FMAs issued.
+    // Issue order (pinned by sched barriers): each fragment's two MFMAs
+    // back to back, then the promotion of the fragment before it, so its
+    // FMAs wait only for an MFMA that finished while the next fragment's
+    // two were queued (an FMA group between the two MFMAs of a fragment
+    // leaves the MFMA pipe idle while it issues).  At most ~10 LDS reads in
+    // flight (lgkmcnt counts 15); a partial is rewritten only after its FMAs
+    // issued; a row block's A fragments are refilled once their last MFMA
+    // issued.
     i32x8 bf0[FN], bf1[FN], a0, a1;
-    f32x16 p[FN];
+    f32x16 p[2];  // partials of consecutive fragments (mf, nf) in turn
     bf0[0] = read_b(so0, 0);
     a0 = read_a(so0, 0);
-#pragma unroll
-    for (int nf = 1; nf < FN; ++nf) bf0[nf] = read_b(so0, nf);
+    bf1[0] = read_b(so1, 0);
+    a1 = read_a(so1, 0);
     __builtin_amdgcn_sched_barrier(0);
-    auto promote = [&](int nf, int mf) { acc[nf][mf] += s_m[mf] * p[nf]; };
+    auto promote = [&](int nf, int mf) { acc[nf][mf] += s_m[mf] * p[(mf * FN + nf) & 1]; };
     auto dma_share = [&](int mf) {
 #pragma unroll
       for (int n = (2 * LPS * mf) / FM; n < (2 * LPS * (mf + 1)) / FM; ++n) {
@@ -293,43 +295,29 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     for (int mf = 0; mf < FM; ++mf) {
 #pragma unroll
       for (int nf = 0; nf < FN; ++nf) {
-        p[nf] = mfma32_fp8(bf0[nf], a0, f32x16{});
+        f32x16& pp = p[(mf * FN + nf) & 1];
+        pp = mfma32_fp8(bf0[nf], a0, f32x16{});
         __builtin_amdgcn_sched_barrier(0);
-        if (nf == 0) {
-          if (mf == 0) {
-            bf1[0] = read_b(so1, 0);
-            a1 = read_a(so1, 0);
-          } else if (FN > 1) {
-            promote(FN - 1, mf - 1);  // the previous row block's last partial, in this MFMA's shadow
-          }
+        if (mf == 0 && nf + 1 < FN) {
+          bf0[nf + 1] = read_b(so0, nf + 1);
+          bf1[nf + 1] = read_b(so1, nf + 1);
         }
         if (nf == FN - 1) {
-          if (mf == 0) {
-#pragma unroll
-            for (int n2 = 1; n2 < FN; ++n2) bf1[n2] = read_b(so1, n2);
-          }
           if (mf + 1 < FM) a0 = read_a(so0, mf + 1);
           dma_share(mf);
         }
         __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int nf = 0; nf < FN; ++nf) {
-        p[nf] = mfma32_fp8(bf1[nf], a1, p[nf]);
+        pp = mfma32_fp8(bf1[nf], a1, pp);
+        __builtin_amdgcn_sched_barrier(0);
+        if (nf == FN - 1 && mf + 1 < FM) a1 = read_a(so1, mf + 1);
+        if (nf > 0)
+          promote(nf - 1, mf);
+        else if (mf > 0)
+          promote(FN - 1, mf - 1);
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (mf + 1 < FM) a1 = read_a(so1, mf + 1);
-      // every partial but the last is promoted in the shadow of the
-      // MFMAs still running; the last one at the next row block's first
-      if constexpr (FN == 1) {
-        promote(0, mf);
-      } else {
-#pragma unroll
-        for (int nf = 0; nf + 1 < FN; ++nf) promote(nf, mf);
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (FN > 1) promote(FN - 1, FM - 1);
+    promote(FN - 1, FM - 1);  // the block's last fragment
     s0 = s0 >= NS - 2 ? s0 - (NS - 2) : s0 + 2;
   }
   wait_scales<0>(sa_n, sb_n);  // no DMA may land in LDS after the workgroup ends

@@ -28,6 +28,16 @@
 //    them (busy = 1), or issue the same MFMA stream (busy = 2).  Each wave
 //    records its hardware id, so the host can check that waves w and w + 4
 //    share a SIMD.
+//  * mxp_promote_launch: the fp8 GEMM's block promotion.  Every wave keeps
+//    8 fp32 accumulators of 32x32 and per iteration, for each, builds a
+//    fresh partial from two 32x32x64 fp8 MFMAs (one 128-deep scale block)
+//    and promotes it, acc += s * partial (16 v_fma per lane); the partials
+//    rotate through NP registers sets, and the promotion of fragment f runs
+//    after the MFMAs of fragment f + LAG, in the compiler's order or in an
+//    enforced one.  Variants: no promotion (the MFMAs accumulate straight
+//    into the accumulators), alone or beside the same FMAs on registers no
+//    MFMA writes.  One workgroup per CU of 4 waves (one per
+//    SIMD) or 8 (two per SIMD); shader-clock cycles per wave.
 //  * mxp_wg_read_launch: nwg workgroups of 256 threads; workgroup w reads n16
 //    16-byte elements starting at element w * stride16 (eight loads in
 //    flight per thread) and writes one XOR per thread, so the time of a
@@ -395,6 +405,91 @@ int launch_contend(int busy, int nwg, int iters, int valu_iters, const u32x4* op
   return hip_status(hipGetLastError());
 }
 
+// MODE 0: no promotion; 1: acc += s * partial, the partial of fragment f
+// promoted after the MFMAs of fragment f + LAG (NP = LAG + 1 partial sets,
+// rounded up to a divisor of 8), in the compiler's order; 3: the same with
+// that order enforced (scheduling groups: the fragment's two MFMAs, then the
+// 16 FMAs); 2: mode 0's MFMAs plus the same FMAs on registers no MFMA
+// writes.  cycles[b * NW + w].
+template <int MODE, int LAG, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void promote_kernel(const u32x4* __restrict__ ops, float* out,
+                                                            long long* cycles, int iters) {
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  constexpr int NP = LAG + 1 <= 2 ? 2 : (LAG + 1 <= 4 ? 4 : 8);
+  const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  u32x4 q[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) q[j] = ops[t * 4 + j];
+  i32x8 a8 = __builtin_bit_cast(i32x8, (u32x4[2]){q[0], q[1]});
+  const i32x8 b8 = __builtin_bit_cast(i32x8, (u32x4[2]){q[2], q[3]});
+  const float sc = 1.0f + 1e-3f * (float)(threadIdx.x & 7);
+  f32x16 acc[8], part[NP];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
+#pragma unroll
+  for (int j = 0; j < NP; ++j) part[j] = f32x16{} + 1e-3f * j;
+  auto promote = [&](int f) {
+    const f32x16& p = part[f % NP];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[f][e] = __builtin_fmaf(sc, p[e], acc[f][e]);
+  };
+  const long long t0 = __builtin_readcyclecounter();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      // an empty statement that the compiler must assume rewrote the operand,
+      // so no fragment's fresh partial is hoisted out of the loop or shared
+      asm volatile("" : "+v"(a8));
+      if constexpr (MODE == 0 || MODE == 2) {
+        acc[f] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[f], 0, 0, 0, 127, 0, 127);
+        acc[f] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b8, a8, acc[f], 0, 0, 0, 127, 0, 127);
+        if constexpr (MODE == 2) {
+          const f32x16& r = part[f % NP];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) part[(f + 1) % NP][e] = __builtin_fmaf(sc, r[e], part[(f + 1) % NP][e]);
+        }
+      } else {
+        f32x16 p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, f32x16{}, 0, 0, 0, 127, 0, 127);
+        p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b8, a8, p, 0, 0, 0, 127, 0, 127);
+        part[f % NP] = p;
+        if (f >= LAG) promote(f - LAG);
+        if constexpr (MODE == 3) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          if (f >= LAG) __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+        }
+      }
+    }
+    if constexpr (MODE == 1 || MODE == 3) {
+#pragma unroll
+      for (int f = 8 - LAG; f < 8; ++f) promote(f);
+    }
+  }
+  const long long t1 = __builtin_readcyclecounter();
+  float r = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 15];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) r += part[j][threadIdx.x & 15];
+  out[t] = r;
+  if ((threadIdx.x & 63) == 0) cycles[blockIdx.x * NW + wave] = t1 - t0;
+}
+
+template <int MODE, int LAG, int NW>
+int launch_promote(int nwg, int iters, const u32x4* ops, float* out, long long* cycles, hipStream_t s) {
+  hipLaunchKernelGGL((promote_kernel<MODE, LAG, NW>), dim3(nwg), dim3(64 * NW), 0, s, ops, out, cycles, iters);
+  return hip_status(hipGetLastError());
+}
+
+template <int MODE, int NW>
+int launch_promote_lag(int lag, int nwg, int iters, const u32x4* ops, float* out, long long* cycles, hipStream_t s) {
+  switch (lag) {
+    case 1: return launch_promote<MODE, 1, NW>(nwg, iters, ops, out, cycles, s);
+    case 2: return launch_promote<MODE, 2, NW>(nwg, iters, ops, out, cycles, s);
+    default: return launch_promote<MODE, 3, NW>(nwg, iters, ops, out, cycles, s);
+  }
+}
+
 template <int DEPTH>
 __global__ __launch_bounds__(256) void stream_reg_kernel(const uint4* __restrict__ src, long long stride16,
                                                         long long n16, unsigned* out) {
@@ -549,6 +644,29 @@ extern "C" int mxp_contend_launch(int form, int busy, int nwg, int iters, int va
     case 1: return launch_contend<1>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
     case 2: return launch_contend<2>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
     default: return launch_contend<3>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
+  }
+}
+
+// mode 0..3 as promote_kernel; lag 1..3 (modes 1 and 3); waves 4 or 8 per
+// workgroup.  ops: nwg * 64 * waves * 4 16-byte fragments (lane t reads its 4
+// at 4 t); out: nwg * 64 * waves floats; cycles: nwg * waves.
+extern "C" int mxp_promote_launch(int mode, int lag, int waves, int nwg, int iters, const void* ops, float* out,
+                                  long long* cycles, void* stream) {
+  if (nwg <= 0 || iters <= 0 || !ops || !out || !cycles || mode < 0 || mode > 3 || (waves != 4 && waves != 8) ||
+      ((mode == 1 || mode == 3) && (lag < 1 || lag > 3)))
+    return -1;
+  const u32x4* o = static_cast<const u32x4*>(ops);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool two = waves == 8;
+  switch (mode) {
+    case 0: return two ? launch_promote<0, 1, 8>(nwg, iters, o, out, cycles, s)
+                       : launch_promote<0, 1, 4>(nwg, iters, o, out, cycles, s);
+    case 2: return two ? launch_promote<2, 1, 8>(nwg, iters, o, out, cycles, s)
+                       : launch_promote<2, 1, 4>(nwg, iters, o, out, cycles, s);
+    case 1: return two ? launch_promote_lag<1, 8>(lag, nwg, iters, o, out, cycles, s)
+                       : launch_promote_lag<1, 4>(lag, nwg, iters, o, out, cycles, s);
+    default: return two ? launch_promote_lag<3, 8>(lag, nwg, iters, o, out, cycles, s)
+                        : launch_promote_lag<3, 4>(lag, nwg, iters, o, out, cycles, s);
   }
 }
 

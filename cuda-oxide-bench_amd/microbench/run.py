@@ -1,7 +1,8 @@
 """Run the MI355X characterisation probes (libmxprobes.so, built with the
 kernel library) and print their results as Markdown tables.
 
-    python cuda-oxide-bench_amd/microbench/run.py [--overlap] [--mfma-rate] [--contend] [--wg-read] [--stream]
+    python cuda-oxide-bench_amd/microbench/run.py [--overlap] [--mfma-rate] [--contend] [--promote]
+                                                  [--wg-read] [--stream]
 
 --overlap: how much of a wave's other work runs beside its own MFMAs at one
 wave per SIMD.  For each instruction mix: shader-clock cycles per iteration
@@ -19,6 +20,11 @@ second.
 (bf16 32x32x16 or fp8 32x32x64, accumulators in VGPRs or AGPRs) while the
 other wave on its SIMD idles, runs independent v_fma_f32 work, or issues the
 same MFMAs, with the clock the chip held meanwhile.
+
+--promote: the fp8 GEMM's block promotion (two 32x32x64 fp8 MFMAs into a
+fresh partial, then acc += s * partial) in shader-clock cycles per
+fragment-block and SIMD, against the MFMAs alone and against the same FMAs
+on registers no MFMA writes, at one and two waves per SIMD.
 
 --wg-read: the read bandwidth of one workgroup (256 threads, 16-byte loads,
 eight in flight per thread) against many, on data just written and on data
@@ -74,6 +80,8 @@ def load() -> ctypes.CDLL:
     lib.mxp_mfma_rate_launch.restype = i
     lib.mxp_contend_launch.argtypes = [i, i, i, i, i, vp, vp, vp, vp, vp, vp]
     lib.mxp_contend_launch.restype = i
+    lib.mxp_promote_launch.argtypes = [i, i, i, i, i, vp, vp, vp, vp]
+    lib.mxp_promote_launch.restype = i
     lib.mxp_stream_launch.argtypes = [i, i, vp, ll, ll, i, vp, vp]
     lib.mxp_stream_launch.restype = i
     lib.mxp_error_string.argtypes = [i]
@@ -269,6 +277,45 @@ def contend(lib, iters: int = 4000, reps: int = 3) -> list[str]:
     return lines
 
 
+PROMOTE_CASES = [(0, 1, "MFMAs only (accumulating straight into the accumulators)"),
+                 (2, 1, "MFMAs only, beside the same FMAs on registers no MFMA writes"),
+                 (1, 1, "promotion, the compiler's order (lag 1: two partial sets)"),
+                 (1, 3, "promotion, the compiler's order (lag 3: four partial sets)"),
+                 (3, 1, "promotion after the next fragment's two MFMAs (enforced)"),
+                 (3, 2, "promotion after two more fragments' MFMAs (enforced)"),
+                 (3, 3, "promotion after three more fragments' MFMAs (enforced)")]
+
+
+def promote(lib, iters: int = 2000, reps: int = 3) -> list[str]:
+    import torch
+
+    nwg = torch.cuda.get_device_properties(0).multi_processor_count
+    g = torch.Generator(device="cuda").manual_seed(11)
+    ops = torch.randn(nwg * 512 * 64, device="cuda", generator=g).to(torch.float8_e4m3fn)
+    out = torch.empty(nwg * 512, dtype=torch.float32, device="cuda")
+    cycles = torch.zeros(nwg * 8, dtype=torch.int64, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(mode, lag, waves):
+        vals = []
+        for _ in range(reps):
+            rc = lib.mxp_promote_launch(mode, lag, waves, nwg, iters, ops.data_ptr(), out.data_ptr(),
+                                        cycles.data_ptr(), st)
+            if rc != 0:
+                raise RuntimeError(f"mxp_promote_launch: {lib.mxp_error_string(rc).decode()} ({rc})")
+            torch.cuda.synchronize()
+            c = cycles[: nwg * waves].view(nwg, waves).double()
+            vals.append(c.max(dim=1).values.median().item() / (iters * 8 * (waves // 4)))
+        return statistics.median(vals)
+
+    lines = ["| per fragment and scale block (2 MFMAs = 128 MFMA cycles, 16 v_fma) | one wave per SIMD | two waves per SIMD |",
+             "|---|---:|---:|"]
+    for mode, lag, name in PROMOTE_CASES:
+        one, two = run(mode, lag, 4), run(mode, lag, 8)
+        lines.append(f"| {name} | {one:.1f} | {two:.1f} |")
+    return lines
+
+
 STREAM_CASES = [  # (name, workgroups, element stride between workgroups, elements per workgroup)
     ("1 workgroup x 1 MB", 1, 0, (1 << 20) // 16),
     ("256 workgroups x 256 KB, distinct", 256, (256 << 10) // 16, (256 << 10) // 16),
@@ -322,11 +369,12 @@ def main() -> int:
     ap.add_argument("--overlap", action="store_true")
     ap.add_argument("--mfma-rate", action="store_true")
     ap.add_argument("--contend", action="store_true")
+    ap.add_argument("--promote", action="store_true")
     ap.add_argument("--wg-read", action="store_true")
     ap.add_argument("--stream", action="store_true")
     ap.add_argument("--iters", type=int, default=2000, help="overlap-probe iterations per launch")
     args = ap.parse_args()
-    every = not (args.overlap or args.mfma_rate or args.contend or args.wg_read or args.stream)
+    every = not (args.overlap or args.mfma_rate or args.contend or args.promote or args.wg_read or args.stream)
     import torch
 
     if not torch.cuda.is_available():
@@ -345,6 +393,9 @@ def main() -> int:
     if every or args.contend:
         print("\n## MFMAs beside another wave's VALU work (cycles per MFMA, two waves per SIMD)\n")
         print("\n".join(contend(lib)), flush=True)
+    if every or args.promote:
+        print("\n## fp8 block promotion (shader-clock cycles per fragment and scale block, per SIMD)\n")
+        print("\n".join(promote(lib)), flush=True)
     if every or args.wg_read:
         print("\n## Read bandwidth of one workgroup against many\n")
         print("\n".join(wg_read(lib)), flush=True)
