@@ -23,13 +23,15 @@
 //    128(m) x 64(n): the fp32 accumulators stay in architectural VGPRs,
 //    where the promotion FMAs can reach them.  Grids under 256 such tiles
 //    use 128x128 tiles.
-//  * A and B go HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging)
-//    in 64-byte-deep stages (half a scale block) through a 5-slot ring that
-//    fills the 160 KB of LDS: while a wave computes scale block j (stages
-//    2j, 2j+1) the stages 2j+2 .. 2j+4 are in flight, one and a half scale
-//    blocks ahead, with one barrier per scale block.  Every block issues
-//    exactly two stages (past the end, the last stage again into slots
-//    nobody reads), so the wait counts are the same in every block.
+//  * A and B go HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging),
+//    filling the 160 KB of LDS with two rings: A in whole scale blocks (BM
+//    rows of 128 bytes, so every load request is a full 128-byte line; rows
+//    of 64 bytes made each line two half-line requests, which kept the L1
+//    address path stalled) in 3 slots, issued two blocks ahead; B in
+//    64-deep stages (64 k-rows of BN bytes, whole lines already) in 4
+//    slots, one block ahead.  One barrier per scale block.  Every block
+//    issues the same loads (past the end, the last block again into slots
+//    nobody reads), so the wait counts never vary.
 //  * The block scales are read with vector loads issued as inline asm and
 //    waited for by the same vmcnt wait that lands the stages, as operands
 //    of that wait: the compiler tracks neither, so it never inserts a
@@ -47,9 +49,10 @@
 namespace mx {
 namespace gemm8 {
 
-constexpr int SBK = 128;   // bytes of K per scale block
-constexpr int BKS = 64;    // bytes of K per LDS stage (one 32x32x64 k-step)
-constexpr int NS = 5;      // ring slots
+constexpr int SBK = 128;   // bytes of K per scale block (= per A slot)
+constexpr int BKS = 64;    // bytes of K per B stage (one 32x32x64 k-step)
+constexpr int NSA = 3;     // A ring slots (whole scale blocks)
+constexpr int NSB = 4;     // B ring slots (half scale blocks)
 constexpr int NWAVES = 8;  // 2 (m) x 4 (n), two waves per SIMD
 constexpr int NT = 64 * NWAVES;
 constexpr int GROUP_M = 8;
@@ -95,13 +98,13 @@ struct Cfg {
   static constexpr int WM = 2, WN = 4;
   static constexpr int TM = BM / WM, TN = BN / WN;   // wave tile
   static constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments
-  static constexpr int A_S = BM * BKS;               // A stage: BM rows of 64 B
-  static constexpr int B_S = BKS * BN;               // B stage: 64 k-rows of BN B
-  static constexpr int STAGE = A_S + B_S;
-  static constexpr int LDS = NS * STAGE;
-  static constexpr int A_LPW = A_S / 1024 / NWAVES;  // 1 KB direct loads per wave per stage
-  static constexpr int B_LPW = B_S / 1024 / NWAVES;
-  static constexpr int LPS = A_LPW + B_LPW;
+  static constexpr int A_S = BM * SBK;               // A slot: BM rows of 128 B (one scale block)
+  static constexpr int B_S = BKS * BN;               // B slot: 64 k-rows of BN B
+  static constexpr int B_OFF = NSA * A_S;            // the B ring follows the A ring
+  static constexpr int LDS = NSA * A_S + NSB * B_S;
+  static constexpr int A_LPW = A_S / 1024 / NWAVES;  // 1 KB direct loads per wave per A block
+  static constexpr int B_LPW = B_S / 1024 / NWAVES;  // ... per B stage
+  static constexpr int A_RPL = 1024 / SBK;           // A rows per 1 KB load
   static constexpr int B_CH = BN / 16;               // 16-byte chunks per B row
   static constexpr int B_RPL = 1024 / BN;            // B rows per 1 KB load
   static_assert(FM >= 1 && FN >= 1 && A_LPW >= 1 && B_LPW >= 1, "tile split");
@@ -110,11 +113,11 @@ struct Cfg {
   static_assert(LDS <= 160 * 1024, "LDS ring");
 };
 
-// Chunk position swizzles.  A rows (64 B, 4 chunks): a 16-lane b128 phase
-// reads one chunk of 16 consecutive rows, four rows per 256 B, so the
-// position takes (m/4)%4.  B rows: a 32-lane transposing phase reads 8
+// Chunk position swizzles.  A rows (128 B, 8 chunks): a 16-lane b128 phase
+// reads one chunk of 16 consecutive rows, two rows per 256 B, so the
+// position takes (m/2)%8.  B rows: a 32-lane transposing phase reads 8
 // consecutive k-rows x 2 adjacent chunks.
-__device__ __forceinline__ int swz_a(int m) { return (m >> 2) & 3; }
+__device__ __forceinline__ int swz_a(int m) { return (m >> 1) & 7; }
 template <int BN>
 __device__ __forceinline__ int swz_b(int k) {
   return BN == 256 ? ((k & 7) << 1) : (((k >> 1) & 3) << 1);
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
                                                            const float* __restrict__ sB,
                                                            uint16_t* __restrict__ C, int M, int N, int K) {
   using CF = Cfg<BM, BN>;
-  constexpr int FM = CF::FM, FN = CF::FN, LPS = CF::LPS;
+  constexpr int FM = CF::FM, FN = CF::FN;
   extern __shared__ __align__(1024) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
@@ -148,8 +151,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   const int nst = 2 * kblocks;  // 64-byte stages
   const int nblocks_n = (N + 127) / 128;
 
-  // ---- direct loads.  A load n: rows 16n .. 16n+15 (lane i: row 16n + i/4,
-  // chunk (i%4) ^ swz_a(row)); B load n: k-rows B_RPL*n .. (lane i: k-row
+  // ---- direct loads.  A load n: rows 8n .. 8n+7 (lane i: row 8n + i/8,
+  // chunk (i%8) ^ swz_a(row)); B load n: k-rows B_RPL*n .. (lane i: k-row
   // B_RPL*n + i/B_CH, chunk (i%B_CH) ^ swz_b(row)).  Rows past M and
   // columns past N re-read the last valid ones (never stored). ----
   const uint32_t lds0 = lds_addr(smem);
@@ -157,9 +160,9 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   uint32_t a_off[CF::A_LPW], b_off[CF::B_LPW];
 #pragma unroll
   for (int n = 0; n < CF::A_LPW; ++n) {
-    const int row = 16 * (wave * CF::A_LPW + n) + (lane >> 2);
+    const int row = CF::A_RPL * (wave * CF::A_LPW + n) + (lane >> 3);
     const int gm = full_m ? m0 + row : min(m0 + row, M - 1);
-    a_off[n] = (uint32_t)(gm - m0) * K + 16 * ((lane & 3) ^ swz_a(row));
+    a_off[n] = (uint32_t)(gm - m0) * K + 16 * ((lane & 7) ^ swz_a(row));
   }
 #pragma unroll
   for (int n = 0; n < CF::B_LPW; ++n) {
@@ -170,25 +173,30 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   }
   const uint8_t* a_tile = A + (size_t)m0 * K;
   const uint8_t* b_tile = B + n0;
-  // Stage s (64 bytes of K) into slot s % NS; stages past the end re-load
-  // the last one (into a slot no later block reads).
-  auto issue_part = [&](int s, int slot, int n) {
+  // Part n of A block j (128 bytes of K: whole 128-byte lines of every row)
+  // into A slot j % NSA, and of B stage s (64 bytes of K) into B slot
+  // s % NSB.  Blocks and stages past the end re-load the last one (into a
+  // slot no later block reads).
+  auto issue_a = [&](int j, int n) {
+    const int src = min(j, kblocks - 1);
+    dma16(a_tile + (size_t)src * SBK, a_off[n], lds0 + (j % NSA) * CF::A_S + (wave * CF::A_LPW + n) * 1024);
+  };
+  auto issue_b = [&](int s, int n) {
     const int src = min(s, nst - 1);
-    const uint32_t st = lds0 + slot * CF::STAGE;
-    if (n < CF::A_LPW)
-      dma16(a_tile + (size_t)src * BKS, a_off[n], st + (wave * CF::A_LPW + n) * 1024);
-    else
-      dma16(b_tile + (size_t)src * BKS * N, b_off[n - CF::A_LPW],
-            st + CF::A_S + (wave * CF::B_LPW + n - CF::A_LPW) * 1024);
+    dma16(b_tile + (size_t)src * BKS * N, b_off[n],
+          lds0 + CF::B_OFF + (s % NSB) * CF::B_S + (wave * CF::B_LPW + n) * 1024);
   };
 
-  // ---- fragment lane addresses in slot 0 (a slot is STAGE bytes on) ----
-  // A^T (B operand): row m = wm*TM + 32 mf + l%32, chunks 2 (l/32) + {0,1}.
+  // ---- fragment lane addresses in the first slot of each ring ----
+  // A^T (B operand): row m = wm*TM + 32 mf + l%32, chunks 4 kh + 2 (l/32)
+  // + {0,1} for the block's k half kh.
   const int am = wm * CF::TM + (lane & 31);
   const int a_x = swz_a(am);  // the same for every mf (32 rows apart)
-  uint32_t a_col[2];
+  uint32_t a_col[2][2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) a_col[h] = lds0 + am * BKS + 16 * ((2 * (lane >> 5) + h) ^ a_x);
+  for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) a_col[kh][h] = lds0 + am * SBK + 16 * ((4 * kh + 2 * (lane >> 5) + h) ^ a_x);
   // B^T (A operand) via tr_b8: in 16-lane group q, lane 2j+h reads k-row
   // 32 (q>>1) + 8 r + j, columns wn*TN + 32 nf + 16 (q&1) + 8 h.
   const int q = lane >> 4, jj = (lane & 15) >> 1, hh = lane & 1;
@@ -199,7 +207,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
 #pragma unroll
   for (int nf = 0; nf < FN; ++nf) {
     const int col = b_c0 + 32 * nf;
-    b_col[nf] = lds0 + CF::A_S + b_k0 * BN + 16 * ((col >> 4) ^ b_x) + (col & 15);
+    b_col[nf] = lds0 + CF::B_OFF + b_k0 * BN + 16 * ((col >> 4) ^ b_x) + (col & 15);
   }
 
   f32x16 acc[FN][FM];
@@ -229,42 +237,45 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     return i32x8{(int)v[0][0], (int)v[0][1], (int)v[1][0], (int)v[1][1],
                  (int)v[2][0], (int)v[2][1], (int)v[3][0], (int)v[3][1]};
   };
-  auto read_a = [&](uint32_t so, int mf) {
-    const uint32_t r = so + 32 * mf * BKS;
-    const u32x4 lo = lds_ld128(a_col[0] + r);
-    const u32x4 hi = lds_ld128(a_col[1] + r);
+  auto read_a = [&](uint32_t so, int kh, int mf) {
+    const uint32_t r = so + 32 * mf * SBK;
+    const u32x4 lo = lds_ld128(a_col[kh][0] + r);
+    const u32x4 hi = lds_ld128(a_col[kh][1] + r);
     return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
   };
 
   land_args(C);  // C is used only after the loop
 
-  // Prologue: the scales of block 0 and stages 0..2 in flight.
+  // Prologue, in the order the block waits need: the scales of block 0,
+  // A block 0, B stages 0 and 1, then A block 1 (which may still be in
+  // flight when block 0 starts).
   load_scales(0);
 #pragma unroll
-  for (int s = 0; s < 3; ++s)
+  for (int n = 0; n < CF::A_LPW; ++n) issue_a(0, n);
 #pragma unroll
-    for (int n = 0; n < LPS; ++n) issue_part(s, s, n);
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int n = 0; n < CF::B_LPW; ++n) issue_b(s, n);
+#pragma unroll
+  for (int n = 0; n < CF::A_LPW; ++n) issue_a(1, n);
 
-  // Scale block j: stages 2j (slot s0) and 2j+1 (slot s1).  The two MFMAs
-  // of each fragment build a fresh fp32 partial over the block's 128 k,
-  // promoted with one FMA per element after the next fragment's two MFMAs:
-  // acc += (sA sB) * partial.  Stages 2j+3 and 2j+4 are issued spread over
-  // the row blocks.
-  int s0 = 0;  // slot of stage 2j
+  // Scale block j: A block j and B stages 2j, 2j+1.  The two MFMAs of each
+  // fragment build a fresh fp32 partial over the block's 128 k, promoted
+  // with one FMA per element after the next fragment's two MFMAs:
+  // acc += (sA sB) * partial.  The block's loads (B stages 2j+2, 2j+3, then
+  // A block j+2) are issued spread over the row blocks.
   for (int j = 0; j < kblocks; ++j) {
-    // Stages 2j, 2j+1 and the scales of block j landed (stage 2j+2 may be
-    // in flight); after the barrier every wave has finished block j-1, so
-    // its slots take stages 2j+3 and 2j+4.
-    wait_scales<LPS>(sa_n, sb_n);
+    // A block j, B stages 2j, 2j+1 and the scales of block j landed (only A
+    // block j+1 may be in flight); after the barrier every wave has
+    // finished block j-1, so its A slot and B slots take the new loads.
+    wait_scales<CF::A_LPW>(sa_n, sb_n);
     lds_barrier();
     float s_m[FM];
 #pragma unroll
     for (int mf = 0; mf < FM; ++mf) s_m[mf] = sa_n[mf] * sb_n;
     load_scales(j + 1);
-    const int s1 = s0 == NS - 1 ? 0 : s0 + 1;
-    const int s3 = s0 >= 2 ? s0 - 2 : s0 + 3;  // slot of stage 2j+3 (= that of 2j-2)
-    const int s4 = s3 == NS - 1 ? 0 : s3 + 1;
-    const uint32_t so0 = s0 * CF::STAGE, so1 = s1 * CF::STAGE;
+    const uint32_t ao = (j % NSA) * CF::A_S;
+    const uint32_t so0 = ((2 * j) % NSB) * CF::B_S, so1 = ((2 * j + 1) % NSB) * CF::B_S;
 
     // Issue order (pinned by sched barriers): each fragment's two MFMAs
     // back to back, then the promotion of the fragment before it, so its
@@ -277,18 +288,19 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     i32x8 bf0[FN], bf1[FN], a0, a1;
     f32x16 p[2];  // partials of consecutive fragments (mf, nf) in turn
     bf0[0] = read_b(so0, 0);
-    a0 = read_a(so0, 0);
+    a0 = read_a(ao, 0, 0);
     bf1[0] = read_b(so1, 0);
-    a1 = read_a(so1, 0);
+    a1 = read_a(ao, 1, 0);
     __builtin_amdgcn_sched_barrier(0);
     auto promote = [&](int nf, int mf) { acc[nf][mf] += s_m[mf] * p[(mf * FN + nf) & 1]; };
+    constexpr int NLD = 2 * CF::B_LPW + CF::A_LPW;  // loads per block and wave
     auto dma_share = [&](int mf) {
 #pragma unroll
-      for (int n = (2 * LPS * mf) / FM; n < (2 * LPS * (mf + 1)) / FM; ++n) {
-        if (n < LPS)
-          issue_part(2 * j + 3, s3, n);
+      for (int n = (NLD * mf) / FM; n < (NLD * (mf + 1)) / FM; ++n) {
+        if (n < 2 * CF::B_LPW)
+          issue_b(2 * j + 2 + n / CF::B_LPW, n % CF::B_LPW);
         else
-          issue_part(2 * j + 4, s4, n - LPS);
+          issue_a(j + 2, n - 2 * CF::B_LPW);
       }
     };
 #pragma unroll
@@ -303,13 +315,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
           bf1[nf + 1] = read_b(so1, nf + 1);
         }
         if (nf == FN - 1) {
-          if (mf + 1 < FM) a0 = read_a(so0, mf + 1);
+          if (mf + 1 < FM) a0 = read_a(ao, 0, mf + 1);
           dma_share(mf);
         }
         __builtin_amdgcn_sched_barrier(0);
         pp = mfma32_fp8(bf1[nf], a1, pp);
         __builtin_amdgcn_sched_barrier(0);
-        if (nf == FN - 1 && mf + 1 < FM) a1 = read_a(so1, mf + 1);
+        if (nf == FN - 1 && mf + 1 < FM) a1 = read_a(ao, 1, mf + 1);
         if (nf > 0)
           promote(nf - 1, mf);
         else if (mf > 0)
@@ -318,7 +330,6 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
       }
     }
     promote(FN - 1, FM - 1);  // the block's last fragment
-    s0 = s0 >= NS - 2 ? s0 - (NS - 2) : s0 + 2;
   }
   wait_scales<0>(sa_n, sb_n);  // no DMA may land in LDS after the workgroup ends
 
