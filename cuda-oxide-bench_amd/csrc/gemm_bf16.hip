@@ -16,6 +16,9 @@
 // A/B tiles copied HBM -> LDS by direct loads into a 5-stage (6 at
 // 128x128) ring, one barrier per K tile, the next K tile's fragments read
 // during the current tile's MFMAs.  Details at the kernel.
+// gemm_bf16_dma16s_kernel takes the 256x256 tiles when K % 64 == 0: the
+// same MFMAs and schedule, with A in 64-deep blocks of whole 128-byte lines
+// through a ring of its own beside the B ring.
 //
 // gemm_bf16_sdma_kernel (about one 64x64 tile per CU and a long K, e.g.
 // 1024^3): two wave groups split K, each with its own direct-load ring.
@@ -732,6 +735,255 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bf16_dma16_kernel(const 
   }
 }
 
+// ---------------------------------------------------------------------------
+// gemm_bf16_dma16s_kernel: gemm_bf16_dma16_kernel's 256x256 tiles and
+// fragment schedule with whole 128-byte A lines.  In the single ring, a
+// 32-deep stage holds 64 bytes of each A row, so every A line is fetched as
+// two half-line requests; the L1 then holds up the address unit (the fp8
+// GEMM measured the same).  Here A goes through its own ring of 64-deep
+// blocks (256 rows x 128 B, 3 slots) beside a ring of 32-deep B stages
+// (32 k-rows x 512 B, 4 slots), 160 KB in all:
+//  * step kt computes K tile kt (B stage kt, half kt % 2 of A block kt / 2)
+//    and reads tile kt+1's fragments; it issues B stage kt+3 and half kt % 2
+//    of A block kt/2 + 2, each into the slot of the stage / block that the
+//    barrier just freed, so every step issues the same 4 loads per wave and
+//    waits for all but the 4 of the step before.
+//  * A rows of 8 chunks: chunk c ^ ((m >> 1) & 7) keeps the 16-lane phases
+//    of the A^T reads on distinct bank slots.
+// Shapes: K % 64 == 0 (whole A blocks).
+// ---------------------------------------------------------------------------
+struct S16Cfg {
+  static constexpr int BM = 256, BN = 256, BK = 32, BKA = 64;
+  static constexpr int WM = DMA_WM, WN = DMA_WN, NW = WM * WN, NT = 64 * NW;
+  static constexpr int TM = BM / WM, TN = BN / WN;   // wave block
+  static constexpr int FM = TM / 16, FN = TN / 16;   // 16x16 fragments
+  static constexpr int RA = BKA * 2, RB = BN * 2;    // LDS row bytes (A 128, B 512)
+  static constexpr int A_B = BM * RA, B_B = BK * RB;  // A block 32 KB, B stage 16 KB
+  static constexpr int NSA = 3, NSB = 4;
+  static constexpr int B_OFF = NSA * A_B;
+  static constexpr int LDS = NSA * A_B + NSB * B_B;
+  static constexpr int A_LPW = A_B / 1024 / NW;      // 1 KB loads per wave per A block
+  static constexpr int B_LPW = B_B / 1024 / NW;      // ... per B stage
+  static constexpr int A_RPL = 1024 / RA;            // A rows per load
+  static constexpr int B_CH = RB / 16, B_RPL = 1024 / RB;
+  static constexpr int VM = B_LPW + A_LPW / 2;       // loads per step and wave
+  static constexpr int P = 12;                        // steps until slots and parity repeat
+  static_assert(LDS <= 160 * 1024 && A_LPW % 2 == 0 && A_LPW >= 2 && B_LPW >= 1, "rings");
+};
+__device__ __forceinline__ int swz_a16w(int m) { return (m >> 1) & 7; }
+
+template <int P, int I = 0, typename Step>
+__device__ __forceinline__ void steps_s(Step& step, int kt) {
+  if constexpr (I < P) {
+    step(kt + I, std::integral_constant<int, I>{});
+    steps_s<P, I + 1>(step, kt);
+  }
+}
+template <int P, int I = 0, typename Step>
+__device__ __forceinline__ void steps_tail_s(Step& step, int kt, int n) {
+  if constexpr (I < P - 1) {
+    if (I < n) {
+      step(kt + I, std::integral_constant<int, I>{});
+      steps_tail_s<P, I + 1>(step, kt, n);
+    }
+  }
+}
+
+__global__ __launch_bounds__(S16Cfg::NT, 1) void gemm_bf16_dma16s_kernel(const uint16_t* __restrict__ A,
+                                                                        const uint16_t* __restrict__ B,
+                                                                        uint16_t* __restrict__ C, int M, int N,
+                                                                        int K, int lda, int ldb, int ldc) {
+  using CF = S16Cfg;
+  constexpr int FM = CF::FM, FN = CF::FN, BK = CF::BK, WN = CF::WN;
+  extern __shared__ __align__(1024) unsigned char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int kg = lane >> 4;  // k-group of the lane's operand and row quad of its result
+
+  // ---- tile -> (tm, tn), grouped for L2 reuse, XCD-aware ----
+  const int tiles_m = (M + CF::BM - 1) / CF::BM, tiles_n = (N + CF::BN - 1) / CF::BN;
+  const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = GROUP_M * tiles_n;
+  const int group = id / per_group;
+  const int first_m = group * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (id % per_group) % gsz;
+  const int tn = (id % per_group) / gsz;
+  const int m0 = tm * CF::BM, n0 = tn * CF::BN;
+  const int nk = K / BK, nka = K / CF::BKA;
+
+  // ---- direct-load lane offsets (bytes from the tile's first element).
+  // Rows past M / columns past N re-read the last valid ones; their
+  // results are never stored. ----
+  const uint32_t lds0 = lds_addr(smem);
+  const bool full_m = m0 + CF::BM <= M, full_n = n0 + CF::BN <= N;
+  uint32_t a_off[CF::A_LPW], b_off[CF::B_LPW];
+#pragma unroll
+  for (int n = 0; n < CF::A_LPW; ++n) {
+    const int row = CF::A_RPL * (wave * CF::A_LPW + n) + lane / 8;
+    const int gm = full_m ? m0 + row : min(m0 + row, M - 1);
+    a_off[n] = (uint32_t)(gm - m0) * (uint32_t)lda * 2u + 16u * ((lane % 8) ^ swz_a16w(row));
+  }
+#pragma unroll
+  for (int n = 0; n < CF::B_LPW; ++n) {
+    const int row = CF::B_RPL * (wave * CF::B_LPW + n) + lane / CF::B_CH;
+    int col = 8 * ((lane % CF::B_CH) ^ swz_b16(row));  // elements
+    if (!full_n) col = min(n0 + col, N - 8) - n0;
+    b_off[n] = (uint32_t)row * (uint32_t)ldb * 2u + 2u * col;
+  }
+  // B stage s into B slot s % NSB; half h of A block j into A slot j % NSA.
+  // Stages and blocks past the end re-load the last one (into slots no
+  // later step reads).
+  auto issue_b = [&](int s, int slot) {
+    const uint16_t* bbase = B + (size_t)min(s, nk - 1) * BK * ldb + n0;
+#pragma unroll
+    for (int n = 0; n < CF::B_LPW; ++n)
+      dma16(bbase, b_off[n], lds0 + CF::B_OFF + slot * CF::B_B + (wave * CF::B_LPW + n) * 1024);
+  };
+  auto issue_a = [&](int j, int h, int slot) {
+    const uint16_t* abase = A + (size_t)m0 * lda + (size_t)min(j, nka - 1) * CF::BKA;
+#pragma unroll
+    for (int n = h * CF::A_LPW / 2; n < (h + 1) * CF::A_LPW / 2; ++n)
+      dma16(abase, a_off[n], lds0 + slot * CF::A_B + (wave * CF::A_LPW + n) * 1024);
+  };
+
+  // ---- fragment lane addresses: one base per A slot and K half, and per
+  // B slot and column fragment (slots lie past ds_read's 16-bit immediate) ----
+  // A^T (B operand): row am + 16 mf, chunk (4 h + kg) ^ swz(am) (swz is the
+  // same for every mf, 16 rows apart).
+  const int am = wm * CF::TM + (lane & 15);
+  uint32_t a_col[CF::NSA][2];
+#pragma unroll
+  for (int st = 0; st < CF::NSA; ++st)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      a_col[st][h] = lds0 + st * CF::A_B + am * CF::RA + 16 * ((4 * h + kg) ^ swz_a16w(am));
+      asm volatile("" : "+v"(a_col[st][h]));  // keep it a base register
+    }
+  // B^T (A operand): lane (kg, j, a) reads k-rows 8kg + 4r + j, columns
+  // wn*TN + 16 nf + 4a .. +3 (8 bytes of a 16-byte chunk).
+  const int b_j = (lane >> 2) & 3, b_a = lane & 3;
+  const int bk = 8 * kg + b_j;
+  uint32_t b_col[CF::NSB][FN];
+#pragma unroll
+  for (int st = 0; st < CF::NSB; ++st)
+#pragma unroll
+    for (int nf = 0; nf < FN; ++nf) {
+      const int chunk = (wn * CF::TN + 16 * nf + 4 * b_a) >> 3;
+      b_col[st][nf] = lds0 + CF::B_OFF + st * CF::B_B + bk * CF::RB + 16 * (chunk ^ swz_b16(bk)) + 8 * (b_a & 1);
+      asm volatile("" : "+v"(b_col[st][nf]));
+    }
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{};
+
+  u32x4 af[FM];     // A^T fragments of the current tile, refilled in place
+  u32x4 bf[2][FN];  // B^T fragments, double buffered by tile parity
+  auto read_b = [&](int stg, int buf) {
+#pragma unroll
+    for (int nf = 0; nf < FN; ++nf) {
+      const u32x2 lo = lds_read_tr16_at(b_col[stg][nf]);
+      const u32x2 hi = lds_read_tr16_at(b_col[stg][nf] + 4 * CF::RB);
+      bf[buf][nf] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
+  auto read_a = [&](int stg, int h, int mf) { af[mf] = lds_ld128(a_col[stg][h] + 16 * mf * CF::RA); };
+
+  // Step kt = 12q + I: tile kt's fragments are in af and bf[I % 2]; B
+  // stage kt sits in slot I % 4 and A block kt / 2 in slot (I / 2) % 3.
+  auto step = [&](int kt, auto i_tag) {
+    constexpr int I = decltype(i_tag)::value;
+    constexpr int PAR = I % 2;
+    constexpr int NB = (I + 1) % CF::NSB, NA = ((I + 1) / 2) % CF::NSA, NH = (I + 1) % 2;
+    // Every wave has read tile kt (during step kt-1) and its own loads up
+    // to those of step kt-2 have landed, tile kt+1's among them: after the
+    // barrier tile kt+1 is readable, and B stage kt-1 (read during step
+    // kt-2) and A block kt/2 - 1 (its last tile read no later) are free.
+    wait_vmcnt<CF::VM>();
+    lds_barrier();
+    issue_b(kt + 3, (I + 3) % CF::NSB);
+    issue_a(kt / 2 + 2, I % 2, (I / 2 + 2) % CF::NSA);
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(NB, PAR ^ 1);
+#pragma unroll
+    for (int mf = 0; mf < FM; ++mf) {
+#pragma unroll
+      for (int nf = 0; nf < FN; ++nf) acc[mf][nf] = mfma16<BF16>(bf[PAR][nf], af[mf], acc[mf][nf]);
+      read_a(NA, NH, mf);
+    }
+    interleave_rows16<FM, FN>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  land_args(C);  // C is used only after the K loop
+  // Prologue, in the order the waits need: A block 0, B stages 0 and 1,
+  // A block 1, B stage 2; then tile 0's fragments.
+  issue_a(0, 0, 0);
+  issue_a(0, 1, 0);
+  issue_b(0, 0);
+  issue_b(1, 1);
+  issue_a(1, 0, 1);
+  issue_a(1, 1, 1);
+  issue_b(2, 2);
+  wait_vmcnt<2 * CF::B_LPW + CF::A_LPW>();  // B stage 1, A block 1 and B stage 2 may be in flight
+  lds_barrier();
+  read_b(0, 0);
+#pragma unroll
+  for (int mf = 0; mf < FM; ++mf) read_a(0, 0, mf);
+  int kt = 0;
+  for (; kt + CF::P <= nk; kt += CF::P) steps_s<CF::P>(step, kt);
+  steps_tail_s<CF::P>(step, kt, nk - kt);
+  wait_vmcnt<0>();  // no DMA may land in LDS after the workgroup ends
+
+  // ---- epilogue (as gemm_bf16_dma16_kernel): the tile goes through LDS as
+  // bf16 rows padded by 16 bytes and is stored as whole rows. ----
+  constexpr int CROW = CF::BN * 2 + 16;
+  static_assert(CF::BM * CROW <= CF::LDS, "C tile fits the rings");
+  __syncthreads();
+#pragma unroll
+  for (int mf = 0; mf < FM; ++mf) {
+    const int r = am + 16 * mf;
+#pragma unroll
+    for (int nf = 0; nf < FN; ++nf) {
+      const int c = wn * CF::TN + 16 * nf + 4 * kg;
+      const f32x4& a = acc[mf][nf];
+      *reinterpret_cast<u32x2*>(smem + r * CROW + 2 * c) = u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+    }
+  }
+  __syncthreads();
+  {
+    constexpr int CPR = CF::BN / 8;     // 16-byte chunks per tile row
+    constexpr int RPI = CF::NT / CPR;   // rows per workgroup-wide store
+    const int t = threadIdx.x;
+    const int cc = t % CPR, r0 = t / CPR;
+    const int gn = n0 + 8 * cc;
+#pragma unroll 4
+    for (int r = r0; r < CF::BM; r += RPI) {
+      const int gm = m0 + r;
+      if (gm < M && gn < N)
+        st128(C + (size_t)gm * ldc + gn, *reinterpret_cast<const u32x4*>(smem + r * CROW + 16 * cc));
+    }
+  }
+}
+
+static int launch_dma16s(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
+                         hipStream_t stream) {
+  using CF = S16Cfg;
+  const long long tiles = (long long)((M + CF::BM - 1) / CF::BM) * ((N + CF::BN - 1) / CF::BN);
+  if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
+  constexpr auto kern = gemm_bf16_dma16s_kernel;
+  MX_RETURN_IF_HIP(lds_limit_once<kern>(CF::LDS));
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CF::NT), CF::LDS, stream, (const uint16_t*)A,
+                     (const uint16_t*)B, (uint16_t*)C, M, N, K, lda, ldb, ldc);
+  MX_RETURN_IF_HIP(hipGetLastError());
+  return MX_OK;
+}
+
 template <int NS, int WM, int WN, int BM_ = 256, int BN_ = 256>
 static int launch_dma16(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb, int ldc,
                         hipStream_t stream) {
@@ -1268,6 +1520,8 @@ extern "C" int mx_gemm_bf16(const void* A, const void* B, void* C, int M, int N,
   const bool big = tiles256 >= 256 || 13 * r256 < 5 * r128;
   // Whole K tiles: the direct-load kernel (its lane offsets are 32-bit: 256
   // rows of A must span < 4 GiB).
+  if (big && K % 64 == 0 && (long long)lda * 2 * 256 <= 0xffffffffLL && (long long)ldb * 2 * 32 <= 0xffffffffLL)
+    return mx::gemm::launch_dma16s(A, B, C, M, N, K, lda, ldb, ldc, s);
   if (big && K % mx::gemm::DMA_BK == 0 && (long long)lda * 2 * 256 <= 0xffffffffLL)
     return mx::gemm::launch_dma16<mx::gemm::DMA_NS, mx::gemm::DMA_WM, mx::gemm::DMA_WN>(A, B, C, M, N, K, lda, ldb,
                                                                                           ldc, s);

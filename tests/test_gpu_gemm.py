@@ -138,11 +138,14 @@ def test_kat_pattern(ops):
     assert torch.equal(c, want)
 
 
-@pytest.mark.parametrize("mnk", [(4096, 4096, 32), (4096, 4096, 96), (4000, 4040, 4128), (4096, 4352, 2048)])
+@pytest.mark.parametrize("mnk", [(4096, 4096, 32), (4096, 4096, 96), (4000, 4040, 4128), (4096, 4352, 2048),
+                                 (4096, 4096, 64), (4096, 4096, 192), (4000, 4040, 4096), (4096, 4096, 1600)])
 def test_direct_load_path(ops, mnk):
-    """Shapes that take the large-problem kernel (>= 256 tiles of 256x256,
-    K % 32 == 0): a single K tile, fewer K tiles than ring stages, ragged M
-    and N with a K-tile count that is not a multiple of the ring depth."""
+    """Shapes that take the large-problem kernels (>= 256 tiles of 256x256):
+    with K % 64 == 0 the split-ring kernel (whole 128-byte A lines), else
+    the single ring (K % 32 == 0).  A single K tile or A block, fewer K
+    tiles than ring slots, ragged M and N, and K-tile counts that are not a
+    multiple of either ring's period."""
     m, n, k = mnk
     announce(f"gemm_bf16 direct-load {m}x{n}x{k}")
     a, b = inputs.gemm_inputs(shapes.GemmShape("t", m, n, k))
