@@ -35,7 +35,11 @@
 //  * The block scales are read with vector loads issued as inline asm and
 //    waited for by the same vmcnt wait that lands the stages, as operands
 //    of that wait: the compiler tracks neither, so it never inserts a
-//    vmcnt(0) of its own that would drain the ring.
+//    vmcnt(0) of its own that would drain the ring.  When K is a multiple
+//    of 512 the activation scales come four blocks per 8-byte load (the
+//    two half-waves take blocks 4g, 4g+1 and 4g+2, 4g+3 of the rows they
+//    share), once per four blocks: one scale per lane per block made each
+//    block's scale loads touch more cache lines than its A and B tiles.
 //  * A^T fragments are plain ds_read_b128; B^T fragments come from k-major
 //    B rows through gfx950's transposing read ds_read_b64_tr_b8: in each
 //    16-lane group, lane 8h+b receives byte b of the 8-byte rows addressed
@@ -44,6 +48,8 @@
 //    transposes.
 //  * 16-byte chunks are XOR-swizzled per row so every fragment read phase
 //    is bank-conflict free.
+#include <type_traits>
+
 #include "mx_common.h"
 
 namespace mx {
@@ -79,10 +85,42 @@ __device__ __forceinline__ float ld_scale(const float* sbase, uint32_t voff) {
   asm volatile("global_load_dword %0, %1, %2" : "=v"(x) : "v"(voff), "s"(sbase) : "memory");
   return x;
 }
+// Untracked 8-byte scale loads (two consecutive scales each, otherwise as
+// ld_scale) issued only when `go` is nonzero, with the branch inside the
+// statement: the registers are read-write operands, so they keep their
+// values when the loads are skipped and the compiler sees no control flow
+// (a branch around the loads split the registers' live ranges, and the
+// allocator then copied an in-flight one).
+__device__ __forceinline__ void ld_scales_if(u32x2 (&x)[4], const float* sbase, const uint32_t (&voff)[4],
+                                             uint32_t go) {
+  asm volatile(
+      "s_cmp_eq_u32 %[go], 0\n\t"
+      "s_cbranch_scc1 1f\n\t"
+      "global_load_dwordx2 %0, %4, %[b]\n\t"
+      "global_load_dwordx2 %1, %5, %[b]\n\t"
+      "global_load_dwordx2 %2, %6, %[b]\n\t"
+      "global_load_dwordx2 %3, %7, %[b]\n"
+      "1:"
+      : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3])
+      : "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]), [b] "s"(sbase), [go] "s"(go)
+      : "memory", "scc");
+}
+__device__ __forceinline__ void ld_scales_if(u32x2 (&x)[2], const float* sbase, const uint32_t (&voff)[2],
+                                             uint32_t go) {
+  asm volatile(
+      "s_cmp_eq_u32 %[go], 0\n\t"
+      "s_cbranch_scc1 1f\n\t"
+      "global_load_dwordx2 %0, %2, %[b]\n\t"
+      "global_load_dwordx2 %1, %3, %[b]\n"
+      "1:"
+      : "+v"(x[0]), "+v"(x[1])
+      : "v"(voff[0]), "v"(voff[1]), [b] "s"(sbase), [go] "s"(go)
+      : "memory", "scc");
+}
 // s_waitcnt vmcnt(N) that also lands the untracked scale loads: the scale
 // registers are operands, so no read of them is scheduled before it.
-template <int N, int FM>
-__device__ __forceinline__ void wait_scales(float (&sa)[FM], float& sb) {
+template <int N, typename S, int FM>
+__device__ __forceinline__ void wait_scales(S (&sa)[FM], float& sb) {
   static_assert(N >= 0 && N < 16, "vmcnt immediate");
   static_assert(FM == 2 || FM == 4, "scale registers");
   if constexpr (FM == 4)
@@ -123,7 +161,9 @@ __device__ __forceinline__ int swz_b(int k) {
   return BN == 256 ? ((k & 7) << 1) : (((k >> 1) & 3) << 1);
 }
 
-template <int BM, int BN>
+// GS (K a multiple of 512): the activation scales are loaded four blocks
+// at a time (see load_sa), else one block at a time.
+template <int BM, int BN, bool GS>
 __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __restrict__ A,
                                                            const float* __restrict__ sA,
                                                            const uint8_t* __restrict__ B,
@@ -217,17 +257,40 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
 
   // Block scales: the sA row of this lane per m fragment, the sB of this
-  // wave's 128-column block (wave-uniform, read by every lane).
+  // wave's 128-column block (wave-uniform, read by every lane).  A wave's
+  // 32 rows per m fragment lie 4 K/128 bytes apart, so a load of one scale
+  // per lane touches 32 cache lines for 128 useful bytes; per block that
+  // was more L1 lookups than the block's A and B tiles.  With GS the two
+  // half-waves (lanes l and l + 32 share a row) load blocks 4g, 4g+1 and
+  // 4g+2, 4g+3 of their row with one 8-byte load, once per four blocks,
+  // and a v_permlane32_swap hands each lane the scale of the current block.
   uint32_t sa_off[FM];
 #pragma unroll
-  for (int mf = 0; mf < FM; ++mf) sa_off[mf] = (uint32_t)min(m0 + am + 32 * mf, M - 1) * (uint32_t)kblocks * 4u;
+  for (int mf = 0; mf < FM; ++mf)
+    sa_off[mf] = (uint32_t)min(m0 + am + 32 * mf, M - 1) * (uint32_t)kblocks * 4u + (GS ? 8u * (lane >> 5) : 0u);
   const uint32_t sb_off = (uint32_t)min((n0 + wn * CF::TN) / 128, nblocks_n - 1) * 4u;
-  float sa_n[FM], sb_n;
-  auto load_scales = [&](int j) {
-    const int jb = min(j, kblocks - 1);
-    sb_n = ld_scale(sB + (size_t)jb * nblocks_n, sb_off);
+  std::conditional_t<GS, u32x2, float> sa_n[FM];
+  float sb_n;
+  auto load_sb = [&](int j) { sb_n = ld_scale(sB + (size_t)min(j, kblocks - 1) * nblocks_n, sb_off); };
+  auto load_sa = [&](int j) {  // GS: at j = 4g - 1, group g (blocks 4g .. 4g+3)
+    if constexpr (GS) {
+      ld_scales_if(sa_n, sA + min(j + 1, kblocks - 4), sa_off, (uint32_t)(((j & 3) + 1) >> 2));  // 1 at j % 4 == 3
+    } else {
+      const int jb = min(j, kblocks - 1);
 #pragma unroll
-    for (int mf = 0; mf < FM; ++mf) sa_n[mf] = ld_scale(sA + jb, sa_off[mf]);
+      for (int mf = 0; mf < FM; ++mf) sa_n[mf] = ld_scale(sA + jb, sa_off[mf]);
+    }
+  };
+  // The activation scale of block 4g + t (GS; else of the loaded block)
+  // for this lane's row in m fragment mf.
+  auto sa_of = [&](int t, int mf) {
+    if constexpr (GS) {
+      const uint32_t v = (t & 1) ? sa_n[mf][1] : sa_n[mf][0];
+      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return __uint_as_float(t < 2 ? r[0] : r[1]);  // r[0]: lanes 0-31's value, r[1]: lanes 32-63's
+    } else {
+      return sa_n[mf];
+    }
   };
 
   auto read_b = [&](uint32_t so, int nf) {
@@ -249,7 +312,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   // Prologue, in the order the block waits need: the scales of block 0,
   // A block 0, B stages 0 and 1, then A block 1 (which may still be in
   // flight when block 0 starts).
-  load_scales(0);
+  load_sb(0);
+  load_sa(GS ? -1 : 0);  // GS: group 0 (blocks 0 .. 3)
 #pragma unroll
   for (int n = 0; n < CF::A_LPW; ++n) issue_a(0, n);
 #pragma unroll
@@ -272,8 +336,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
     lds_barrier();
     float s_m[FM];
 #pragma unroll
-    for (int mf = 0; mf < FM; ++mf) s_m[mf] = sa_n[mf] * sb_n;
-    load_scales(j + 1);
+    for (int mf = 0; mf < FM; ++mf) s_m[mf] = sa_of(j & 3, mf) * sb_n;
+    // the next block's scales, issued before the block's tile loads so the
+    // next block's wait lands them (GS: the next group's, once per group)
+    load_sb(j + 1);
+    if constexpr (GS) load_sa(j);
+    else load_sa(j + 1);
     const uint32_t ao = (j % NSA) * CF::A_S;
     const uint32_t so0 = ((2 * j) % NSB) * CF::B_S, so1 = ((2 * j + 1) % NSB) * CF::B_S;
 
@@ -377,14 +445,14 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_bs_kernel(const uint8_t* __res
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool GS>
 static int launch(const void* A, const float* sA, const void* B, const float* sB, void* C, int M, int N, int K,
                   hipStream_t stream) {
   using CF = Cfg<BM, BN>;
   const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7fffffffLL) return MX_ERR_SHAPE;
   const size_t smem = CF::LDS;
-  constexpr auto kern = gemm_fp8_bs_kernel<BM, BN>;
+  constexpr auto kern = gemm_fp8_bs_kernel<BM, BN, GS>;
   MX_RETURN_IF_HIP(lds_limit_once<kern>((int)smem));
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NT), smem, stream, (const uint8_t*)A, sA, (const uint8_t*)B,
                      sB, (uint16_t*)C, M, N, K);
@@ -655,6 +723,11 @@ extern "C" int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, con
   if (M <= 64 || (tiles128s <= 64 && M <= 512))
     return mx::gemm8::launch_smallm<2, SMALLM_NW, 3>(A, sA, B, sB, C, M, N, K, s);
   const long long r256 = (tiles256 + 255) / 256, r128 = (tiles128 + 255) / 256;
-  if (tiles256 >= 256 || 12 * r256 < 5 * r128) return mx::gemm8::launch<256, 256>(A, sA, B, sB, C, M, N, K, s);
-  return mx::gemm8::launch<128, 128>(A, sA, B, sB, C, M, N, K, s);
+  const bool big = tiles256 >= 256 || 12 * r256 < 5 * r128;
+  // activation scales four blocks per load when the blocks come in fours
+  if (K % 512 == 0)
+    return big ? mx::gemm8::launch<256, 256, true>(A, sA, B, sB, C, M, N, K, s)
+               : mx::gemm8::launch<128, 128, true>(A, sA, B, sB, C, M, N, K, s);
+  return big ? mx::gemm8::launch<256, 256, false>(A, sA, B, sB, C, M, N, K, s)
+             : mx::gemm8::launch<128, 128, false>(A, sA, B, sB, C, M, N, K, s);
 }
