@@ -425,7 +425,7 @@ def _gemm_bf16(c: Ctx, shape, name: str) -> dict:
     ms, wall = time_graph(lambda: c.ops.gemm_bf16(ad, bd, out=out), c.steps, c.warmup)
     flops = c.F.gemm_flops(shape)
     wl = f"gemm_bf16 M{shape.m} N{shape.n} K{shape.k} U[-1,1]"
-    kernel = ("gemm_bf16_dma16_kernel<5, 2, 4, 256, 256>" if shape.m >= 4096
+    kernel = ("gemm_bf16_dma16s_kernel (256x256 tiles, A and B rings)" if shape.m >= 4096
               else "gemm_bf16_sdma_kernel (64x64 tiles, K split between two wave groups)")
     rec = {"workload": wl, "unit": "TFLOPS", "mean_ms": ms, "wall_ms": wall, "value": c.F.tflops(flops, ms),
            "roofline": roofline("mfma", flops, ms, c.F.PEAK_BF16_TFLOPS, "TFLOP/s", wl, kernel)}
