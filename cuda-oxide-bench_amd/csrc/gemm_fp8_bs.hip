@@ -724,8 +724,9 @@ extern "C" int mx_gemm_fp8_bs(const void* A, const float* sA, const void* B, con
     return mx::gemm8::launch_smallm<2, SMALLM_NW, 3>(A, sA, B, sB, C, M, N, K, s);
   const long long r256 = (tiles256 + 255) / 256, r128 = (tiles128 + 255) / 256;
   const bool big = tiles256 >= 256 || 12 * r256 < 5 * r128;
-  // activation scales four blocks per load when the blocks come in fours
-  if (K % 512 == 0)
+  // activation scales four blocks per 8-byte load when the blocks come in
+  // fours and sA is 8-byte aligned (the interface asks only for 4)
+  if (K % 512 == 0 && ((uintptr_t)sA & 7) == 0)
     return big ? mx::gemm8::launch<256, 256, true>(A, sA, B, sB, C, M, N, K, s)
                : mx::gemm8::launch<128, 128, true>(A, sA, B, sB, C, M, N, K, s);
   return big ? mx::gemm8::launch<256, 256, false>(A, sA, B, sB, C, M, N, K, s)

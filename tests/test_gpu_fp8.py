@@ -87,6 +87,30 @@ def test_large_tile_path(ops, mnk):
     assert err <= TOL, f"normwise rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("mnk", [(4096, 4096, 512), (2048, 2048, 1024)])
+def test_scale_alignment(ops, mnk):
+    """With K a multiple of 512 the kernels read the activation scales four
+    blocks per 8-byte load when sA is 8-byte aligned; the interface asks
+    only for 4-byte alignment, and an sA 4 bytes off an 8-byte boundary
+    takes the one-scale-per-load path.  Both give the same bits."""
+    m, n, k = mnk
+    announce(f"fp8 sA alignment {m}x{n}x{k}")
+    a8, sa, b8, sb = inputs.fp8_gemm_inputs(shapes.FP8GemmShape("t", m, n, k))
+    ad, bd, sbd = a8.cuda(), b8.cuda(), sb.cuda()
+    sa_aligned = sa.cuda()
+    buf = torch.empty(sa.numel() + 1, dtype=torch.float32, device="cuda")
+    sa_off = buf[1:].view(sa.shape)
+    sa_off.copy_(sa_aligned)
+    assert sa_aligned.data_ptr() % 8 == 0 and sa_off.data_ptr() % 8 == 4
+    c_aligned = ops.gemm_fp8_bs(ad, sa_aligned, bd, sbd)
+    c_off = ops.gemm_fp8_bs(ad, sa_off, bd, sbd)
+    torch.cuda.synchronize()
+    assert torch.equal(c_aligned.view(torch.int16), c_off.view(torch.int16))
+    ref = ofp8.gemm_fp8_bs_ref_torch(a8, sa, b8, sb)
+    err = normwise_rel_err(c_off.cpu(), ref)
+    assert err <= TOL, f"normwise rel err {err:.3e}"
+
+
 def test_bit_exact_kat(ops):
     """Operands that are multiples of 1/16 in [0, 0.9375] with unit scales: the
     fp32 sums are exact, so the bf16 output equals the bf16 rounding of the
