@@ -13,6 +13,7 @@ import pytest
 from conftest import REPO_ROOT, announce
 
 RUN_PY = REPO_ROOT / "cuda-oxide-bench_amd" / "microbench" / "run.py"
+ABLATE_PY = REPO_ROOT / "cuda-oxide-bench_amd" / "microbench" / "ablate.py"
 
 
 @pytest.fixture(scope="module")
@@ -47,6 +48,20 @@ def test_probe_library_exports_its_launchers(runner):
     assert lib.mxp_stream_launch(2, 8, p, 0, 64, 1, p, None) == -1    # no such mode
     assert lib.mxp_stream_launch(1, 8, p, 0, 100, 1, p, None) == -1   # LDS copies take whole 1 KB chunks
     assert lib.mxp_stream_launch(1, 8, p, 0, 64, 0, p, None) == -1
+
+
+def test_ablation_patches_apply():
+    """Every ablation variant's text patches still match the kernel source
+    exactly once (the tool refuses to build otherwise), and each variant
+    changes the source (CPU only; the build and the GPU run are the tool's)."""
+    spec = importlib.util.spec_from_file_location("mx_microbench_ablate", ABLATE_PY)
+    ab = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(ab)
+    for kernel, k in ab.KERNELS.items():
+        base = (REPO_ROOT / "cuda-oxide-bench_amd" / "csrc" / k["source"]).read_text()
+        for v, (_, parts) in k["variants"].items():
+            text = ab.patched_source(kernel, v)
+            assert (text == base) == (not parts), f"{kernel}/{v}"
 
 
 @pytest.mark.gpu
