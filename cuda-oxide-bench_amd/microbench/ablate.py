@@ -20,7 +20,10 @@ calls, one graph of 20 launches, replayed after 300 ms of a device GEMM);
 the variants take turns, --runs times.  The variants compute wrong results,
 which is the point, so nothing checks their output; every variant keeps
 every memory access in bounds and every wait count exact, as its
-description says.
+description says, and issues the MFMAs of the kernel as built (a variant
+whose operands became equal could let the compiler merge MFMAs and time
+less work: the register-operand GQA variant feeds its two key halves from
+different registers for that reason).
 """
 from __future__ import annotations
 
@@ -91,10 +94,63 @@ FP8_VARIANTS = {
                            ["promotion", "act_scales", "tile_loads", "barrier"]),
 }
 
+# ---------------------------------------------------------------------------
+# Causal GQA forward (csrc/gqa_fwd.hip): B1 Hq32 Hkv8
+# S4096 D128 bf16, default tile.  Only the default kernel is launched.
+# ---------------------------------------------------------------------------
+GQA_PARTS = {
+    # Scores go to P as they are (no v_exp_f32); every other instruction,
+    # access and wait unchanged.
+    "exp2": [
+        ("        for (int e = 0; e < 8; ++e) s[qt][0][e] = __builtin_amdgcn_exp2f(s[qt][0][e]);\n",
+         "        for (int e = 0; e < 8; ++e) (void)s[qt][0][e];\n"),
+        ("            for (int e = 0; e < 8; ++e) s[qt][t1][j1 + e] = __builtin_amdgcn_exp2f(s[qt][t1][j1 + e]);\n",
+         "            for (int e = 0; e < 8; ++e) (void)s[qt][t1][j1 + e];\n"),
+    ],
+    # K and V fragments come from registers (the wave's Q fragments) instead
+    # of LDS reads.  The MFMAs still chain on loop-carried accumulators, and
+    # the two key halves take different registers so that the compiler does
+    # not merge their (then identical) score chains.
+    "lds_reads": [
+        ("        return lds_ld128(koff[dc] + st + t * 32 * L::ROWK);",
+         "        (void)st; return qf[0][(dc + t) % DC];"),
+        ("        const uint32_t vb = v_off[dt] + st + (16 * c) * L::ROWV;\n"
+         "        const u32x2 lo = lds_read_tr16_at(vb);\n"
+         "        const u32x2 hi = lds_read_tr16_at(vb + 8 * L::ROWV);\n"
+         "        return u32x4{lo[0], lo[1], hi[0], hi[1]};",
+         "        (void)c; return qf[0][dt];"),
+    ],
+    # Only key tile 0 is loaded (each query block's first); later tiles read
+    # the stages as they are (in bounds).  Every tile still waits for all of
+    # its wave's loads (vmcnt(0)).
+    "kv_loads": [
+        ("  auto issue_part = [&](int blk, int n) {\n", "  auto issue_part = [&](int blk, int n) {\n    if (blk >= 1) return;\n"),
+        ("  auto issue = [&](int blk) {\n", "  auto issue = [&](int blk) {\n    if (blk >= 1) return;\n"),
+    ],
+    # No barrier per key tile: waves may read a stage another wave's loads
+    # are overwriting (wrong values, in bounds).
+    "barrier": [
+        ("    __syncthreads();\n    // the next tile's loads go out one per k step",
+         "    // the next tile's loads go out one per k step"),
+    ],
+}
+GQA_VARIANTS = {
+    "as_built": ("the kernel as built", []),
+    "no_exp2": ("without exp2 (scores passed through)", ["exp2"]),
+    "no_lds_reads": ("without the K and V fragment reads (register operands)", ["lds_reads"]),
+    "no_exp2_lds_reads": ("without both", ["exp2", "lds_reads"]),
+    "no_exp2_lds_reads_kv_loads": ("... and without the K/V loads after the first tile", ["exp2", "lds_reads", "kv_loads"]),
+    "no_exp2_lds_reads_kv_loads_barrier": ("... and without the per-tile barrier",
+                                           ["exp2", "lds_reads", "kv_loads", "barrier"]),
+}
+
 KERNELS = {
     "fp8": {"source": "gemm_fp8_bs.hip", "parts": FP8_PARTS, "variants": FP8_VARIANTS,
             "workload": "gemm_fp8_bs M8192 N8192 K8192 e4m3 1x128/128x128 scales",
             "kernel_prefix": "_ZN2mx5gemm818gemm_fp8_bs_kernel"},
+    "gqa": {"source": "gqa_fwd.hip", "parts": GQA_PARTS, "variants": GQA_VARIANTS,
+            "workload": "gqa_fwd causal B1 Hq32 Hkv8 S4096 D128 bf16, default tile",
+            "kernel_prefix": "_ZN2mx3gqa14gqa_fwd_kernel"},
 }
 
 
@@ -174,11 +230,20 @@ def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 3
     sys.path.insert(0, str(REPO_ROOT))
     pkg = importlib.import_module("cuda-oxide-bench_amd")
     ops = pkg.load_ops()
-    if kernel != "fp8":
+    if kernel == "fp8":
+        a8, sa, b8, sb = (t.cuda() for t in
+                          pkg.inputs.fp8_gemm_inputs(pkg.shapes.FP8GemmShape("t", 8192, 8192, 8192)))
+        out = torch.empty((8192, 8192), dtype=torch.bfloat16, device="cuda")
+        fn = lambda: ops.gemm_fp8_bs(a8, sa, b8, sb, out=out)  # noqa: E731
+    elif kernel == "gqa":
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        q = torch.randn((1, 32, 4096, 128), device="cuda", generator=gen).to(torch.bfloat16)
+        k = torch.randn((1, 8, 4096, 128), device="cuda", generator=gen).to(torch.bfloat16)
+        v = torch.randn((1, 8, 4096, 128), device="cuda", generator=gen).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        fn = lambda: ops.gqa_fwd(q, k, v, causal=True, out=out)  # noqa: E731
+    else:
         raise ValueError(kernel)
-    a8, sa, b8, sb = (t.cuda() for t in pkg.inputs.fp8_gemm_inputs(pkg.shapes.FP8GemmShape("t", 8192, 8192, 8192)))
-    out = torch.empty((8192, 8192), dtype=torch.bfloat16, device="cuda")
-    fn = lambda: ops.gemm_fp8_bs(a8, sa, b8, sb, out=out)  # noqa: E731
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
