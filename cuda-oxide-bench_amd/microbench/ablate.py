@@ -144,6 +144,49 @@ GQA_VARIANTS = {
                                            ["exp2", "lds_reads", "kv_loads", "barrier"]),
 }
 
+# ---------------------------------------------------------------------------
+# Absorbed MLA decode (csrc/mla_decode.hip): B32 H128
+# T4096, 576/512 bf16, the same buffers every launch; each launch is the
+# decode kernel and the split merge.
+# ---------------------------------------------------------------------------
+MLA_PARTS = {
+    # Every stage loads the split's first two stages' cache rows again, so
+    # the cache reads after the first two stages come from L2, not HBM.
+    # Same loads, slots and waits.
+    "l2_loads": [
+        ("    issue_part(kvb, t0 + i * BT, t1, lds0", "    issue_part(kvb, t0 + (i & 1) * BT, t1, lds0"),
+    ],
+    # No direct loads inside the stage loop: the prologue's stages 0 and 1
+    # are the only ones loaded, later stages read their slots as they are (in
+    # bounds).  The kernel has no untracked register loads, so the waits
+    # (now waiting for less) cannot leave a register in flight.
+    "loop_loads": [
+        ("  scores_alone(0, nblk > 2 ? 2 : -1);", "  scores_alone(0, -1);"),
+        ("    f32x16 sc = score_mfma(i, i + 2 < nblk ? i + 2 : -1);", "    f32x16 sc = score_mfma(i, -1);"),
+    ],
+    # P = s * scale - m instead of exp2 of it (no v_exp_f32).
+    "exp2": [
+        ("    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(sc[8 * k2 + e], sl2, -m_run));",
+         "    for (int e = 0; e < 8; ++e) p[e] = fmaf(sc[8 * k2 + e], sl2, -m_run);"),
+    ],
+    # No partial-output stores at the end of a split (the merge then reads
+    # the workspace as it is, in bounds).  The single-split store path that
+    # keeps the accumulators live is unchanged.
+    "partial_stores": [
+        ("          st64(po + (slot * 64 + lane) * 2, u32x2{pack_bf16x2(a[4 * i] * inv, a[4 * i + 1] * inv),\n"
+         "                                                  pack_bf16x2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)});",
+         "          (void)po; (void)slot; (void)a; (void)inv;"),
+    ],
+}
+MLA_VARIANTS = {
+    "as_built": ("the decode and merge as built", []),
+    "l2_loads": ("every stage's cache rows from L2 (all stages reload the split's first 64 tokens)", ["l2_loads"]),
+    "no_loop_loads": ("without the direct loads inside the stage loop (stages past the first two read stale "
+                      "slots)", ["loop_loads"]),
+    "no_exp2": ("without exp2 (P = scaled score minus the running max)", ["exp2"]),
+    "no_partial_stores": ("without the partial-output stores at the end of each split", ["partial_stores"]),
+}
+
 KERNELS = {
     "fp8": {"source": "gemm_fp8_bs.hip", "parts": FP8_PARTS, "variants": FP8_VARIANTS,
             "workload": "gemm_fp8_bs M8192 N8192 K8192 e4m3 1x128/128x128 scales",
@@ -151,6 +194,9 @@ KERNELS = {
     "gqa": {"source": "gqa_fwd.hip", "parts": GQA_PARTS, "variants": GQA_VARIANTS,
             "workload": "gqa_fwd causal B1 Hq32 Hkv8 S4096 D128 bf16, default tile",
             "kernel_prefix": "_ZN2mx3gqa14gqa_fwd_kernel"},
+    "mla": {"source": "mla_decode.hip", "parts": MLA_PARTS, "variants": MLA_VARIANTS,
+            "workload": "mla_decode absorbed B32 H128 T4096 576/512 bf16, decode + merge, same buffers",
+            "kernel_prefix": "_ZN2mx3mla17mla_decode_kernel"},
 }
 
 
@@ -242,6 +288,13 @@ def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 3
         v = torch.randn((1, 8, 4096, 128), device="cuda", generator=gen).to(torch.bfloat16)
         out = torch.empty_like(q)
         fn = lambda: ops.gqa_fwd(q, k, v, causal=True, out=out)  # noqa: E731
+    elif kernel == "mla":
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        q = torch.randn((32, 128, 576), device="cuda", generator=gen).to(torch.bfloat16)
+        kv = torch.randn((32, 4096, 576), device="cuda", generator=gen).to(torch.bfloat16)
+        out = torch.empty((32, 128, 512), dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(max(1, ops.mla_decode_workspace_bytes(32, 128, 4096)), dtype=torch.uint8, device="cuda")
+        fn = lambda: ops.mla_decode(q, kv, 192 ** -0.5, out=out, workspace=ws)  # noqa: E731
     else:
         raise ValueError(kernel)
     for _ in range(warmup):
