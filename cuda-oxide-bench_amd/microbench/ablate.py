@@ -20,10 +20,11 @@ calls, one graph of 20 launches, replayed after 300 ms of a device GEMM);
 the variants take turns, --runs times.  The variants compute wrong results,
 which is the point, so nothing checks their output; every variant keeps
 every memory access in bounds and every wait count exact, as its
-description says, and issues the MFMAs of the kernel as built (a variant
-whose operands became equal could let the compiler merge MFMAs and time
-less work: the register-operand GQA variant feeds its two key halves from
-different registers for that reason).
+description says.  Unless its description says it removes them, a variant
+issues the MFMAs of the kernel as built (a variant whose operands became
+equal could let the compiler merge MFMAs and time less work: the
+register-operand GQA variant feeds its two key halves from different
+registers for that reason).
 """
 from __future__ import annotations
 
@@ -187,6 +188,45 @@ MLA_VARIANTS = {
     "no_partial_stores": ("without the partial-output stores at the end of each split", ["partial_stores"]),
 }
 
+# ---------------------------------------------------------------------------
+# bf16 GEMM 1024^3 (csrc/gemm_bf16.hip, gemm_bf16_sdma_kernel), BASELINE
+# what a launch of about one 64x64 tile per CU spends its time
+# on.  These variants remove work on purpose (MFMAs included).
+# ---------------------------------------------------------------------------
+BF16_PARTS = {
+    # No MFMAs and no fragment reads: the accumulators stay zero.
+    "mfma_reads": [
+        ("    compute(kt % CF::NSL);\n", "    (void)compute;\n"),
+    ],
+    # No tile loads at all (prologue and loop): the slots are read as they
+    # are (in bounds); the kernel has no untracked register loads.
+    "loads": [
+        ("  for (int p = 0; p < CF::NSL - 1; ++p) issue(min(p, nk - 1), p);\n",
+         "  for (int p = 0; p < CF::NSL - 1; ++p) (void)p;\n"),
+        ("    issue(min(kt + CF::NSL - 1, nk - 1), (kt + CF::NSL - 1) % CF::NSL);\n", "    (void)issue;\n"),
+    ],
+    # No C stores (the reduction of the two K groups through LDS stays).
+    "stores": [
+        ("    st64(crow + 8 * i, u32x2{pack_bf16x2(acc[4 * i], acc[4 * i + 1]), "
+         "pack_bf16x2(acc[4 * i + 2], acc[4 * i + 3])});",
+         "    (void)crow;"),
+    ],
+    # Every workgroup returns at once.
+    "all": [
+        ("  using CF = SCfg;\n  extern __shared__ __align__(1024) unsigned char smem[];\n  const int lane = threadIdx.x & 63;\n",
+         "  using CF = SCfg;\n  if (M > 0) return;\n  extern __shared__ __align__(1024) unsigned char smem[];\n"
+         "  const int lane = threadIdx.x & 63;\n"),
+    ],
+}
+BF16_VARIANTS = {
+    "as_built": ("the kernel as built", []),
+    "no_mfma_reads": ("without the MFMAs and their fragment reads", ["mfma_reads"]),
+    "no_loads": ("without the tile loads", ["loads"]),
+    "no_mfma_reads_loads": ("without both", ["mfma_reads", "loads"]),
+    "no_mfma_reads_loads_stores": ("... and without the C stores", ["mfma_reads", "loads", "stores"]),
+    "return_at_once": ("every workgroup returning at once", ["all"]),
+}
+
 KERNELS = {
     "fp8": {"source": "gemm_fp8_bs.hip", "parts": FP8_PARTS, "variants": FP8_VARIANTS,
             "workload": "gemm_fp8_bs M8192 N8192 K8192 e4m3 1x128/128x128 scales",
@@ -194,6 +234,9 @@ KERNELS = {
     "gqa": {"source": "gqa_fwd.hip", "parts": GQA_PARTS, "variants": GQA_VARIANTS,
             "workload": "gqa_fwd causal B1 Hq32 Hkv8 S4096 D128 bf16, default tile",
             "kernel_prefix": "_ZN2mx3gqa14gqa_fwd_kernel"},
+    "bf16_1024": {"source": "gemm_bf16.hip", "parts": BF16_PARTS, "variants": BF16_VARIANTS,
+                  "workload": "gemm_bf16 M1024 N1024 K1024 U[-1,1] (gemm_bf16_sdma_kernel)",
+                  "kernel_prefix": "_ZN2mx4gemm21gemm_bf16_sdma_kernel"},
     "mla": {"source": "mla_decode.hip", "parts": MLA_PARTS, "variants": MLA_VARIANTS,
             "workload": "mla_decode absorbed B32 H128 T4096 576/512 bf16, decode + merge, same buffers",
             "kernel_prefix": "_ZN2mx3mla17mla_decode_kernel"},
@@ -288,6 +331,11 @@ def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 3
         v = torch.randn((1, 8, 4096, 128), device="cuda", generator=gen).to(torch.bfloat16)
         out = torch.empty_like(q)
         fn = lambda: ops.gqa_fwd(q, k, v, causal=True, out=out)  # noqa: E731
+    elif kernel == "bf16_1024":
+        a = (torch.rand((1024, 1024), device="cuda") * 2 - 1).to(torch.bfloat16)
+        b = (torch.rand((1024, 1024), device="cuda") * 2 - 1).to(torch.bfloat16)
+        out = torch.empty((1024, 1024), dtype=torch.bfloat16, device="cuda")
+        fn = lambda: ops.gemm_bf16(a, b, out=out)  # noqa: E731
     elif kernel == "mla":
         gen = torch.Generator(device="cuda").manual_seed(0)
         q = torch.randn((32, 128, 576), device="cuda", generator=gen).to(torch.bfloat16)
@@ -346,7 +394,8 @@ def run_variants(kernel: str, variants: list[str], runs: int) -> str:
     lines = [f"| variant ({spec['workload']}) | µs per launch, run by run | min–max |", "|---|---|---:|"]
     for v in variants:
         t = res[v]
-        lines.append(f"| {spec['variants'][v][0]} | {', '.join(f'{x:.1f}' for x in t)} | {min(t):.0f}–{max(t):.0f} |")
+        d = 1 if max(t) < 100 else 0  # decimals of the range
+        lines.append(f"| {spec['variants'][v][0]} | {', '.join(f'{x:.1f}' for x in t)} | {min(t):.{d}f}–{max(t):.{d}f} |")
     return "\n".join(lines)
 
 
