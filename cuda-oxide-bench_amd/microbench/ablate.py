@@ -81,6 +81,100 @@ FP8_PARTS = {
     "barrier": [
         ("    lds_barrier();\n    float s_m[FM];\n", "    float s_m[FM];\n"),
     ],
+    # ---- alternative designs (each computes what the kernel as built does) ----
+    # Order of a block's tile loads (the A block stays last, so the waits
+    # stay exact).  As built: spread evenly over the four row blocks.
+    "loads_b_first": [('    auto dma_share = [&](int mf) {\n#pragma unroll\n      for (int n = (NLD * mf) / FM; n < (NLD * (mf + 1)) / FM; ++n) {\n        if (n < 2 * CF::B_LPW)\n          issue_b(2 * j + 2 + n / CF::B_LPW, n % CF::B_LPW);\n        else\n          issue_a(j + 2, n - 2 * CF::B_LPW);\n      }\n    };\n', '    auto dma_share = [&](int mf) {\n      if (mf == 0) {\n#pragma unroll\n        for (int n = 0; n < 2 * CF::B_LPW; ++n) issue_b(2 * j + 2 + n / CF::B_LPW, n % CF::B_LPW);\n      } else {\n#pragma unroll\n        for (int n = (CF::A_LPW * (mf - 1)) / (FM - 1); n < (CF::A_LPW * mf) / (FM - 1); ++n) issue_a(j + 2, n);\n      }\n    };\n')],
+    "loads_after_barrier": [('    auto dma_share = [&](int mf) {\n#pragma unroll\n      for (int n = (NLD * mf) / FM; n < (NLD * (mf + 1)) / FM; ++n) {\n        if (n < 2 * CF::B_LPW)\n          issue_b(2 * j + 2 + n / CF::B_LPW, n % CF::B_LPW);\n        else\n          issue_a(j + 2, n - 2 * CF::B_LPW);\n      }\n    };\n', '    auto dma_share = [&](int mf) { (void)mf; };\n#pragma unroll\n    for (int n = 0; n < NLD; ++n) {\n      if (n < 2 * CF::B_LPW)\n        issue_b(2 * j + 2 + n / CF::B_LPW, n % CF::B_LPW);\n      else\n        issue_a(j + 2, n - 2 * CF::B_LPW);\n    }\n')],
+    "b_loads_after_barrier": [('    auto dma_share = [&](int mf) {\n#pragma unroll\n      for (int n = (NLD * mf) / FM; n < (NLD * (mf + 1)) / FM; ++n) {\n        if (n < 2 * CF::B_LPW)\n          issue_b(2 * j + 2 + n / CF::B_LPW, n % CF::B_LPW);\n        else\n          issue_a(j + 2, n - 2 * CF::B_LPW);\n      }\n    };\n', '    auto dma_share = [&](int mf) {\n#pragma unroll\n      for (int n = (CF::A_LPW * mf) / FM; n < (CF::A_LPW * (mf + 1)) / FM; ++n) issue_a(j + 2, n);\n    };\n#pragma unroll\n    for (int n = 0; n < 2 * CF::B_LPW; ++n) issue_b(2 * j + 2 + n / CF::B_LPW, n % CF::B_LPW);\n')],
+    # Activation scales eight blocks per 16-byte load when K % 1024 == 0
+    # and sA is 16-byte aligned (four per 8-byte load otherwise, as built).
+    "act_scales_8": [
+        ("__device__ __forceinline__ void ld_scales_if(u32x2 (&x)[2], const float* sbase, const uint32_t (&voff)[2],\n",
+         "__device__ __forceinline__ void ld_scales_if(u32x4 (&x)[4], const float* sbase, const uint32_t (&voff)[4],\n"
+         "                                             uint32_t go) {\n"
+         "  asm volatile(\n"
+         "      \"s_cmp_eq_u32 %[go], 0\\n\\t\"\n"
+         "      \"s_cbranch_scc1 1f\\n\\t\"\n"
+         "      \"global_load_dwordx4 %0, %4, %[b]\\n\\t\"\n"
+         "      \"global_load_dwordx4 %1, %5, %[b]\\n\\t\"\n"
+         "      \"global_load_dwordx4 %2, %6, %[b]\\n\\t\"\n"
+         "      \"global_load_dwordx4 %3, %7, %[b]\\n\"\n"
+         "      \"1:\"\n"
+         "      : \"+v\"(x[0]), \"+v\"(x[1]), \"+v\"(x[2]), \"+v\"(x[3])\n"
+         "      : \"v\"(voff[0]), \"v\"(voff[1]), \"v\"(voff[2]), \"v\"(voff[3]), [b] \"s\"(sbase), [go] \"s\"(go)\n"
+         "      : \"memory\", \"scc\");\n"
+         "}\n"
+         "__device__ __forceinline__ void ld_scales_if(u32x4 (&x)[2], const float* sbase, const uint32_t (&voff)[2],\n"
+         "                                             uint32_t go) {\n"
+         "  asm volatile(\n"
+         "      \"s_cmp_eq_u32 %[go], 0\\n\\t\"\n"
+         "      \"s_cbranch_scc1 1f\\n\\t\"\n"
+         "      \"global_load_dwordx4 %0, %2, %[b]\\n\\t\"\n"
+         "      \"global_load_dwordx4 %1, %3, %[b]\\n\"\n"
+         "      \"1:\"\n"
+         "      : \"+v\"(x[0]), \"+v\"(x[1])\n"
+         "      : \"v\"(voff[0]), \"v\"(voff[1]), [b] \"s\"(sbase), [go] \"s\"(go)\n"
+         "      : \"memory\", \"scc\");\n"
+         "}\n"
+         "__device__ __forceinline__ void ld_scales_if(u32x2 (&x)[2], const float* sbase, const uint32_t (&voff)[2],\n"),
+        ("template <int BM, int BN, bool GS>\n__global__", "template <int BM, int BN, int G>\n__global__"),
+        ("* (uint32_t)kblocks * 4u + (GS ? 8u * (lane >> 5) : 0u);",
+         "* (uint32_t)kblocks * 4u + (G > 1 ? 2u * G * (uint32_t)(lane >> 5) : 0u);"),
+        ("  std::conditional_t<GS, u32x2, float> sa_n[FM];",
+         "  constexpr bool GS = G > 1;\n  constexpr int LG = G == 8 ? 3 : G == 4 ? 2 : 0;\n"
+         "  std::conditional_t<G == 8, u32x4, std::conditional_t<G == 4, u32x2, float>> sa_n[FM];"),
+        ("      ld_scales_if(sa_n, sA + min(j + 1, kblocks - 4), sa_off, (uint32_t)(((j & 3) + 1) >> 2));",
+         "      ld_scales_if(sa_n, sA + min(j + 1, kblocks - G), sa_off, (uint32_t)(((j & (G - 1)) + 1) >> LG));"),
+        ("    if constexpr (GS) {\n      const uint32_t v = (t & 1) ? sa_n[mf][1] : sa_n[mf][0];",
+         "    if constexpr (G == 8) {\n      const uint32_t v01 = (t & 1) ? sa_n[mf][1] : sa_n[mf][0];\n"
+         "      const uint32_t v23 = (t & 1) ? sa_n[mf][3] : sa_n[mf][2];\n      const uint32_t v = (t & 2) ? v23 : v01;\n"
+         "      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);\n"
+         "      return __uint_as_float(t < 4 ? r[0] : r[1]);\n    } else if constexpr (G == 4) {\n"
+         "      const uint32_t v = (t & 1) ? sa_n[mf][1] : sa_n[mf][0];"),
+        ("s_m[mf] = sa_of(j & 3, mf) * sb_n;", "s_m[mf] = sa_of(j & (G - 1), mf) * sb_n;"),
+        ("template <int BM, int BN, bool GS>\nstatic int launch(", "template <int BM, int BN, int G>\nstatic int launch("),
+        ("  constexpr auto kern = gemm_fp8_bs_kernel<BM, BN, GS>;", "  constexpr auto kern = gemm_fp8_bs_kernel<BM, BN, G>;"),
+        ("  if (K % 512 == 0 && ((uintptr_t)sA & 7) == 0)\n"
+         "    return big ? mx::gemm8::launch<256, 256, true>(A, sA, B, sB, C, M, N, K, s)\n"
+         "               : mx::gemm8::launch<128, 128, true>(A, sA, B, sB, C, M, N, K, s);\n"
+         "  return big ? mx::gemm8::launch<256, 256, false>(A, sA, B, sB, C, M, N, K, s)\n"
+         "             : mx::gemm8::launch<128, 128, false>(A, sA, B, sB, C, M, N, K, s);",
+         "  if (K % 1024 == 0 && ((uintptr_t)sA & 15) == 0)\n"
+         "    return big ? mx::gemm8::launch<256, 256, 8>(A, sA, B, sB, C, M, N, K, s)\n"
+         "               : mx::gemm8::launch<128, 128, 8>(A, sA, B, sB, C, M, N, K, s);\n"
+         "  if (K % 512 == 0 && ((uintptr_t)sA & 7) == 0)\n"
+         "    return big ? mx::gemm8::launch<256, 256, 4>(A, sA, B, sB, C, M, N, K, s)\n"
+         "               : mx::gemm8::launch<128, 128, 4>(A, sA, B, sB, C, M, N, K, s);\n"
+         "  return big ? mx::gemm8::launch<256, 256, 1>(A, sA, B, sB, C, M, N, K, s)\n"
+         "             : mx::gemm8::launch<128, 128, 1>(A, sA, B, sB, C, M, N, K, s);"),
+    ],
+    # Each block's LDS read bases (lane address + slot offset) computed once
+    # and hidden from the compiler, so every fragment read carries its own
+    # offset as an immediate (8 address adds per block instead of 24).
+    "read_bases": [
+        ("  auto read_b = [&](uint32_t so, int nf) {\n    u32x2 v[4];\n#pragma unroll\n"
+         "    for (int r = 0; r < 4; ++r) v[r] = lds_read_tr8_at(b_col[nf] + so + 8 * r * BN);",
+         "  auto read_b = [&](uint32_t base) {\n    u32x2 v[4];\n#pragma unroll\n"
+         "    for (int r = 0; r < 4; ++r) v[r] = lds_read_tr8_at(base + 8 * r * BN);"),
+        ("  auto read_a = [&](uint32_t so, int kh, int mf) {\n    const uint32_t r = so + 32 * mf * SBK;\n"
+         "    const u32x4 lo = lds_ld128(a_col[kh][0] + r);\n    const u32x4 hi = lds_ld128(a_col[kh][1] + r);",
+         "  auto read_a = [&](const uint32_t (&base)[2], int mf) {\n"
+         "    const u32x4 lo = lds_ld128(base[0] + 32 * mf * SBK);\n    const u32x4 hi = lds_ld128(base[1] + 32 * mf * SBK);"),
+        ("    const uint32_t so0 = ((2 * j) % NSB) * CF::B_S, so1 = ((2 * j + 1) % NSB) * CF::B_S;\n",
+         "    const uint32_t so0 = ((2 * j) % NSB) * CF::B_S, so1 = ((2 * j + 1) % NSB) * CF::B_S;\n"
+         "    uint32_t ab[2][2], bb0[FN], bb1[FN];\n#pragma unroll\n    for (int kh = 0; kh < 2; ++kh)\n#pragma unroll\n"
+         "      for (int h = 0; h < 2; ++h) {\n        ab[kh][h] = a_col[kh][h] + ao;\n        asm(\"\" : \"+v\"(ab[kh][h]));\n      }\n"
+         "#pragma unroll\n    for (int nf = 0; nf < FN; ++nf) {\n      bb0[nf] = b_col[nf] + so0;\n      bb1[nf] = b_col[nf] + so1;\n"
+         "      asm(\"\" : \"+v\"(bb0[nf]));\n      asm(\"\" : \"+v\"(bb1[nf]));\n    }\n"),
+        ("    bf0[0] = read_b(so0, 0);\n    a0 = read_a(ao, 0, 0);\n    bf1[0] = read_b(so1, 0);\n    a1 = read_a(ao, 1, 0);",
+         "    bf0[0] = read_b(bb0[0]);\n    a0 = read_a(ab[0], 0);\n    bf1[0] = read_b(bb1[0]);\n    a1 = read_a(ab[1], 0);"),
+        ("          bf0[nf + 1] = read_b(so0, nf + 1);\n          bf1[nf + 1] = read_b(so1, nf + 1);",
+         "          bf0[nf + 1] = read_b(bb0[nf + 1]);\n          bf1[nf + 1] = read_b(bb1[nf + 1]);"),
+        ("          if (mf + 1 < FM) a0 = read_a(ao, 0, mf + 1);", "          if (mf + 1 < FM) a0 = read_a(ab[0], mf + 1);"),
+        ("        if (nf == FN - 1 && mf + 1 < FM) a1 = read_a(ao, 1, mf + 1);",
+         "        if (nf == FN - 1 && mf + 1 < FM) a1 = read_a(ab[1], mf + 1);"),
+    ],
 }
 FP8_VARIANTS = {
     "as_built": ("the kernel as built", []),
@@ -93,6 +187,13 @@ FP8_VARIANTS = {
     "mfma_and_lds_reads": ("no promotion, no tile loads in the loop, no barrier, activation scales from one "
                            "line: the MFMAs, their LDS fragment reads and the scale loads",
                            ["promotion", "act_scales", "tile_loads", "barrier"]),
+    "alt_loads_b_first": ("both B stages in the first row block's share, the A block over the next ones",
+                          ["loads_b_first"], True),
+    "alt_loads_after_barrier": ("all eight tile loads right after the barrier", ["loads_after_barrier"], True),
+    "alt_b_loads_after_barrier": ("the B stages right after the barrier, the A block spread",
+                                  ["b_loads_after_barrier"], True),
+    "alt_act_scales_8": ("activation scales eight blocks per 16-byte load (K % 1024 == 0)", ["act_scales_8"], True),
+    "alt_read_bases": ("per-block LDS read bases, fragment offsets as immediates", ["read_bases"], True),
 }
 
 # ---------------------------------------------------------------------------
@@ -134,6 +235,33 @@ GQA_PARTS = {
         ("    __syncthreads();\n    // the next tile's loads go out one per k step",
          "    // the next tile's loads go out one per k step"),
     ],
+    # ---- alternative designs (each computes what the kernel as built does) ----
+    # The next tile's loads unconditional and branch-free, valid when S is a
+    # multiple of 64 (the timed shape): past the last tile the last tile
+    # again into the free stage, from a scalar tile base plus the
+    # precomputed lane offsets (no row clamp, no address VALU, no branch);
+    # the loop then waits for those loads before the ring is reused.
+    "branch_free_loads": [
+        ("  auto issue = [&](int blk) {\n    const int kv0 = blk * BN;",
+         "  auto issue_full = [&](int src, int slot, int n) {\n    const int ld = wave * L::LPW + n;\n"
+         "    const bool vt = ld >= L::NLK;\n    const int kv0 = src * BN;\n"
+         "    dma16((vt ? Vh + (size_t)kv0 * L::ROWV : Kh + (size_t)kv0 * L::ROWK), ld_off[n],\n"
+         "          lds0 + slot * L::STAGE + ld * 1024);\n  };\n"
+         "  auto issue = [&](int blk) {\n    const int kv0 = blk * BN;"),
+        ("          if (dc == n * DC / L::LPW && load_next) issue_part(blk + NS - 1, n);",
+         "          if (dc == n * DC / L::LPW) issue_full(load_next ? blk + NS - 1 : nblk - 1, (blk + NS - 1) % NS, n);"),
+        ("      if (blk + 2 < nblk) tile(blk + 2, std::integral_constant<int, 2>{});\n  }\n",
+         "      if (blk + 2 < nblk) tile(blk + 2, std::integral_constant<int, 2>{});\n  }\n  wait_vmcnt<0>();\n"),
+    ],
+    # K fragments read three k-steps ahead instead of two.
+    "k_lookahead_3": [
+        ("      constexpr int KLA = DQK > 128 ? 1 : 2;", "      constexpr int KLA = DQK > 128 ? 1 : 3;"),
+    ],
+    # No wave priority (s_setprio) around the MFMA phases.
+    "no_setprio": [
+        ("      __builtin_amdgcn_s_setprio(1);\n", "", 2),
+        ("      __builtin_amdgcn_s_setprio(0);\n", "", 2),
+    ],
 }
 GQA_VARIANTS = {
     "as_built": ("the kernel as built", []),
@@ -143,6 +271,10 @@ GQA_VARIANTS = {
     "no_exp2_lds_reads_kv_loads": ("... and without the K/V loads after the first tile", ["exp2", "lds_reads", "kv_loads"]),
     "no_exp2_lds_reads_kv_loads_barrier": ("... and without the per-tile barrier",
                                            ["exp2", "lds_reads", "kv_loads", "barrier"]),
+    "alt_branch_free_loads": ("next tile's loads unconditional and branch-free (S % 64 == 0 only)",
+                              ["branch_free_loads"], True),
+    "alt_k_lookahead_3": ("K fragment reads three k-steps ahead instead of two", ["k_lookahead_3"], True),
+    "alt_no_setprio": ("no wave priority around the MFMA phases", ["no_setprio"], True),
 }
 
 # ---------------------------------------------------------------------------
@@ -250,14 +382,27 @@ def _package_build():
     return build
 
 
+def variant_exact(kernel: str, variant: str) -> bool:
+    """Whether the variant computes what the kernel as built computes (an
+    alternative design rather than a part switched off)."""
+    v = KERNELS[kernel]["variants"][variant]
+    return len(v) > 2 and bool(v[2])
+
+
 def patched_source(kernel: str, variant: str) -> str:
+    """The kernel source with the variant's patches: (anchor, replacement)
+    pairs whose anchor must occur exactly once, or (anchor, replacement,
+    count) for an anchor that must occur exactly count times."""
     spec = KERNELS[kernel]
     text = (PKG_DIR / "csrc" / spec["source"]).read_text()
     for part in spec["variants"][variant][1]:
-        for anchor, repl in spec["parts"][part]:
+        for patch in spec["parts"][part]:
+            anchor, repl = patch[0], patch[1]
+            want = patch[2] if len(patch) > 2 else 1
             n = text.count(anchor)
-            if n != 1:
-                raise RuntimeError(f"{kernel}/{variant}: patch anchor of part {part!r} occurs {n} times: {anchor!r}")
+            if n != want:
+                raise RuntimeError(f"{kernel}/{variant}: patch anchor of part {part!r} occurs {n} times, not {want}: "
+                                   f"{anchor!r}")
             text = text.replace(anchor, repl)
     return text
 
@@ -309,8 +454,10 @@ def build_variants(kernel: str, variants: list[str]) -> None:
         print(f"built {kernel}/{v}: {lib}", flush=True)
 
 
-def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 300.0) -> float:
-    """Mean µs per launch of one graph replay (this process's kernel library)."""
+def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 300.0) -> tuple[float, str]:
+    """Mean µs per launch of one graph replay (this process's kernel
+    library), and the SHA-256 of the output of one more call."""
+    import hashlib
     import importlib
     import time
 
@@ -371,12 +518,21 @@ def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 3
     g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / steps
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    out.zero_()
+    fn()
+    torch.cuda.synchronize()
+    return us, hashlib.sha256(out.cpu().contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()
 
 
 def run_variants(kernel: str, variants: list[str], runs: int) -> str:
+    """Time the variants in turn; an exact variant's output is compared, bit
+    for bit (SHA-256 of the output tensor), with the kernel as built."""
     spec = KERNELS[kernel]
+    if any(variant_exact(kernel, v) for v in variants) and "as_built" not in variants:
+        variants = ["as_built", *variants]
     res = {v: [] for v in variants}
+    digest: dict[str, set] = {}
     for r in range(runs):
         for v in variants:
             lib = OUT_ROOT / kernel / v / "libmxkernels.so"
@@ -387,15 +543,27 @@ def run_variants(kernel: str, variants: list[str], runs: int) -> str:
             p = subprocess.run([sys.executable, str(Path(__file__).resolve()), "time", kernel], env=env,
                                capture_output=True, text=True, timeout=300)
             m = re.search(r"^us_per_launch ([\d.]+)$", p.stdout, re.M)
-            if p.returncode != 0 or not m:
+            h = re.search(r"^out_sha256 ([0-9a-f]+)$", p.stdout, re.M)
+            if p.returncode != 0 or not m or not h:
                 raise RuntimeError(f"{kernel}/{v} failed (rc {p.returncode})\n{p.stdout[-2000:]}\n{p.stderr[-2000:]}")
             res[v].append(float(m.group(1)))
+            digest.setdefault(v, set()).add(h.group(1))
             print(f"[ablate] {kernel}/{v}: {res[v][-1]:.1f} us", file=sys.stderr, flush=True)
-    lines = [f"| variant ({spec['workload']}) | µs per launch, run by run | min–max |", "|---|---|---:|"]
+    lines = [f"| variant ({spec['workload']}) | µs per launch, run by run | min–max | output |",
+             "|---|---|---:|---|"]
     for v in variants:
         t = res[v]
         d = 1 if max(t) < 100 else 0  # decimals of the range
-        lines.append(f"| {spec['variants'][v][0]} | {', '.join(f'{x:.1f}' for x in t)} | {min(t):.{d}f}–{max(t):.{d}f} |")
+        if len(digest[v]) != 1:
+            out = "differs between runs"
+        elif v == "as_built":
+            out = "reference"
+        elif variant_exact(kernel, v):
+            out = "bit-identical" if digest[v] == digest.get("as_built") else "DIFFERS"
+        else:
+            out = "not compared (work removed)"
+        lines.append(f"| {spec['variants'][v][0]} | {', '.join(f'{x:.1f}' for x in t)} | "
+                     f"{min(t):.{d}f}–{max(t):.{d}f} | {out} |")
     return "\n".join(lines)
 
 
@@ -415,7 +583,8 @@ def main() -> int:
     elif args.action == "run":
         print(run_variants(args.kernel, variants, args.runs))
     else:
-        print(f"us_per_launch {time_one(args.kernel):.3f}", flush=True)
+        us, sha = time_one(args.kernel)
+        print(f"us_per_launch {us:.3f}\nout_sha256 {sha}", flush=True)
     return 0
 
 

@@ -27,8 +27,8 @@ SRC = REPO_ROOT / "cuda-oxide-bench_amd" / "csrc" / "gemm_fp8_bs.hip"
 KERNEL = "_ZN2mx5gemm818gemm_fp8_bs_kernel"
 
 _VMEM = re.compile(r"^\s*(global_|buffer_|flat_|scratch_)")
-# the scale loads: one scale (global_load_dword) or two (global_load_dwordx2) per lane
-_SCALE_LOAD = re.compile(r"^global_load_dword(?:x2)?\s+(v\d+|v\[\d+:\d+\]),\s*v\d+,\s*s\[")
+# the scale loads: one scale (global_load_dword), two or four (x2, x4) per lane
+_SCALE_LOAD = re.compile(r"^global_load_dword(?:x2|x4)?\s+(v\d+|v\[\d+:\d+\]),\s*v\d+,\s*s\[")
 
 
 def _check_kernel(lines: list[str]) -> tuple[int, list[str]]:

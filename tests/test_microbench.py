@@ -59,9 +59,9 @@ def test_ablation_patches_apply():
     spec.loader.exec_module(ab)
     for kernel, k in ab.KERNELS.items():
         base = (REPO_ROOT / "cuda-oxide-bench_amd" / "csrc" / k["source"]).read_text()
-        for v, (_, parts) in k["variants"].items():
+        for v, spec_v in k["variants"].items():
             text = ab.patched_source(kernel, v)
-            assert (text == base) == (not parts), f"{kernel}/{v}"
+            assert (text == base) == (not spec_v[1]), f"{kernel}/{v}"
 
 
 @pytest.mark.gpu
