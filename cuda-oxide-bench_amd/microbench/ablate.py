@@ -366,6 +366,9 @@ KERNELS = {
     "gqa": {"source": "gqa_fwd.hip", "parts": GQA_PARTS, "variants": GQA_VARIANTS,
             "workload": "gqa_fwd causal B1 Hq32 Hkv8 S4096 D128 bf16, default tile",
             "kernel_prefix": "_ZN2mx3gqa14gqa_fwd_kernel"},
+    "bf16_8192": {"source": "gemm_bf16.hip", "parts": {}, "variants": {"as_built": ("the kernel as built", [])},
+                  "workload": "gemm_bf16 M8192 N8192 K8192 U[-1,1] (gemm_bf16_dma16s_kernel)",
+                  "kernel_prefix": "_ZN2mx4gemm23gemm_bf16_dma16s_kernel"},
     "bf16_1024": {"source": "gemm_bf16.hip", "parts": BF16_PARTS, "variants": BF16_VARIANTS,
                   "workload": "gemm_bf16 M1024 N1024 K1024 U[-1,1] (gemm_bf16_sdma_kernel)",
                   "kernel_prefix": "_ZN2mx4gemm21gemm_bf16_sdma_kernel"},
@@ -454,9 +457,13 @@ def build_variants(kernel: str, variants: list[str]) -> None:
         print(f"built {kernel}/{v}: {lib}", flush=True)
 
 
-def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 300.0) -> tuple[float, str]:
+def time_one(kernel: str, inputs: str = "random", steps: int = 20, warmup: int = 3,
+             settle_ms: float = 300.0) -> tuple[float, str]:
     """Mean µs per launch of one graph replay (this process's kernel
-    library), and the SHA-256 of the output of one more call."""
+    library), and the SHA-256 of the output of one more call.  inputs
+    "constant" fills every operand with one value (fp8: code 0x38 = 1.0 with
+    unit scales; otherwise 0.5): the same work on operands that switch
+    nothing in the MFMA datapath."""
     import hashlib
     import importlib
     import time
@@ -479,8 +486,9 @@ def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 3
         out = torch.empty_like(q)
         fn = lambda: ops.gqa_fwd(q, k, v, causal=True, out=out)  # noqa: E731
     elif kernel == "bf16_1024":
-        a = (torch.rand((1024, 1024), device="cuda") * 2 - 1).to(torch.bfloat16)
-        b = (torch.rand((1024, 1024), device="cuda") * 2 - 1).to(torch.bfloat16)
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        a = (torch.rand((1024, 1024), device="cuda", generator=gen) * 2 - 1).to(torch.bfloat16)
+        b = (torch.rand((1024, 1024), device="cuda", generator=gen) * 2 - 1).to(torch.bfloat16)
         out = torch.empty((1024, 1024), dtype=torch.bfloat16, device="cuda")
         fn = lambda: ops.gemm_bf16(a, b, out=out)  # noqa: E731
     elif kernel == "mla":
@@ -490,8 +498,24 @@ def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 3
         out = torch.empty((32, 128, 512), dtype=torch.bfloat16, device="cuda")
         ws = torch.empty(max(1, ops.mla_decode_workspace_bytes(32, 128, 4096)), dtype=torch.uint8, device="cuda")
         fn = lambda: ops.mla_decode(q, kv, 192 ** -0.5, out=out, workspace=ws)  # noqa: E731
+    elif kernel == "bf16_8192":
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        a = (torch.rand((8192, 8192), device="cuda", generator=gen) * 2 - 1).to(torch.bfloat16)
+        b = (torch.rand((8192, 8192), device="cuda", generator=gen) * 2 - 1).to(torch.bfloat16)
+        out = torch.empty((8192, 8192), dtype=torch.bfloat16, device="cuda")
+        fn = lambda: ops.gemm_bf16(a, b, out=out)  # noqa: E731
     else:
         raise ValueError(kernel)
+    if inputs == "constant":
+        for name, t in list(locals().items()):
+            if name in ("a8", "b8"):
+                t.view(torch.uint8).fill_(0x38)
+            elif name in ("sa", "sb"):
+                t.fill_(1.0)
+            elif name in ("a", "b", "q", "k", "v", "kv"):
+                t.fill_(0.5)
+    elif inputs != "random":
+        raise ValueError(inputs)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -525,45 +549,46 @@ def time_one(kernel: str, steps: int = 20, warmup: int = 3, settle_ms: float = 3
     return us, hashlib.sha256(out.cpu().contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()
 
 
-def run_variants(kernel: str, variants: list[str], runs: int) -> str:
+def run_variants(kernel: str, variants: list[str], runs: int, inputs: list[str] | None = None) -> str:
     """Time the variants in turn; an exact variant's output is compared, bit
     for bit (SHA-256 of the output tensor), with the kernel as built."""
     spec = KERNELS[kernel]
     if any(variant_exact(kernel, v) for v in variants) and "as_built" not in variants:
         variants = ["as_built", *variants]
-    res = {v: [] for v in variants}
-    digest: dict[str, set] = {}
+    modes = inputs or ["random"]
+    res = {(v, m): [] for v in variants for m in modes}
+    digest: dict[tuple, set] = {}
     for r in range(runs):
-        for v in variants:
+        for v, mode in [(v, m) for v in variants for m in modes]:
             lib = OUT_ROOT / kernel / v / "libmxkernels.so"
             if not lib.exists():
                 raise RuntimeError(f"{lib} missing: run the build step first")
-            print(f"[ablate] run {r + 1}/{runs}: {kernel}/{v}", file=sys.stderr, flush=True)
+            print(f"[ablate] run {r + 1}/{runs}: {kernel}/{v} ({mode} inputs)", file=sys.stderr, flush=True)
             env = dict(os.environ, MX_KERNELS_LIB=str(lib))
-            p = subprocess.run([sys.executable, str(Path(__file__).resolve()), "time", kernel], env=env,
+            p = subprocess.run([sys.executable, str(Path(__file__).resolve()), "time", kernel, "--inputs", mode], env=env,
                                capture_output=True, text=True, timeout=300)
             m = re.search(r"^us_per_launch ([\d.]+)$", p.stdout, re.M)
             h = re.search(r"^out_sha256 ([0-9a-f]+)$", p.stdout, re.M)
             if p.returncode != 0 or not m or not h:
                 raise RuntimeError(f"{kernel}/{v} failed (rc {p.returncode})\n{p.stdout[-2000:]}\n{p.stderr[-2000:]}")
-            res[v].append(float(m.group(1)))
-            digest.setdefault(v, set()).add(h.group(1))
-            print(f"[ablate] {kernel}/{v}: {res[v][-1]:.1f} us", file=sys.stderr, flush=True)
+            res[(v, mode)].append(float(m.group(1)))
+            digest.setdefault((v, mode), set()).add(h.group(1))
+            print(f"[ablate] {kernel}/{v} ({mode} inputs): {res[(v, mode)][-1]:.1f} us", file=sys.stderr, flush=True)
     lines = [f"| variant ({spec['workload']}) | µs per launch, run by run | min–max | output |",
              "|---|---|---:|---|"]
-    for v in variants:
-        t = res[v]
+    for v, mode in [(v, m) for v in variants for m in modes]:
+        t = res[(v, mode)]
         d = 1 if max(t) < 100 else 0  # decimals of the range
-        if len(digest[v]) != 1:
+        if len(digest[(v, mode)]) != 1:
             out = "differs between runs"
         elif v == "as_built":
             out = "reference"
         elif variant_exact(kernel, v):
-            out = "bit-identical" if digest[v] == digest.get("as_built") else "DIFFERS"
+            out = "bit-identical" if digest[(v, mode)] == digest.get(("as_built", mode)) else "DIFFERS"
         else:
             out = "not compared (work removed)"
-        lines.append(f"| {spec['variants'][v][0]} | {', '.join(f'{x:.1f}' for x in t)} | "
-                     f"{min(t):.{d}f}–{max(t):.{d}f} | {out} |")
+        name = spec["variants"][v][0] + ("" if mode == "random" else f", {mode} inputs")
+        lines.append(f"| {name} | {', '.join(f'{x:.1f}' for x in t)} | {min(t):.{d}f}–{max(t):.{d}f} | {out} |")
     return "\n".join(lines)
 
 
@@ -573,6 +598,8 @@ def main() -> int:
     ap.add_argument("kernel", choices=sorted(KERNELS))
     ap.add_argument("--variants", default="", help="comma-separated subset (default: all)")
     ap.add_argument("--runs", type=int, default=3)
+    ap.add_argument("--inputs", default="random",
+                    help="run: comma-separated input modes timed in turn (random, constant); time: one of them")
     args = ap.parse_args()
     variants = [v for v in args.variants.split(",") if v] or list(KERNELS[args.kernel]["variants"])
     for v in variants:
@@ -581,9 +608,9 @@ def main() -> int:
     if args.action == "build":
         build_variants(args.kernel, variants)
     elif args.action == "run":
-        print(run_variants(args.kernel, variants, args.runs))
+        print(run_variants(args.kernel, variants, args.runs, args.inputs.split(",")))
     else:
-        us, sha = time_one(args.kernel)
+        us, sha = time_one(args.kernel, args.inputs)
         print(f"us_per_launch {us:.3f}\nout_sha256 {sha}", flush=True)
     return 0
 
