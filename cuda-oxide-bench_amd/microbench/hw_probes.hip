@@ -25,7 +25,9 @@
 //    VGPRs or, as inline asm, in AGPRs) and time themselves in shader-clock
 //    cycles and in the 100 MHz real-time counter; meanwhile waves 4-7 idle
 //    (busy = 0), run independent v_fma_f32 streams long enough to outlast
-//    them (busy = 1), or issue the same MFMA stream (busy = 2).  Each wave
+//    them (busy = 1), issue the same MFMA stream (busy = 2), or stream
+//    conflict-free 128-bit LDS reads (busy = 3: 1 KB per instruction, eight
+//    in flight per wave).  Each wave
 //    records its hardware id, so the host can check that waves w and w + 4
 //    share a SIMD.
 //  * mxp_promote_launch: the fp8 GEMM's block promotion.  Every wave keeps
@@ -49,6 +51,7 @@
 //    copies: 1 KB per wave instruction, DEPTH of them in flight per wave
 //    through a ring of DEPTH KB), so the time of a launch gives a
 //    workgroup's read rate against the bytes it keeps in flight.
+#include <type_traits>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -57,6 +60,7 @@
 
 namespace {
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -108,18 +112,43 @@ __global__ __launch_bounds__(kOverlapThreads, 1) void overlap_kernel(float* out,
     e[i] = 1e-6f * (threadIdx.x + i);
     u[i] = threadIdx.x * 7u + i;
   }
+  // OP 10: each MFMA's B operand is a 128-bit LDS read (1 KB per wave,
+  // lane i reading bytes 16 i .. 16 i + 15: conflict-free) issued one
+  // iteration ahead, as the kernels read their fragments; without MFMAs the
+  // reads are consumed by one v_xor each.  Each wave reads its own 32 KB.
+  u32x4 v[8];
+  const u32x4* lb = reinterpret_cast<const u32x4*>(lds) + (threadIdx.x >> 6) * 2048;
+  if constexpr (OP == 10) {
+    u32x4* lw = reinterpret_cast<u32x4*>(lds) + (threadIdx.x >> 6) * 2048;
+    for (int i = threadIdx.x & 63; i < 2048; i += 64) lw[i] = u32x4{0x3f803f80u ^ (unsigned)i, 0x3e003e00u, 0x3f003f00u, (unsigned)i};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) v[m] = lb[m * 64 + (threadIdx.x & 63)];
+  }
   const long long t0 = __builtin_readcyclecounter();
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      if constexpr (MF)
-        acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                         acc[m], 0, 0, 0);
-      mix<OP>(e, u, m);
+      if constexpr (OP == 10) {
+        if constexpr (MF)
+          acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                           __builtin_bit_cast(bf16x8, v[m]), acc[m], 0, 0, 0);
+        else
+          u[m] ^= v[m][0];
+        v[m] = lb[(((it + 1) * 8 + m) & 31) * 64 + (threadIdx.x & 63)];
+      } else {
+        if constexpr (MF)
+          acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                           acc[m], 0, 0, 0);
+        mix<OP>(e, u, m);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   const long long t1 = __builtin_readcyclecounter();
+  if constexpr (OP == 10) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) u[m] ^= v[m][1];
+  }
   float r = 0.f;
 #pragma unroll
   for (int m = 0; m < 8; ++m) r += acc[m][threadIdx.x & 15];
@@ -316,7 +345,8 @@ __global__ __launch_bounds__(256) void wg_read_kernel(const uint4* __restrict__ 
 
 // FORM 0: bf16 32x32x16, VGPR accumulators; 1: the same in AGPRs (asm);
 // 2: fp8 e4m3 32x32x64, VGPR accumulators (the scaled form with unit
-// scales, as the kernels issue it); 3: fp8 32x32x64 in AGPRs (asm).
+// scales, as the kernels issue it); 3: fp8 32x32x64 in AGPRs (asm); 4: bf16
+// 16x16x32, VGPR accumulators (the bf16 GEMMs' shape).
 // cycles[8 b + w], rtime[8 b + w] (waves 4-7 only with busy > 0) and
 // hwid[8 b + w] per wave w of workgroup b.
 template <int FORM, int BUSY>
@@ -337,15 +367,19 @@ __global__ __launch_bounds__(512, 1) void contend_kernel(const u32x4* __restrict
     }
     const i32x8 a8 = __builtin_bit_cast(i32x8, (u32x4[2]){a[0], a[1]});
     const i32x8 b8 = __builtin_bit_cast(i32x8, (u32x4[2]){b[0], b[1]});
-    f32x16 acc[8];
+    using Acc = std::conditional_t<FORM == 4, f32x4_t, f32x16>;
+    Acc acc[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
+    for (int j = 0; j < 8; ++j) acc[j] = Acc{};
     const long long r0 = __builtin_amdgcn_s_memrealtime();
     const long long t0 = __builtin_readcyclecounter();
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        if constexpr (FORM == 0)
+        if constexpr (FORM == 4)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[j & 1]),
+                                                           __builtin_bit_cast(bf16x8, b[(j >> 1) & 1]), acc[j], 0, 0, 0);
+        else if constexpr (FORM == 0)
           acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[j & 1]),
                                                            __builtin_bit_cast(bf16x8, b[(j >> 1) & 1]), acc[j], 0, 0, 0);
         else if constexpr (FORM == 1)
@@ -363,8 +397,34 @@ __global__ __launch_bounds__(512, 1) void contend_kernel(const u32x4* __restrict
       for (int j = 0; j < 8; ++j) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4" : "+a"(acc[j]));
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & 15];
+    for (int j = 0; j < 8; ++j) r += acc[j][threadIdx.x & (FORM == 4 ? 3 : 15)];
     if ((threadIdx.x & 63) == 0) {
+      cycles[blockIdx.x * 8 + wave] = t1 - t0;
+      rtime[blockIdx.x * 8 + wave] = r1 - r0;
+    }
+  } else if constexpr (BUSY == 3) {
+    // waves 4-7 read their own 16 KB of LDS: lane i reads bytes 16 i ..
+    // 16 i + 15 of a 1 KB block (16 distinct 16-byte slots per 16-lane
+    // group: no bank conflicts), eight blocks per iteration
+    __shared__ u32x4 lbuf[4 * 1024];
+    u32x4* mine = lbuf + (wave - 4) * 1024;
+    const int lane = threadIdx.x & 63;
+    for (int i = lane; i < 1024; i += 64) mine[i] = u32x4{(unsigned)i, (unsigned)t, 1u, 2u};
+    u32x4 x = u32x4{0u, 0u, 0u, 0u};
+    const long long r0 = __builtin_amdgcn_s_memrealtime();
+    const long long t0 = __builtin_readcyclecounter();
+    for (int it = 0; it < valu_iters; ++it) {
+      asm volatile("" ::: "memory");  // every iteration reads LDS again
+      u32x4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = mine[((it * 8 + j) & 15) * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x ^= v[j];
+    }
+    const long long t1 = __builtin_readcyclecounter();
+    const long long r1 = __builtin_amdgcn_s_memrealtime();
+    r += (float)(x[0] ^ x[1] ^ x[2] ^ x[3]);
+    if (lane == 0) {
       cycles[blockIdx.x * 8 + wave] = t1 - t0;
       rtime[blockIdx.x * 8 + wave] = r1 - r0;
     }
@@ -399,8 +459,11 @@ int launch_contend(int busy, int nwg, int iters, int valu_iters, const u32x4* op
   else if (busy == 1)
     hipLaunchKernelGGL((contend_kernel<FORM, 1>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
                        valu_iters);
-  else
+  else if (busy == 2)
     hipLaunchKernelGGL((contend_kernel<FORM, 2>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
+                       valu_iters);
+  else
+    hipLaunchKernelGGL((contend_kernel<FORM, 3>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
                        valu_iters);
   return hip_status(hipGetLastError());
 }
@@ -550,7 +613,9 @@ int launch_stream(const uint4* src, long long stride16, long long n16, int nwg, 
 
 // probe: 0 MFMAs only, 1 v_exp_f32, 2 v_cvt_pk_bf16_f32, 3 v_dot2_f32_bf16,
 // 4 v_add_f32, 5 v_mul_f32, 6 v_fma_f32 (32 per iteration), 7 s_nop 0,
-// 8 s_nop 1 (one per MFMA), 9 the v_exp_f32 mix with an s_nop 1 per MFMA.  out: nwg * 256 floats; cycles: nwg entries.
+// 8 s_nop 1 (one per MFMA), 9 the v_exp_f32 mix with an s_nop 1 per MFMA,
+// 10 eight 128-bit LDS reads, each the B operand of the next iteration's
+// MFMA (without MFMAs: consumed by one v_xor each).  out: nwg * 256 floats; cycles: nwg entries.
 // Returns 0, -1 for invalid arguments or an unknown probe, or -(1000 + e)
 // for HIP error e.
 extern "C" int mxp_overlap_launch(int probe, int with_mfma, int nwg, int iters, float* out, long long* cycles,
@@ -568,6 +633,7 @@ extern "C" int mxp_overlap_launch(int probe, int with_mfma, int nwg, int iters, 
     case 7: return launch_op<7>(with_mfma, nwg, iters, out, cycles, s);
     case 8: return launch_op<8>(with_mfma, nwg, iters, out, cycles, s);
     case 9: return launch_op<9>(with_mfma, nwg, iters, out, cycles, s);
+    case 10: return launch_op<10>(with_mfma, nwg, iters, out, cycles, s);
     default: return -1;
   }
 }
@@ -629,13 +695,13 @@ extern "C" int mxp_stream_launch(int mode, int depth, const void* src, long long
   }
 }
 
-// form 0..3 as contend_kernel; busy 0 (waves 4-7 idle), 1 (VALU) or 2
-// (the same MFMAs).  ops: nwg * 512 * 4 16-byte fragments (lane t reads its
+// form 0..4 as contend_kernel; busy 0 (waves 4-7 idle), 1 (VALU), 2 (the
+// same MFMAs) or 3 (LDS reads; valu_iters iterations of eight 1 KB reads).  ops: nwg * 512 * 4 16-byte fragments (lane t reads its
 // 4 at 4 t); out: nwg * 512 floats; cycles, rtime and hwid: nwg * 8 each.
 extern "C" int mxp_contend_launch(int form, int busy, int nwg, int iters, int valu_iters, const void* ops, float* out,
                                   long long* cycles, long long* rtime, unsigned* hwid, void* stream) {
   if (nwg <= 0 || iters <= 0 || valu_iters < 0 || !ops || !out || !cycles || !rtime || !hwid || form < 0 ||
-      form > 3 || busy < 0 || busy > 2)
+      form > 4 || busy < 0 || busy > 3)
     return -1;
   const u32x4* o = static_cast<const u32x4*>(ops);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -643,7 +709,8 @@ extern "C" int mxp_contend_launch(int form, int busy, int nwg, int iters, int va
     case 0: return launch_contend<0>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
     case 1: return launch_contend<1>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
     case 2: return launch_contend<2>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
-    default: return launch_contend<3>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
+    case 3: return launch_contend<3>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
+    default: return launch_contend<4>(busy, nwg, iters, valu_iters, o, out, cycles, rtime, hwid, s);
   }
 }
 

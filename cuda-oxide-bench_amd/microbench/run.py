@@ -60,6 +60,7 @@ OVERLAP_PROBES = [
     (7, "8 s_nop 0 (one per MFMA)"),
     (8, "8 s_nop 1 (one per MFMA)"),
     (9, "32 v_exp_f32 + 8 s_nop 1 (one per MFMA)"),
+    (10, "8 ds_read_b128 of 1 KB, each the B operand of the next iteration's MFMA (alone: consumed by a v_xor)"),
 ]
 
 
@@ -225,7 +226,8 @@ def wg_read(lib, reps: int = 20) -> list[str]:
 
 
 CONTEND_FORMS = [(0, "32x32x16 bf16, VGPR accumulators"), (1, "32x32x16 bf16, AGPR accumulators"),
-                 (2, "32x32x64 fp8, VGPR accumulators"), (3, "32x32x64 fp8, AGPR accumulators")]
+                 (2, "32x32x64 fp8, VGPR accumulators"), (3, "32x32x64 fp8, AGPR accumulators"),
+                 (4, "16x16x32 bf16, VGPR accumulators")]
 
 
 def contend(lib, iters: int = 4000, reps: int = 3) -> list[str]:
@@ -245,10 +247,10 @@ def contend(lib, iters: int = 4000, reps: int = 3) -> list[str]:
         """Median over reps of: cycles per MFMA of waves 0-3, their clock (GHz from the
         100 MHz real-time counter), waves 4-7's cycles, and the share of workgroups whose
         waves w and w + 4 report the same SIMD."""
-        valu_iters = 12 * iters if busy == 1 else 0
+        valu_iters = 12 * iters if busy == 1 else (3 * iters if busy == 3 else 0)
         mf, clk, other, paired = [], [], [], []
         for _ in range(reps):
-            ops = bf16 if form < 2 else fp8
+            ops = bf16 if form in (0, 1, 4) else fp8
             rc = lib.mxp_contend_launch(form, busy, nwg, iters, valu_iters, ops.data_ptr(), out.data_ptr(),
                                         cycles.data_ptr(), rtime.data_ptr(), hwid.data_ptr(), st)
             if rc != 0:
@@ -264,16 +266,27 @@ def contend(lib, iters: int = 4000, reps: int = 3) -> list[str]:
         return statistics.median(mf), statistics.median(clk), statistics.median(other), min(paired)
 
     lines = ["| MFMA (operands random) | waves 4-7 | waves 0-3: cycles per MFMA | clock GHz | "
-             "waves 4-7: cycles per instruction | waves 4-7 took (cycles) | waves 0-3 took | waves share a SIMD |",
-             "|---|---|---:|---:|---:|---:|---:|---:|"]
+             "waves 4-7: cycles per instruction | waves 4-7 took (cycles) | waves 0-3 took | waves share a SIMD | "
+             "MFMA cycles lost per KB read |",
+             "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
     for form, name in CONTEND_FORMS:
-        for busy, label in ((0, "idle"), (1, "v_fma_f32 stream"), (2, "the same MFMA stream")):
+        idle = None
+        for busy, label in ((0, "idle"), (1, "v_fma_f32 stream"), (2, "the same MFMA stream"),
+                            (3, "128-bit LDS reads (1 KB each, conflict-free)")):
             per_wave, ghz, other, paired = run(form, busy)
-            n_other = 12 * iters * 32 if busy == 1 else iters * 8
+            n_other = {1: 12 * iters * 32, 2: iters * 8, 3: 3 * iters * 8}.get(busy, 1)
             o_per = f"{other / n_other:.1f}" if busy else ""
             o_tot = f"{other:.0f}" if busy else ""
+            if busy == 0:
+                idle = per_wave
+            lost = ""
+            if busy == 3:
+                # KB the partner wave read while this wave's MFMAs ran, at its own rate
+                t_m = per_wave * iters * 8
+                kb = (3 * iters * 8) * t_m / max(other, 1.0)
+                lost = f"{(per_wave - idle) * iters * 8 / kb:.1f}"
             lines.append(f"| {name} | {label} | {per_wave:.1f} | {ghz:.2f} | {o_per} | {o_tot} | "
-                         f"{per_wave * iters * 8:.0f} | {100 * paired:.0f}% |")
+                         f"{per_wave * iters * 8:.0f} | {100 * paired:.0f}% | {lost} |")
     return lines
 
 
@@ -391,7 +404,7 @@ def main() -> int:
         print("\n## Chip-wide MFMA throughput, two waves per SIMD\n")
         print("\n".join(mfma_rate(lib)), flush=True)
     if every or args.contend:
-        print("\n## MFMAs beside another wave's VALU work (cycles per MFMA, two waves per SIMD)\n")
+        print("\n## MFMAs beside another wave's work (cycles per MFMA, two waves per SIMD)\n")
         print("\n".join(contend(lib)), flush=True)
     if every or args.promote:
         print("\n## fp8 block promotion (shader-clock cycles per fragment and scale block, per SIMD)\n")

@@ -38,11 +38,11 @@ def test_probe_library_exports_its_launchers(runner):
     assert lib.mxp_mfma_rate_launch(8, 4, 10, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == -1
     assert lib.mxp_mfma_rate_launch(0, 4, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == -1
     p = ctypes.c_void_p(16)
-    assert lib.mxp_contend_launch(4, 0, 1, 10, 0, p, p, p, p, p, None) == -1   # no such form
+    assert lib.mxp_contend_launch(5, 0, 1, 10, 0, p, p, p, p, p, None) == -1   # no such form
     assert lib.mxp_promote_launch(1, 4, 4, 1, 10, p, p, p, None) == -1   # lag 1..3
     assert lib.mxp_promote_launch(0, 1, 6, 1, 10, p, p, p, None) == -1   # 4 or 8 waves
     assert lib.mxp_promote_launch(4, 1, 4, 1, 10, p, p, p, None) == -1
-    assert lib.mxp_contend_launch(0, 3, 1, 10, 0, p, p, p, p, p, None) == -1
+    assert lib.mxp_contend_launch(0, 4, 1, 10, 0, p, p, p, p, p, None) == -1
     assert lib.mxp_contend_launch(0, 1, 1, 10, 10, p, p, p, p, None, None) == -1
     assert lib.mxp_stream_launch(0, 12, p, 0, 64, 1, p, None) == -1   # no such depth
     assert lib.mxp_stream_launch(2, 8, p, 0, 64, 1, p, None) == -1    # no such mode
@@ -78,7 +78,7 @@ def test_probes_run(runner):
     assert len(lines) == 2 + 16
     announce("microbench MFMA beside VALU")
     lines = runner.contend(lib, iters=200, reps=1)
-    assert len(lines) == 2 + 3 * len(runner.CONTEND_FORMS)
+    assert len(lines) == 2 + 4 * len(runner.CONTEND_FORMS)
     announce("microbench fp8 promotion")
     lines = runner.promote(lib, iters=100, reps=1)
     assert len(lines) == 2 + len(runner.PROMOTE_CASES)
