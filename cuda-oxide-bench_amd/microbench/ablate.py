@@ -1,25 +1,30 @@
-"""Where a kernel's time goes: variants of one kernel source with one part
-switched off, each built as its own kernel library and timed on the GPU.
+"""Where a kernel's time goes, and what its alternatives cost: variants of
+one kernel source, each built as its own kernel library and timed on the GPU.
 
     python cuda-oxide-bench_amd/microbench/ablate.py build fp8   # CPU: patch, compile, check, link
     python cuda-oxide-bench_amd/microbench/ablate.py run fp8     # GPU: time every variant, interleaved
+    ... run gqa --variants as_built --inputs random,constant     # the same launches on constant operands
+
+Two kinds of variants: parts switched off (no_*, and the like: they compute
+wrong results, which is the point, so their output is not checked) and
+alternative designs (alt_*: they compute what the kernel as built computes,
+and run compares their output with it bit for bit, by SHA-256).
 
 build: for each variant, a copy of the kernel source gets the variant's
-text patches (each anchor must occur exactly once, so a patch cannot drift
-onto other code), is compiled with the library's own flags and linked with
-the package's other objects (from its last build) into
-microbench/_ablate/<kernel>/<variant>/libmxkernels.so.  Before linking, the
-variant's gfx950 assembly goes through the same check as
-tests/test_fp8_scale_loads.py: every untracked scale load is landed by its
-wait before any instruction names its register; a variant that fails is not
-built.
+text patches (each anchor must occur exactly the stated number of times,
+once unless given, so a patch cannot drift onto other code), is compiled
+with the library's own flags and linked with the package's other objects
+(from its last build) into microbench/_ablate/<kernel>/<variant>/
+libmxkernels.so.  Before linking, an fp8 variant's gfx950 assembly goes
+through the same check as tests/test_fp8_scale_loads.py: every untracked
+scale load is landed by its wait before any instruction names its
+register; a variant that fails is not built.
 
 run: each variant's library is loaded in a process of its own
 (MX_KERNELS_LIB) and timed like bench.py's graph-replayed cases (warm-up
 calls, one graph of 20 launches, replayed after 300 ms of a device GEMM);
-the variants take turns, --runs times.  The variants compute wrong results,
-which is the point, so nothing checks their output; every variant keeps
-every memory access in bounds and every wait count exact, as its
+the variants (and input modes) take turns, --runs times.  Every variant
+keeps every memory access in bounds and every wait count exact, as its
 description says.  Unless its description says it removes them, a variant
 issues the MFMAs of the kernel as built (a variant whose operands became
 equal could let the compiler merge MFMAs and time less work: the
