@@ -27,7 +27,9 @@
 //    (busy = 0), run independent v_fma_f32 streams long enough to outlast
 //    them (busy = 1), issue the same MFMA stream (busy = 2), or stream
 //    conflict-free 128-bit LDS reads (busy = 3: 1 KB per instruction, eight
-//    in flight per wave).  Each wave
+//    in flight per wave), or run independent v_exp_f32 (busy = 4) or
+//    v_dot2_f32_bf16 (busy = 5) streams, the attention softmax's
+//    transcendental and row-sum instructions.  Each wave
 //    records its hardware id, so the host can check that waves w and w + 4
 //    share a SIMD.
 //  * mxp_promote_launch: the fp8 GEMM's block promotion.  Every wave keeps
@@ -428,15 +430,24 @@ __global__ __launch_bounds__(512, 1) void contend_kernel(const u32x4* __restrict
       cycles[blockIdx.x * 8 + wave] = t1 - t0;
       rtime[blockIdx.x * 8 + wave] = r1 - r0;
     }
-  } else if constexpr (BUSY == 1) {
+  } else if constexpr (BUSY == 1 || BUSY == 4 || BUSY == 5) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
     float e[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) e[i] = 1e-6f * (threadIdx.x + i);
+    const bf2 p2{(__bf16)1e-6f, (__bf16)2e-6f}, ones{(__bf16)1.0f, (__bf16)1.0f};
     const long long r0 = __builtin_amdgcn_s_memrealtime();
     const long long t0 = __builtin_readcyclecounter();
     for (int it = 0; it < valu_iters; ++it) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) e[i] = __builtin_fmaf(e[i], 0.999f, e[i ^ 2]);
+      for (int i = 0; i < 32; ++i) {
+        if constexpr (BUSY == 1)
+          e[i] = __builtin_fmaf(e[i], 0.999f, e[i ^ 2]);
+        else if constexpr (BUSY == 4)
+          e[i] = __builtin_amdgcn_exp2f(-e[i]);  // stays in (0, 1]
+        else
+          e[i] = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, e[i], false);
+      }
     }
     const long long t1 = __builtin_readcyclecounter();
     const long long r1 = __builtin_amdgcn_s_memrealtime();
@@ -462,8 +473,14 @@ int launch_contend(int busy, int nwg, int iters, int valu_iters, const u32x4* op
   else if (busy == 2)
     hipLaunchKernelGGL((contend_kernel<FORM, 2>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
                        valu_iters);
-  else
+  else if (busy == 3)
     hipLaunchKernelGGL((contend_kernel<FORM, 3>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
+                       valu_iters);
+  else if (busy == 4)
+    hipLaunchKernelGGL((contend_kernel<FORM, 4>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
+                       valu_iters);
+  else
+    hipLaunchKernelGGL((contend_kernel<FORM, 5>), dim3(nwg), dim3(512), 0, s, ops, out, cycles, rtime, hwid, iters,
                        valu_iters);
   return hip_status(hipGetLastError());
 }
@@ -696,12 +713,13 @@ extern "C" int mxp_stream_launch(int mode, int depth, const void* src, long long
 }
 
 // form 0..4 as contend_kernel; busy 0 (waves 4-7 idle), 1 (VALU), 2 (the
-// same MFMAs) or 3 (LDS reads; valu_iters iterations of eight 1 KB reads).  ops: nwg * 512 * 4 16-byte fragments (lane t reads its
+// same MFMAs), 3 (LDS reads; valu_iters iterations of eight 1 KB reads), 4
+// (v_exp_f32) or 5 (v_dot2_f32_bf16; 4 and 5 as 1: 32 chains per lane).  ops: nwg * 512 * 4 16-byte fragments (lane t reads its
 // 4 at 4 t); out: nwg * 512 floats; cycles, rtime and hwid: nwg * 8 each.
 extern "C" int mxp_contend_launch(int form, int busy, int nwg, int iters, int valu_iters, const void* ops, float* out,
                                   long long* cycles, long long* rtime, unsigned* hwid, void* stream) {
   if (nwg <= 0 || iters <= 0 || valu_iters < 0 || !ops || !out || !cycles || !rtime || !hwid || form < 0 ||
-      form > 4 || busy < 0 || busy > 3)
+      form > 4 || busy < 0 || busy > 5)
     return -1;
   const u32x4* o = static_cast<const u32x4*>(ops);
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -18,8 +18,9 @@ second.
 
 --contend: shader-clock cycles per MFMA of a wave issuing independent MFMAs
 (bf16 32x32x16 or fp8 32x32x64, accumulators in VGPRs or AGPRs) while the
-other wave on its SIMD idles, runs independent v_fma_f32 work, or issues the
-same MFMAs, with the clock the chip held meanwhile.
+other wave on its SIMD idles, runs independent v_fma_f32, v_exp_f32 or
+v_dot2_f32_bf16 work, issues the same MFMAs or streams LDS reads, with the
+clock the chip held meanwhile.
 
 --promote: the fp8 GEMM's block promotion (two 32x32x64 fp8 MFMAs into a
 fresh partial, then acc += s * partial) in shader-clock cycles per
@@ -247,7 +248,7 @@ def contend(lib, iters: int = 4000, reps: int = 3) -> list[str]:
         """Median over reps of: cycles per MFMA of waves 0-3, their clock (GHz from the
         100 MHz real-time counter), waves 4-7's cycles, and the share of workgroups whose
         waves w and w + 4 report the same SIMD."""
-        valu_iters = 12 * iters if busy == 1 else (3 * iters if busy == 3 else 0)
+        valu_iters = {1: 12 * iters, 3: 3 * iters, 4: 6 * iters, 5: 12 * iters}.get(busy, 0)
         mf, clk, other, paired = [], [], [], []
         for _ in range(reps):
             ops = bf16 if form in (0, 1, 4) else fp8
@@ -272,9 +273,13 @@ def contend(lib, iters: int = 4000, reps: int = 3) -> list[str]:
     for form, name in CONTEND_FORMS:
         idle = None
         for busy, label in ((0, "idle"), (1, "v_fma_f32 stream"), (2, "the same MFMA stream"),
-                            (3, "128-bit LDS reads (1 KB each, conflict-free)")):
+                            (3, "128-bit LDS reads (1 KB each, conflict-free)"),
+                            (4, "v_exp_f32 stream"), (5, "v_dot2_f32_bf16 stream")):
+            if busy >= 4 and form not in (0, 1, 4):
+                continue  # the softmax instructions sit beside bf16 MFMAs only
             per_wave, ghz, other, paired = run(form, busy)
-            n_other = {1: 12 * iters * 32, 2: iters * 8, 3: 3 * iters * 8}.get(busy, 1)
+            n_other = {1: 12 * iters * 32, 2: iters * 8, 3: 3 * iters * 8, 4: 6 * iters * 32,
+                       5: 12 * iters * 32}.get(busy, 1)
             o_per = f"{other / n_other:.1f}" if busy else ""
             o_tot = f"{other:.0f}" if busy else ""
             if busy == 0:
