@@ -13,7 +13,7 @@ import pytest
 from conftest import REPO_ROOT, announce
 
 RUN_PY = REPO_ROOT / "cuda-oxide-bench_amd" / "microbench" / "run.py"
-ABLATE_PY = REPO_ROOT / "cuda-oxide-bench_amd" / "microbench" / "ablate.py"
+ALT_PY = REPO_ROOT / "cuda-oxide-bench_amd" / "microbench" / "alternatives.py"
 
 
 @pytest.fixture(scope="module")
@@ -42,7 +42,7 @@ def test_probe_library_exports_its_launchers(runner):
     assert lib.mxp_promote_launch(1, 4, 4, 1, 10, p, p, p, None) == -1   # lag 1..3
     assert lib.mxp_promote_launch(0, 1, 6, 1, 10, p, p, p, None) == -1   # 4 or 8 waves
     assert lib.mxp_promote_launch(4, 1, 4, 1, 10, p, p, p, None) == -1
-    assert lib.mxp_contend_launch(0, 4, 1, 10, 0, p, p, p, p, p, None) == -1
+    assert lib.mxp_contend_launch(0, 6, 1, 10, 0, p, p, p, p, p, None) == -1
     assert lib.mxp_contend_launch(0, 1, 1, 10, 10, p, p, p, p, None, None) == -1
     assert lib.mxp_stream_launch(0, 12, p, 0, 64, 1, p, None) == -1   # no such depth
     assert lib.mxp_stream_launch(2, 8, p, 0, 64, 1, p, None) == -1    # no such mode
@@ -50,18 +50,21 @@ def test_probe_library_exports_its_launchers(runner):
     assert lib.mxp_stream_launch(1, 8, p, 0, 64, 0, p, None) == -1
 
 
-def test_ablation_patches_apply():
-    """Every ablation variant's text patches still match the kernel source
-    exactly once (the tool refuses to build otherwise), and each variant
-    changes the source (CPU only; the build and the GPU run are the tool's)."""
-    spec = importlib.util.spec_from_file_location("mx_microbench_ablate", ABLATE_PY)
-    ab = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(ab)
-    for kernel, k in ab.KERNELS.items():
+def test_alternative_patches_apply():
+    """Every alternative's text patches still match the kernel source exactly
+    once (the tool refuses to build otherwise), each alternative changes the
+    source, and every variant but the kernel as built is marked exact, so its
+    output is compared bit for bit with the kernel as built's (CPU only; the
+    build and the GPU run are the tool's)."""
+    spec = importlib.util.spec_from_file_location("mx_microbench_alternatives", ALT_PY)
+    alt = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(alt)
+    for kernel, k in alt.KERNELS.items():
         base = (REPO_ROOT / "cuda-oxide-bench_amd" / "csrc" / k["source"]).read_text()
         for v, spec_v in k["variants"].items():
-            text = ab.patched_source(kernel, v)
+            text = alt.patched_source(kernel, v)
             assert (text == base) == (not spec_v[1]), f"{kernel}/{v}"
+            assert (v == "as_built") != alt.variant_exact(kernel, v), f"{kernel}/{v}"
 
 
 @pytest.mark.gpu
