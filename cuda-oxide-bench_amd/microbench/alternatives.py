@@ -204,6 +204,9 @@ KERNELS = {
     "bf16_8192": {"source": "gemm_bf16.hip", "parts": {}, "variants": {"as_built": ("the kernel as built", [])},
                   "workload": "gemm_bf16 M8192 N8192 K8192 U[-1,1] (gemm_bf16_dma16s_kernel)",
                   "kernel_prefix": "_ZN2mx4gemm23gemm_bf16_dma16s_kernel"},
+    "mla": {"source": "mla_decode.hip", "parts": {}, "variants": {"as_built": ("the decode and merge as built", [])},
+            "workload": "mla_decode absorbed B32 H128 T4096 576/512 bf16, decode + merge, same buffers",
+            "kernel_prefix": "_ZN2mx3mla17mla_decode_kernel"},
 }
 
 
@@ -314,6 +317,13 @@ def time_one(kernel: str, inputs: str = "random", steps: int = 20, warmup: int =
         v = torch.randn((1, 8, 4096, 128), device="cuda", generator=gen).to(torch.bfloat16)
         out = torch.empty_like(q)
         fn = lambda: ops.gqa_fwd(q, k, v, causal=True, out=out)  # noqa: E731
+    elif kernel == "mla":
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        q = torch.randn((32, 128, 576), device="cuda", generator=gen).to(torch.bfloat16)
+        kv = torch.randn((32, 4096, 576), device="cuda", generator=gen).to(torch.bfloat16)
+        out = torch.empty((32, 128, 512), dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(max(1, ops.mla_decode_workspace_bytes(32, 128, 4096)), dtype=torch.uint8, device="cuda")
+        fn = lambda: ops.mla_decode(q, kv, 192 ** -0.5, out=out, workspace=ws)  # noqa: E731
     elif kernel == "bf16_8192":
         gen = torch.Generator(device="cuda").manual_seed(0)
         a = (torch.rand((8192, 8192), device="cuda", generator=gen) * 2 - 1).to(torch.bfloat16)

@@ -81,7 +81,8 @@ def test_probes_run(runner):
     assert len(lines) == 2 + 16
     announce("microbench MFMA beside VALU")
     lines = runner.contend(lib, iters=200, reps=1)
-    assert len(lines) == 2 + 4 * len(runner.CONTEND_FORMS)
+    # four partner modes per form, and the v_exp_f32 and v_dot2 streams beside the three bf16 forms
+    assert len(lines) == 2 + sum(4 + (2 if form in (0, 1, 4) else 0) for form, _ in runner.CONTEND_FORMS)
     announce("microbench fp8 promotion")
     lines = runner.promote(lib, iters=100, reps=1)
     assert len(lines) == 2 + len(runner.PROMOTE_CASES)
